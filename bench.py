@@ -1,0 +1,262 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized GGML GEMM path (one JSON line on stdout).
+
+Metric: "q4_0×q8_0 GEMM TOPS @480×1536×1536; M=1 GEMV GB/s @4096×4096".
+One step = one pass of the hot path over one batch of synthetic input:
+  * value  : config 1 — q4_0 x q8_0 GEMV, M=1 N=4096 K=4096, GB/s of algorithmic
+             bytes (weights + q8_0 activation + fp32 output) per second. The step
+             rotates over 32 weight copies (302 MB > the 256 MB Infinity Cache), so
+             the weights stream from HBM as in decode.
+  * gemm   : config 0 — q4_0 x q8_0 GEMM, M=480 N=1536 K=1536, TOPS = 2*M*N*K/s,
+             the other half of the compound metric.
+Activations are quantized once before the timed region (the reference quantizes
+in prepare(), kernels/*/adapter.cpp); an end-to-end figure that includes the GPU
+quantizer is reported beside it. Inputs are resident in HBM when timing starts.
+
+Timed region: W warm-up steps, then K steps bracketed by torch.cuda.synchronize().
+Launches are replayed from a captured graph (32 launches per replay) so that
+host launch overhead does not pace the GPU. Kernel time is measured with HIP
+events on the launch stream over the same region.
+
+cpu_baseline: the reference's own llama_reference::compute (oracle/_ref, built
+from /root/reference sources) timed on this host, one thread, on a bounded
+sample; if oracle/_ref is absent the C restatement (oracle/) is timed instead.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+METRIC = "q4_0×q8_0 GEMM TOPS @480×1536×1536; M=1 GEMV GB/s @4096×4096"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA (5.0 POPS)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def load_package():
+    import importlib.util
+    name = "qgemm_perf_framework_ng_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    d = os.path.join(REPO, "qgemm-perf-framework-ng_amd")
+    spec = importlib.util.spec_from_file_location(name, os.path.join(d, "__init__.py"), submodule_search_locations=[d])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def gemv_bytes(m, n, k):
+    return n * (k // 32) * 18 + m * (k // 32) * 34 + m * n * 4
+
+
+def time_graph(torch, graph, launches_per_replay, steps, warmup):
+    """Replays `graph` until `steps` launches ran; returns (wall_s, event_ms, steps_run)."""
+    reps = max(1, -(-steps // launches_per_replay))
+    wreps = max(1, -(-warmup // launches_per_replay))
+    for _ in range(wreps):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return t1 - t0, e0.elapsed_time(e1), reps * launches_per_replay
+
+
+def capture(torch, fn, count):
+    """Capture `count` calls fn(i) into one graph on a side stream."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(min(count, 3)):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(count):
+            fn(i)
+    torch.cuda.synchronize()
+    return g
+
+
+def cpu_baseline(budget_s):
+    """Time the reference's compute() on the host: c1 (GEMV) in GB/s, c0 (GEMM) in TOPS."""
+    import numpy as np
+    import oracle as O
+    O.lib()
+    use_ref = O.ref_available()
+    m, n, k = 1, 4096, 4096
+    act, w = O.create_input(0, m, n, k, seed=1, variant=0)
+    out = np.zeros((m, n), np.float32)
+    if use_ref:
+        R = O.ref()
+        run = lambda a, ww, o, mm, nn, kk: R.ref_compute(0, O._ptr(a), O._ptr(ww), O._ptr(o), mm, nn, kk)  # noqa: E731
+    else:
+        run = lambda a, ww, o, mm, nn, kk: O.lib().pfo_compute(0, O._ptr(a), O._ptr(ww), O._ptr(o), mm, nn, kk, 1)  # noqa: E731
+    iters = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s * 0.5:
+        run(act, w, out, m, n, k)
+        iters += 1
+    t_gemv = time.perf_counter() - t0
+    gbs = gemv_bytes(m, n, k) * iters / t_gemv / 1e9
+    m2, n2, k2 = 480, 1536, 1536
+    act2, w2 = O.create_input(0, m2, n2, k2, seed=1, variant=0)
+    out2 = np.zeros((m2, n2), np.float32)
+    reps = 0
+    t0 = time.perf_counter()
+    while reps == 0 or time.perf_counter() - t0 < budget_s * 0.5:
+        run(act2, w2, out2, m2, n2, k2)
+        reps += 1
+    t_gemm = time.perf_counter() - t0
+    tops = 2.0 * m2 * n2 * k2 * reps / t_gemm / 1e12
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "reference" if use_ref else "port",
+        "sample": (f"{'llama_reference::compute (oracle/_ref)' if use_ref else 'oracle/pfng_oracle.c compute'}, "
+                   f"1 thread on {cpu}: c1 1x4096x4096 x{iters} calls in {t_gemv:.1f}s (incl. activation quantize); "
+                   f"c0 480x1536x1536 x{reps} in {t_gemm:.1f}s"),
+        "gemm_tops": round(tops, 5),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=6400, help="timed GEMV steps (rounded up to a multiple of 32)")
+    ap.add_argument("--warmup", type=int, default=640)
+    ap.add_argument("--gemm-steps", type=int, default=2048)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline budget (0 = skip)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        log(f"bench.py: --gpus {args.gpus} is not supported; this build runs the hot path on one MI355X "
+            "(N-sharded multi-GPU operation is a design note only).")
+        sys.exit(2)
+    if int(os.environ.get("RANK", "0")) != 0:
+        return
+
+    import numpy as np
+    import torch
+    import oracle as O
+
+    pkg = load_package()
+    arch, cus = pkg.device_check()
+    log(f"[bench] device {arch}, {cus} CUs; {pkg.version()}")
+
+    # ---------------- config 1: GEMV M=1 N=4096 K=4096, rotating weights ----------------
+    m, n, k = 1, 4096, 4096
+    copies = 32
+    act, w = O.create_input(0, m, n, k, seed=1, variant=1)
+    wbytes = np.ascontiguousarray(w).view(np.uint8).reshape(n, -1)
+    base = torch.from_numpy(wbytes).cuda()
+    weights = [base] + [base.clone() for _ in range(copies - 1)]
+    act_t = torch.from_numpy(act).cuda()
+    aq = pkg.quantize_q8_0(act_t)
+    outs = [torch.empty((m, n), dtype=torch.float32, device="cuda") for _ in range(copies)]
+    ws = torch.empty(pkg.lib().pfng_hip_compute_workspace_size(0, m, k), dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    log(f"[bench] c1 gemv {m}x{n}x{k}: {copies} weight copies, {copies * wbytes.nbytes / 1e6:.0f} MB resident")
+
+    g = capture(torch, lambda i: pkg.mul_mat(0, weights[i % copies], aq, m, n, k, out=outs[i % copies]), copies)
+    wall, ev_ms, steps = time_graph(torch, g, copies, args.steps, args.warmup)
+    per_call = gemv_bytes(m, n, k)
+    value = per_call * steps / wall / 1e9
+    kernel_us = ev_ms * 1e3 / steps
+    achieved = per_call / (kernel_us * 1e-6) / 1e9
+    log(f"[bench] c1 gemv: {steps} steps, wall {wall * 1e3:.2f} ms, {value:.1f} GB/s; kernel {kernel_us:.3f} us "
+        f"-> {achieved:.1f} GB/s")
+
+    g2 = capture(torch, lambda i: pkg.compute(0, act_t, weights[i % copies], n, out=outs[i % copies], workspace=ws),
+                 copies)
+    wall2, ev2, steps2 = time_graph(torch, g2, copies, args.steps, args.warmup)
+    e2e_gbs = (per_call + m * k * 4) * steps2 / wall2 / 1e9
+
+    # correctness of the measured configuration against the oracle
+    ref = O.matmul(0, w, O.quantize_q8_0(act), m, n, k)
+    terms = O.abs_terms(0, w, O.quantize_q8_0(act), m, n, k)
+    got = pkg.mul_mat(0, weights[0], aq, m, n, k).cpu().numpy()
+    ok1 = O.within_tolerance(got, ref, terms)[0]
+
+    # ---------------- config 0: GEMM M=480 N=1536 K=1536 ----------------
+    m0, n0, k0 = 480, 1536, 1536
+    act0, w0 = O.create_input(0, m0, n0, k0, seed=1, variant=1)
+    w0_t = torch.from_numpy(np.ascontiguousarray(w0).view(np.uint8).reshape(n0, -1)).cuda()
+    act0_t = torch.from_numpy(act0).cuda()
+    aq0 = pkg.quantize_q8_0(act0_t)
+    out0 = torch.empty((m0, n0), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    gg = capture(torch, lambda i: pkg.mul_mat(0, w0_t, aq0, m0, n0, k0, out=out0), 32)
+    wall0, ev0, steps0 = time_graph(torch, gg, 32, args.gemm_steps, 256)
+    ops = 2.0 * m0 * n0 * k0
+    tops = ops * steps0 / wall0 / 1e12
+    gemm_kernel_us = ev0 * 1e3 / steps0
+    gemm_achieved = ops / (gemm_kernel_us * 1e-6) / 1e12
+    ref0 = O.matmul(0, w0, O.quantize_q8_0(act0), m0, n0, k0)
+    terms0 = O.abs_terms(0, w0, O.quantize_q8_0(act0), m0, n0, k0)
+    ok0 = O.within_tolerance(out0.cpu().numpy(), ref0, terms0)[0]
+    log(f"[bench] c0 gemm: {steps0} steps, {tops:.2f} TOPS wall; kernel {gemm_kernel_us:.3f} us -> "
+        f"{gemm_achieved:.2f} TOPS; verify c1={ok1} c0={ok0}")
+
+    cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
+    if cpu:
+        log(f"[bench] cpu baseline: {cpu}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / steps, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded mt19937 U[-1,1) weights quantized to q4_0, activations to q8_0)",
+        "config": {"workload": "c1: q4_0 x q8_0 GEMV M=1 N=4096 K=4096, 32 rotating weight copies (302 MB)",
+                   "m": m, "n": n, "k": k, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_q4_0_kernel<1>", "kernel_us": round(kernel_us, 4),
+                     "bytes_per_launch": per_call},
+        "e2e_with_quantize_gbs": round(e2e_gbs, 2),
+        "gemm": {"workload": "c0: q4_0 x q8_0 GEMM M=480 N=1536 K=1536", "value": round(tops, 3), "unit": "TOPS",
+                 "steps": steps0, "ms_per_step": round(wall0 * 1e3 / steps0, 6),
+                 "roofline": {"bound": "mfma", "achieved": round(gemm_achieved, 3), "peak": INT8_PEAK_TOPS,
+                              "unit": "TFLOP/s", "frac": round(gemm_achieved / INT8_PEAK_TOPS, 4), "traffic": None,
+                              "kernel": "gemm_q4_0_kernel", "kernel_us": round(gemm_kernel_us, 4)}},
+        "verified": bool(ok1 and ok0),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,175 @@
+// C-ABI entry points of libpfng_hip (declared in include/pfng_hip.h).
+// Validates arguments on the host, picks a kernel path and launches it
+// asynchronously on the caller's stream. Errors are returned as pfng_status
+// codes with a thread-local message; nothing throws across the boundary.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "kernels.h"
+#include "pfng_hip.h"
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int status, const char *fmt, ...) {
+    va_list args;
+    va_start(args, fmt);
+    std::vsnprintf(g_error, sizeof g_error, fmt, args);
+    va_end(args);
+    return status;
+}
+
+int hip_status(hipError_t e, const char *what) {
+    if (e == hipSuccess) return PFNG_OK;
+    return fail(PFNG_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int64_t block_elems(int type) { return type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0 ? 32 : 256; }
+
+const char *type_name(int type) {
+    switch (type) {
+    case PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0: return "q4_0 x q8_0";
+    case PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K: return "q4_K x q8_K";
+    case PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K: return "iq2_xxs x q8_K";
+    default: return "unknown";
+    }
+}
+
+// Shape checks shared by every product entry point (validate_shape,
+// kernels/common/adapter_common.h:28-43: K must be a multiple of the block).
+int check_shape(int type, int64_t m, int64_t n, int64_t k) {
+    if (type < 0 || type >= PFNG_QUANTIZATION_TYPE_COUNT) return fail(PFNG_ERR_INVALID_ARGUMENT, "unknown type %d", type);
+    if (m < 0 || n < 0) return fail(PFNG_ERR_INVALID_ARGUMENT, "m and n must be non-negative (m=%lld n=%lld)",
+                                    (long long)m, (long long)n);
+    const int64_t qk = block_elems(type);
+    if (k <= 0 || k % qk) return fail(PFNG_ERR_INVALID_ARGUMENT, "%s: k=%lld must be a positive multiple of %lld",
+                                      type_name(type), (long long)k, (long long)qk);
+    if (m > INT32_MAX || n > INT32_MAX || k / qk > INT32_MAX / 2)
+        return fail(PFNG_ERR_INVALID_ARGUMENT, "shape too large (m=%lld n=%lld k=%lld)", (long long)m, (long long)n,
+                    (long long)k);
+    return PFNG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *pfng_hip_last_error(void) { return g_error; }
+
+const char *pfng_hip_version(void) { return "pfng_hip 0.1.0 (gfx950)"; }
+
+int pfng_hip_device_check(char *arch, size_t arch_len, int *cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(PFNG_ERR_HIP, "hipGetDevice failed");
+    hipDeviceProp_t prop;
+    const hipError_t e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) return hip_status(e, "hipGetDeviceProperties");
+    if (arch && arch_len) {
+        std::strncpy(arch, prop.gcnArchName, arch_len - 1);
+        arch[arch_len - 1] = '\0';
+    }
+    if (cus) *cus = prop.multiProcessorCount;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(PFNG_ERR_DEVICE, "device %d is %s, this library is built for gfx950", dev, prop.gcnArchName);
+    return PFNG_OK;
+}
+
+int pfng_hip_quantize_q8_0(const float *x, void *y, int64_t rows, int64_t k, void *stream) {
+    if (rows < 0 || k <= 0 || k % 32) return fail(PFNG_ERR_INVALID_ARGUMENT, "quantize_q8_0: rows=%lld k=%lld (k must be a positive multiple of 32)", (long long)rows, (long long)k);
+    if (rows == 0) return PFNG_OK;
+    if (!x || !y) return fail(PFNG_ERR_INVALID_ARGUMENT, "quantize_q8_0: null pointer");
+    if (!aligned(x, 16) || !aligned(y, 2)) return fail(PFNG_ERR_INVALID_ARGUMENT, "quantize_q8_0: x must be 16-byte and y 2-byte aligned");
+    return hip_status(pfng::launch_quantize_q8_0(x, y, rows, k, static_cast<hipStream_t>(stream)), "quantize_q8_0 launch");
+}
+
+int pfng_hip_quantize_q8_K(const float *x, void *y, int64_t rows, int64_t k, void *stream) {
+    if (rows < 0 || k <= 0 || k % 256) return fail(PFNG_ERR_INVALID_ARGUMENT, "quantize_q8_K: rows=%lld k=%lld (k must be a positive multiple of 256)", (long long)rows, (long long)k);
+    if (rows == 0) return PFNG_OK;
+    if (!x || !y) return fail(PFNG_ERR_INVALID_ARGUMENT, "quantize_q8_K: null pointer");
+    if (!aligned(x, 16) || !aligned(y, 4)) return fail(PFNG_ERR_INVALID_ARGUMENT, "quantize_q8_K: x must be 16-byte and y 4-byte aligned");
+    return hip_status(pfng::launch_quantize_q8_K(x, y, rows, k, static_cast<hipStream_t>(stream)), "quantize_q8_K launch");
+}
+
+int pfng_hip_mul_mat(int type, const void *weight, const void *act_q, float *out, int64_t m, int64_t n, int64_t k,
+                     int path, void *stream) {
+    int rc = check_shape(type, m, n, k);
+    if (rc) return rc;
+    if (m == 0 || n == 0) return PFNG_OK;
+    if (!weight || !act_q || !out) return fail(PFNG_ERR_INVALID_ARGUMENT, "%s: null pointer", type_name(type));
+    // Tiled paths read blocks with dword (and 16-byte) loads.
+    const bool base_aligned = aligned(weight, 16) && aligned(act_q, 16) && aligned(out, 4);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool gemv_ok = base_aligned && pfng::gemv_supported(type, m, k);
+    const bool mfma_ok = base_aligned && pfng::mfma_supported(type, m, k);
+    switch (path) {
+    case PFNG_PATH_AUTO:
+        if (gemv_ok) return hip_status(pfng::launch_gemv(type, weight, act_q, out, m, n, k, s), "gemv launch");
+        if (mfma_ok) return hip_status(pfng::launch_mfma_mul_mat(type, weight, act_q, out, m, n, k, s), "mfma launch");
+        return hip_status(pfng::launch_naive_mul_mat(type, weight, act_q, out, m, n, k, s), "naive launch");
+    case PFNG_PATH_GEMV:
+        if (!gemv_ok) return fail(PFNG_ERR_UNSUPPORTED, "%s GEMV path needs m<=8, k%%256==0 and 16-byte aligned operands (m=%lld k=%lld)", type_name(type), (long long)m, (long long)k);
+        return hip_status(pfng::launch_gemv(type, weight, act_q, out, m, n, k, s), "gemv launch");
+    case PFNG_PATH_MFMA:
+        if (!mfma_ok) return fail(PFNG_ERR_UNSUPPORTED, "%s MFMA path not available for m=%lld k=%lld", type_name(type), (long long)m, (long long)k);
+        return hip_status(pfng::launch_mfma_mul_mat(type, weight, act_q, out, m, n, k, s), "mfma launch");
+    case PFNG_PATH_NAIVE:
+        return hip_status(pfng::launch_naive_mul_mat(type, weight, act_q, out, m, n, k, s), "naive launch");
+    default: return fail(PFNG_ERR_INVALID_ARGUMENT, "unknown path %d", path);
+    }
+}
+
+int pfng_hip_mul_mat_q4_0_q8_0(const void *weight, const void *act_q8_0, float *out, int64_t m, int64_t n, int64_t k,
+                               int path, void *stream) {
+    return pfng_hip_mul_mat(PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0, weight, act_q8_0, out, m, n, k, path, stream);
+}
+
+int pfng_hip_mul_mat_q4_K_q8_K(const void *weight, const void *act_q8_K, float *out, int64_t m, int64_t n, int64_t k,
+                               int path, void *stream) {
+    return pfng_hip_mul_mat(PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K, weight, act_q8_K, out, m, n, k, path, stream);
+}
+
+int pfng_hip_mul_mat_iq2_xxs_q8_K(const void *weight, const void *act_q8_K, float *out, int64_t m, int64_t n,
+                                  int64_t k, int path, void *stream) {
+    return pfng_hip_mul_mat(PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K, weight, act_q8_K, out, m, n, k, path, stream);
+}
+
+size_t pfng_hip_compute_workspace_size(int type, int64_t m, int64_t k) {
+    if (m <= 0 || k <= 0) return 0;
+    if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return (size_t)m * (size_t)(k / 32) * sizeof(pfng_block_q8_0);
+    return (size_t)m * (size_t)(k / 256) * sizeof(pfng_block_q8_K);
+}
+
+int pfng_hip_compute(int type, const float *activation, const void *weight, float *out, int64_t m, int64_t n,
+                     int64_t k, void *workspace, size_t workspace_bytes, int path, void *stream) {
+    int rc = check_shape(type, m, n, k);
+    if (rc) return rc;
+    if (m == 0 || n == 0) return PFNG_OK;
+    if (workspace_bytes < pfng_hip_compute_workspace_size(type, m, k))
+        return fail(PFNG_ERR_INVALID_ARGUMENT, "compute: workspace of %zu bytes is smaller than the %zu needed",
+                    workspace_bytes, pfng_hip_compute_workspace_size(type, m, k));
+    rc = type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0 ? pfng_hip_quantize_q8_0(activation, workspace, m, k, stream)
+                                                  : pfng_hip_quantize_q8_K(activation, workspace, m, k, stream);
+    if (rc) return rc;
+    return pfng_hip_mul_mat(type, weight, workspace, out, m, n, k, path, stream);
+}
+
+int pfng_hip_block_isums(int type, const void *weight, const void *act_q, int32_t *out, int64_t m, int64_t n,
+                         int64_t k, void *stream) {
+    int rc = check_shape(type, m, n, k);
+    if (rc) return rc;
+    if (m == 0 || n == 0) return PFNG_OK;
+    if (!weight || !act_q || !out) return fail(PFNG_ERR_INVALID_ARGUMENT, "block_isums: null pointer");
+    if (!aligned(weight, 16) || !aligned(act_q, 16) || !aligned(out, 4) || !pfng::mfma_supported(type, m, k))
+        return fail(PFNG_ERR_UNSUPPORTED, "block_isums: %s MFMA tile path not available for k=%lld", type_name(type),
+                    (long long)k);
+    return hip_status(pfng::launch_mfma_block_isums(type, weight, act_q, out, m, n, k, static_cast<hipStream_t>(stream)),
+                      "block_isums launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,214 @@
+// GEMV path (m <= 8) for gfx950: no MFMA, the weight stream is the roofline.
+//
+// Work decomposition. The weight matrix is a stream of 18-byte q4_0 blocks.
+// Eight consecutive blocks (a "group", 144 B) start on a 16-byte boundary
+// whenever k % 256 == 0, so every lane loads its group with nine 16-byte loads
+// and decodes the blocks from registers (bytes sit at fixed offsets 18*j).
+// A wavefront is split into 64/L row slots of L lanes; the L lanes of a slot
+// walk the groups of one weight row and are reduced with cross-lane shuffles.
+// All loads of a lane are issued before any arithmetic, so the whole weight
+// stream of the grid is in flight at once.
+//
+// Activations (m <= 8 rows of q8_0) are staged once per workgroup into LDS in
+// a layout that makes the per-lane reads bank-conflict free: for every group,
+// 8 x 32 bytes of int8 followed by the 8 fp16 scales (272 B per group).
+//
+// Arithmetic per block (exact integer part, then fp32):
+//   w16 = 16 * (nibble - 8) packed as int8 (q4_0_unpack16), isum16 = sum w16 * a
+//   (v_dot4_i32_i8), acc += float(isum16) * (dw * da); the output is acc / 16.
+// |isum16| <= 16 * 32512 < 2^24, so float(isum16) is exact and the result equals
+// the reference's dot (llama_reference.cpp:134-146) up to fp32 reassociation.
+#include "device_common.h"
+#include "kernels.h"
+
+namespace pfng {
+
+namespace {
+
+constexpr int kGroupBlocks = 8;
+constexpr int kGroupBytesLds = kGroupBlocks * 32 + 16;  // 272
+constexpr int kChunkGroups = 16;                        // K chunk of 4096 elements per LDS fill
+constexpr int kThreads = 256;
+
+// Stage activation groups [g0, g0 + ng) of all m rows into LDS.
+template <int M>
+__device__ __forceinline__ void stage_q8_0_groups(const uint8_t *__restrict__ a, uint8_t *lds, int nb, int g0, int ng) {
+    // one task per (row, block pair): 68 bytes, 4-byte aligned since nb is even
+    const int pairs = ng * (kGroupBlocks / 2);
+    for (int task = threadIdx.x; task < M * pairs; task += kThreads) {
+        const int row = task / pairs;
+        const int pr = task % pairs;
+        const int blk = g0 * kGroupBlocks + pr * 2;
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(a + ((size_t)row * nb + blk) * 34);
+        uint32_t v[17];
+#pragma unroll
+        for (int i = 0; i < 17; ++i) v[i] = src[i];
+        uint32_t q0[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q0[i] = shift2(v[i], v[i + 1]);
+        const int lg = pr / 4, lb = (pr % 4) * 2;  // group within chunk, first block within group
+        uint8_t *gbase = lds + (row * kChunkGroups + lg) * kGroupBytesLds;
+        uint4 *dq = reinterpret_cast<uint4 *>(gbase + lb * 32);
+        dq[0] = make_uint4(q0[0], q0[1], q0[2], q0[3]);
+        dq[1] = make_uint4(q0[4], q0[5], q0[6], q0[7]);
+        dq[2] = make_uint4(v[9], v[10], v[11], v[12]);
+        dq[3] = make_uint4(v[13], v[14], v[15], v[16]);
+        *reinterpret_cast<uint32_t *>(gbase + 256 + lb * 2) = (v[0] & 0xffffu) | (v[8] & 0xffff0000u);
+    }
+}
+
+// Nine 16-byte loads of eight consecutive q4_0 blocks (144 B, 16-byte aligned).
+__device__ __forceinline__ void load_q4_0_group(const uint8_t *__restrict__ w, bool ok, size_t first_block,
+                                                uint32_t (&wv)[36]) {
+    if (ok) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(w + first_block * 18);
+#pragma unroll
+        for (int i = 0; i < 9; ++i) {
+            const uint4 t = src[i];
+            wv[4 * i] = t.x;
+            wv[4 * i + 1] = t.y;
+            wv[4 * i + 2] = t.z;
+            wv[4 * i + 3] = t.w;
+        }
+    } else {
+        // decodes to zero weights
+#pragma unroll
+        for (int i = 0; i < 36; ++i) wv[i] = 0x88888888u;
+    }
+}
+
+// Block j of a group sits at byte 18*j: fp16 d, then 16 bytes of nibbles.
+template <int M>
+__device__ __forceinline__ void gemv_q4_0_group(const uint32_t (&wv)[36], const uint8_t *gbase, float (&acc)[M]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        uint32_t q[4], dw16;
+        if (j % 2 == 0) {
+            const int b = 9 * j / 2;
+            dw16 = wv[b] & 0xffffu;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = shift2(wv[b + i], wv[b + i + 1]);
+        } else {
+            const int b = 9 * (j - 1) / 2;
+            dw16 = wv[b + 4] >> 16;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = wv[b + 5 + i];
+        }
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q4_0_unpack16(q[i], lo[i], hi[i]);
+        const float dw = fp16_to_f32(dw16);
+#pragma unroll
+        for (int mi = 0; mi < M; ++mi) {
+            const uint8_t *ab = gbase + mi * kChunkGroups * kGroupBytesLds;
+            const uint4 a0 = *reinterpret_cast<const uint4 *>(ab + j * 32);
+            const uint4 a1 = *reinterpret_cast<const uint4 *>(ab + j * 32 + 16);
+            const float da = fp16_to_f32(*reinterpret_cast<const uint16_t *>(ab + 256 + 2 * j));
+            int s = __builtin_amdgcn_sdot4((int)lo[0], (int)a0.x, 0, false);
+            s = __builtin_amdgcn_sdot4((int)lo[1], (int)a0.y, s, false);
+            s = __builtin_amdgcn_sdot4((int)lo[2], (int)a0.z, s, false);
+            s = __builtin_amdgcn_sdot4((int)lo[3], (int)a0.w, s, false);
+            s = __builtin_amdgcn_sdot4((int)hi[0], (int)a1.x, s, false);
+            s = __builtin_amdgcn_sdot4((int)hi[1], (int)a1.y, s, false);
+            s = __builtin_amdgcn_sdot4((int)hi[2], (int)a1.z, s, false);
+            s = __builtin_amdgcn_sdot4((int)hi[3], (int)a1.w, s, false);
+            acc[mi] = fmaf((float)s, dw * da, acc[mi]);
+        }
+    }
+}
+
+template <int M>
+__global__ __launch_bounds__(kThreads) void gemv_q4_0_kernel(const uint8_t *__restrict__ w,
+                                                            const uint8_t *__restrict__ a, float *__restrict__ c,
+                                                            int n, int nb, int lanes_per_row) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int L = lanes_per_row;
+    const int rows_per_wave = 64 / L;
+    const int slot = lane / L;
+    const int sl = lane % L;
+    const int row = (blockIdx.x * (kThreads / 64) + wave) * rows_per_wave + slot;
+    const bool row_ok = row < n;
+    const int groups = nb / kGroupBlocks;
+
+    float acc[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) acc[i] = 0.0f;
+
+    for (int g0 = 0; g0 < groups; g0 += kChunkGroups) {
+        const int ng = groups - g0 < kChunkGroups ? groups - g0 : kChunkGroups;
+        // issue this lane's first weight group before staging, so that the HBM
+        // latency overlaps the activation staging and the barrier
+        int lg = sl;
+        uint32_t wv[36];
+        load_q4_0_group(w, row_ok && lg < ng, (size_t)row * nb + (size_t)(g0 + lg) * kGroupBlocks, wv);
+        if (g0) __syncthreads();
+        stage_q8_0_groups<M>(a, lds, nb, g0, ng);
+        __syncthreads();
+        while (lg < ng) {
+            uint32_t cur[36];
+#pragma unroll
+            for (int i = 0; i < 36; ++i) cur[i] = wv[i];
+            const int next = lg + L;
+            if (next < ng) load_q4_0_group(w, row_ok, (size_t)row * nb + (size_t)(g0 + next) * kGroupBlocks, wv);
+            gemv_q4_0_group<M>(cur, lds + lg * kGroupBytesLds, acc);
+            lg = next;
+        }
+    }
+    // reduce the L lanes of each row slot
+#pragma unroll
+    for (int mi = 0; mi < M; ++mi) {
+        float v = acc[mi];
+        for (int o = L / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        acc[mi] = v;
+    }
+    // after the butterfly every lane of the slot holds all M sums; lane sl
+    // stores activation rows sl, sl + L, ... (L may be smaller than M)
+    if (row_ok) {
+#pragma unroll
+        for (int mi = 0; mi < M; ++mi)
+            if (mi % L == sl) c[(size_t)mi * n + row] = acc[mi] * 0.0625f;
+    }
+}
+
+template <int M>
+hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n, int64_t k, hipStream_t stream) {
+    const int nb = (int)(k / 32);
+    const int groups = nb / kGroupBlocks;
+    const int gcap = groups < kChunkGroups ? groups : kChunkGroups;
+    int L = 1;
+    while (L * 2 <= gcap) L *= 2;
+    const int rows_per_block = (kThreads / 64) * (64 / L);
+    const int grid = (int)((n + rows_per_block - 1) / rows_per_block);
+    const size_t lds = (size_t)M * kChunkGroups * kGroupBytesLds;
+    hipLaunchKernelGGL(gemv_q4_0_kernel<M>, dim3(grid), dim3(kThreads), lds, stream,
+                       static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(a), c, (int)n, nb, L);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemv_supported(int type, int64_t m, int64_t k) {
+    if (m < 1 || m > 8) return false;
+    if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return k % 256 == 0;
+    return false;
+}
+
+hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
+                       hipStream_t stream) {
+    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return hipErrorInvalidValue;
+    switch (m) {
+    case 1: return launch_gemv_q4_0_m<1>(w, a, c, n, k, stream);
+    case 2: return launch_gemv_q4_0_m<2>(w, a, c, n, k, stream);
+    case 3: return launch_gemv_q4_0_m<3>(w, a, c, n, k, stream);
+    case 4: return launch_gemv_q4_0_m<4>(w, a, c, n, k, stream);
+    case 5: return launch_gemv_q4_0_m<5>(w, a, c, n, k, stream);
+    case 6: return launch_gemv_q4_0_m<6>(w, a, c, n, k, stream);
+    case 7: return launch_gemv_q4_0_m<7>(w, a, c, n, k, stream);
+    case 8: return launch_gemv_q4_0_m<8>(w, a, c, n, k, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace pfng

@@ -1,0 +1,30 @@
+// Launchers of the gfx950 kernels. Host code (api.cpp) validates arguments and
+// then calls these; each returns the launch status.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pfng {
+
+// quantize.hip
+hipError_t launch_quantize_q8_0(const float *x, void *y, int64_t rows, int64_t k, hipStream_t stream);
+hipError_t launch_quantize_q8_K(const float *x, void *y, int64_t rows, int64_t k, hipStream_t stream);
+
+// naive.hip — one thread per output in the reference's exact fp32 order
+hipError_t launch_naive_mul_mat(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
+                                hipStream_t stream);
+
+// gemv.hip — m <= 8
+bool gemv_supported(int type, int64_t m, int64_t k);
+hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
+                       hipStream_t stream);
+
+// gemm_mfma.hip
+bool mfma_supported(int type, int64_t m, int64_t k);
+hipError_t launch_mfma_mul_mat(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
+                               hipStream_t stream);
+hipError_t launch_mfma_block_isums(int type, const void *w, const void *a, int32_t *out, int64_t m, int64_t n,
+                                   int64_t k, hipStream_t stream);
+
+}  // namespace pfng

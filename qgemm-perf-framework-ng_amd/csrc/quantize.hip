@@ -1,0 +1,121 @@
+// Activation quantizers for gfx950: q8_0 and q8_K, byte-identical to the
+// reference's llama_reference::quantize_row_q8_0 / quantize_row_q8_K
+// (bench/llama_reference/llama_reference.cpp:38-52, 54-70).
+//
+// Both kernels are HBM-bound streaming passes (4 B read per element, 1.06 /
+// 1.14 B written). Loads are 16 B per lane and consecutive lanes read
+// consecutive addresses; the q8_0 output is assembled in LDS so the 34-byte
+// blocks leave the workgroup as contiguous dword stores.
+//
+// Bit-exactness relies on: fmaxf for the running |x| maximum (NaNs are ignored,
+// as std::max(amax, NaN) keeps amax); a correctly rounded fp32 division for
+// amax / 127 and 1 / d (hipcc's default); no contraction of x * id; roundf
+// (half away from zero, std::round); the ggml fp32 -> fp16 routine for d.
+#include "device_common.h"
+#include "kernels.h"
+
+namespace pfng {
+
+namespace {
+
+constexpr int kQ8_0BlocksPerGroup = 32;  // 256 threads, 8 lanes per block
+constexpr int kQ8_0GroupBytes = kQ8_0BlocksPerGroup * 34;
+
+__device__ __forceinline__ uint32_t quantize4(float4 v, float id) {
+    const int q0 = (int)roundf(mul_rn(v.x, id));
+    const int q1 = (int)roundf(mul_rn(v.y, id));
+    const int q2 = (int)roundf(mul_rn(v.z, id));
+    const int q3 = (int)roundf(mul_rn(v.w, id));
+    return (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+           ((uint32_t)(q3 & 0xff) << 24);
+}
+
+template <bool kAligned4>
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x, uint8_t *__restrict__ y,
+                                                           int64_t nblocks) {
+    __shared__ uint16_t stage[kQ8_0GroupBytes / 2];
+    const int tid = threadIdx.x;
+    const int local_block = tid >> 3;
+    const int sub = tid & 7;
+    const int64_t block = (int64_t)blockIdx.x * kQ8_0BlocksPerGroup + local_block;
+    const bool valid = block < nblocks;
+
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (valid) v = *reinterpret_cast<const float4 *>(x + block * 32 + sub * 4);
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = group_max<8>(amax);
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint32_t q = quantize4(v, id);
+
+    // block layout in LDS: short 0 = d, shorts 1..16 = qs
+    uint16_t *blk = stage + local_block * 17;
+    blk[1 + sub * 2] = (uint16_t)(q & 0xffff);
+    blk[2 + sub * 2] = (uint16_t)(q >> 16);
+    if (sub == 0) blk[0] = (uint16_t)f32_to_fp16_bits(d);
+    __syncthreads();
+
+    const int64_t first = (int64_t)blockIdx.x * kQ8_0BlocksPerGroup;
+    const int64_t nvalid = nblocks - first < kQ8_0BlocksPerGroup ? nblocks - first : kQ8_0BlocksPerGroup;
+    const int bytes = (int)nvalid * 34;
+    uint8_t *out = y + first * 34;
+    if (kAligned4) {
+        // 1088 B per full group; the group base is a multiple of 1088 (4-aligned).
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(stage);
+        uint32_t *dst = reinterpret_cast<uint32_t *>(out);
+        const int words = bytes >> 2;
+        for (int i = tid; i < words; i += 256) dst[i] = src[i];
+        if ((bytes & 3) && tid == 0) reinterpret_cast<uint16_t *>(out)[bytes / 2 - 1] = stage[bytes / 2 - 1];
+    } else {
+        uint16_t *dst = reinterpret_cast<uint16_t *>(out);
+        for (int i = tid; i < bytes / 2; i += 256) dst[i] = stage[i];
+    }
+}
+
+// One wavefront per 256-element super-block; lane l owns elements 4l..4l+3.
+__global__ __launch_bounds__(256) void quantize_q8_K_kernel(const float *__restrict__ x, uint8_t *__restrict__ y,
+                                                           int64_t nblocks) {
+    const int lane = threadIdx.x & 63;
+    const int64_t block = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (block >= nblocks) return;
+    const float4 v = *reinterpret_cast<const float4 *>(x + block * 256 + lane * 4);
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = group_max<64>(amax);
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint32_t q = quantize4(v, id);
+    int s = (int)(int8_t)(q & 0xff) + (int)(int8_t)((q >> 8) & 0xff) + (int)(int8_t)((q >> 16) & 0xff) +
+            (int)(int8_t)(q >> 24);
+    s = group_sum<4>(s);
+
+    uint8_t *out = y + block * 292;
+    reinterpret_cast<uint32_t *>(out + 4)[lane] = q;
+    if ((lane & 3) == 0) reinterpret_cast<int16_t *>(out + 260)[lane >> 2] = (int16_t)s;
+    if (lane == 0) *reinterpret_cast<float *>(out) = d;
+}
+
+}  // namespace
+
+hipError_t launch_quantize_q8_0(const float *x, void *y, int64_t rows, int64_t k, hipStream_t stream) {
+    const int64_t nblocks = rows * (k / 32);
+    if (nblocks == 0) return hipSuccess;
+    const int64_t groups = (nblocks + kQ8_0BlocksPerGroup - 1) / kQ8_0BlocksPerGroup;
+    const bool aligned4 = (reinterpret_cast<uintptr_t>(y) & 3) == 0;
+    if (aligned4)
+        hipLaunchKernelGGL(quantize_q8_0_kernel<true>, dim3((unsigned)groups), dim3(256), 0, stream, x,
+                           static_cast<uint8_t *>(y), nblocks);
+    else
+        hipLaunchKernelGGL(quantize_q8_0_kernel<false>, dim3((unsigned)groups), dim3(256), 0, stream, x,
+                           static_cast<uint8_t *>(y), nblocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_q8_K(const float *x, void *y, int64_t rows, int64_t k, hipStream_t stream) {
+    const int64_t nblocks = rows * (k / 256);
+    if (nblocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(quantize_q8_K_kernel, dim3((unsigned)((nblocks + 3) / 4)), dim3(256), 0, stream, x,
+                       static_cast<uint8_t *>(y), nblocks);
+    return hipGetLastError();
+}
+
+}  // namespace pfng

@@ -1,0 +1,73 @@
+"""The C-ABI library loads, exports every symbol include/*.h declares, and rejects
+bad arguments before touching the device — CPU only (no kernel launches)."""
+from __future__ import annotations
+
+import ctypes
+import glob
+import os
+import re
+import subprocess
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    for h in glob.glob(os.path.join(REPO, "include", "*.h")):
+        text = open(h).read()
+        for m in re.finditer(r"^\s*(?:const\s+)?[\w\s\*]+?\b(pfng_hip_\w+)\s*\(", text, re.M):
+            names.add(m.group(1))
+    return sorted(names)
+
+
+def test_header_declares_the_abi():
+    names = declared_symbols()
+    assert "pfng_hip_mul_mat_q4_0_q8_0" in names and "pfng_hip_quantize_q8_K" in names
+    assert len(names) >= 12
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg.lib()
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert not missing, missing
+    out = subprocess.run(["nm", "-D", "--defined-only", pkg.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    assert set(declared_symbols()) <= exported
+    assert set(pkg.EXPORTED_SYMBOLS) == set(declared_symbols())
+
+
+def test_version_string(pkg):
+    assert "gfx950" in pkg.version()
+
+
+@pytest.mark.parametrize("call,expect", [
+    (lambda L: L.pfng_hip_quantize_q8_0(None, None, 4, 33, None), 1),
+    (lambda L: L.pfng_hip_quantize_q8_0(None, None, -1, 32, None), 1),
+    (lambda L: L.pfng_hip_quantize_q8_0(None, None, 0, 32, None), 0),
+    (lambda L: L.pfng_hip_quantize_q8_K(None, None, 2, 128, None), 1),
+    (lambda L: L.pfng_hip_quantize_q8_K(ctypes.c_void_p(16), ctypes.c_void_p(3), 2, 256, None), 1),
+    (lambda L: L.pfng_hip_mul_mat(7, None, None, None, 1, 1, 32, 0, None), 1),
+    (lambda L: L.pfng_hip_mul_mat(0, None, None, None, 1, 1, 48, 0, None), 1),
+    (lambda L: L.pfng_hip_mul_mat(1, None, None, None, 1, 1, 512 + 32, 0, None), 1),
+    (lambda L: L.pfng_hip_mul_mat(0, None, None, None, 0, 5, 32, 0, None), 0),
+    (lambda L: L.pfng_hip_mul_mat(0, None, None, None, 4, 4, 64, 0, None), 1),
+    (lambda L: L.pfng_hip_mul_mat(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 4, 4, 64, 9, None), 1),
+    (lambda L: L.pfng_hip_mul_mat(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 64, 4, 96, 2, None), 2),
+    (lambda L: L.pfng_hip_mul_mat(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 9, 4, 256, 1, None), 2),
+    (lambda L: L.pfng_hip_compute(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 4, 4, 64, None, 10, 0, None), 1),
+    (lambda L: L.pfng_hip_block_isums(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 4, 4, 96, None), 2),
+])
+def test_argument_validation(pkg, call, expect):
+    L = pkg.lib()
+    assert call(L) == expect
+    if expect:
+        assert pkg.last_error()
+
+
+def test_workspace_size(pkg):
+    L = pkg.lib()
+    assert L.pfng_hip_compute_workspace_size(0, 3, 64) == 3 * 2 * 34
+    assert L.pfng_hip_compute_workspace_size(1, 3, 512) == 3 * 2 * 292
+    assert L.pfng_hip_compute_workspace_size(2, 0, 512) == 0

@@ -1,0 +1,207 @@
+"""GPU parity: every HIP path through the C-ABI against the CPU oracle.
+
+Bars: quantized activation bytes and integer block sums bit-exact; the naive
+path's fp32 output bit-exact (it keeps the reference's operation order); the
+GEMV and MFMA paths within |err| <= 1e-5 * sum|terms| per output element.
+At the baseline configs' full sizes the oracle checks a seeded sample of rows.
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TOL = 1e-5  # the fp32 contract: |gpu - oracle| <= 1e-5 * sum|terms|
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def dev(torch, arr):
+    """numpy (structured) array -> CUDA uint8/float tensor with the same bytes."""
+    if arr.dtype == np.float32:
+        return torch.from_numpy(np.ascontiguousarray(arr)).cuda()
+    b = np.ascontiguousarray(arr).view(np.uint8).reshape(arr.shape[0], -1)
+    return torch.from_numpy(b).cuda()
+
+
+def host_blocks(t, dtype):
+    b = t.cpu().numpy()
+    return b.reshape(-1).view(dtype).reshape(b.shape[0], -1)
+
+
+def run_mul_mat(hip, torch, qtype, w, aq, m, n, k, path):
+    out = hip.mul_mat(qtype, dev(torch, w), dev(torch, aq), m, n, k, path=path)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def check_close(oracle, qtype, got, w, aq, m, n, k, rows=None, label=""):
+    """Compare got (rows x n) with the oracle on activation rows `rows`."""
+    if rows is None:
+        rows = np.arange(m)
+    sub = np.ascontiguousarray(aq[rows])
+    expect = oracle.matmul(qtype, w, sub, len(rows), n, k)
+    terms = oracle.abs_terms(qtype, w, sub, len(rows), n, k)
+    ok, worst, idx = oracle.within_tolerance(got[rows], expect, terms, TOL)
+    assert ok, f"{label}: worst err/bound {worst:.3g} at {np.unravel_index(idx, expect.shape)}"
+    return worst
+
+
+# ------------------------------------------------------------ quantizers ----
+
+@pytest.mark.parametrize("rows,k", [(1, 32), (37, 4096), (480, 1536), (3, 96)])
+def test_quantize_q8_0_bit_exact(hip, torch_gpu, oracle, rows, k):
+    torch = torch_gpu
+    say(f"quantize_q8_0 rows={rows} k={k}")
+    rng = np.random.default_rng(rows * 7 + k)
+    x = (rng.standard_normal((rows, k)) * rng.uniform(1e-3, 50, (rows, 1))).astype(np.float32)
+    x[0, :min(k, 32)] = 0.0                      # a zero block
+    x[-1, :8] = np.float32(0.5) * np.arange(8)   # ties
+    got = hip.quantize_q8_0(dev(torch, x))
+    torch.cuda.synchronize()
+    expect = oracle.quantize_q8_0(x)
+    assert np.array_equal(got.cpu().numpy().reshape(-1), expect.view(np.uint8).reshape(-1))
+
+
+@pytest.mark.parametrize("rows,k", [(1, 256), (29, 4096), (512, 4096)])
+def test_quantize_q8_K_bit_exact(hip, torch_gpu, oracle, rows, k):
+    torch = torch_gpu
+    say(f"quantize_q8_K rows={rows} k={k}")
+    rng = np.random.default_rng(rows * 5 + k)
+    x = (rng.standard_normal((rows, k)) * rng.uniform(1e-3, 50, (rows, 1))).astype(np.float32)
+    x[0, :256] = 0.0
+    got = hip.quantize_q8_K(dev(torch, x))
+    torch.cuda.synchronize()
+    expect = oracle.quantize_q8_K(x)
+    assert np.array_equal(got.cpu().numpy().reshape(-1), expect.view(np.uint8).reshape(-1))
+
+
+@pytest.mark.parametrize("name", ["q8_0", "q8_K"])
+def test_quantizer_edges_match_reference_fixture(hip, torch_gpu, name):
+    torch = torch_gpu
+    say(f"quantize edges {name}")
+    e = np.load(os.path.join(GOLDEN, "ref_quant_edges.npz"))
+    x, y = e[f"{name}/x"], e[f"{name}/y"]
+    fn = hip.quantize_q8_0 if name == "q8_0" else hip.quantize_q8_K
+    got = fn(dev(torch, x))
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy().reshape(-1), y.reshape(-1))
+
+
+# ------------------------------------------------- golden reference vectors ----
+
+@pytest.mark.parametrize("tag,qtype", [("q4_0_24x32x256", 0), ("q4_0_3x5x96", 0), ("q4_K_8x16x512", 1),
+                                       ("iq2_xxs_8x16x512", 2)])
+def test_compute_matches_reference_vectors(hip, torch_gpu, oracle, tag, qtype):
+    """pfng_hip_compute (GPU quantize + product) on the reference's own seeded inputs."""
+    torch = torch_gpu
+    say(f"compute golden {tag}")
+    v = np.load(os.path.join(GOLDEN, "ref_vectors.npz"))
+    act, w8, out_ref = v[f"{tag}/act"], v[f"{tag}/weight"], v[f"{tag}/out"]
+    m, k = act.shape
+    n = out_ref.shape[1]
+    wt = torch.from_numpy(w8.reshape(n, -1)).cuda()
+    # naive path: the reference's exact fp32 order -> bit-identical
+    got = hip.compute(qtype, dev(torch, act), wt, n, path=hip.PATH_NAIVE)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), out_ref.view(np.uint32))
+    # automatic path: within tolerance
+    got = hip.compute(qtype, dev(torch, act), wt, n, path=hip.PATH_AUTO)
+    torch.cuda.synchronize()
+    w = w8.reshape(-1).view(oracle.WEIGHT_DTYPE[qtype]).reshape(n, -1)
+    aq = oracle.quantize_activation(qtype, act)
+    check_close(oracle, qtype, got.cpu().numpy(), w, aq, m, n, k, label=tag)
+
+
+# ------------------------------------------------------------------ naive ----
+
+@pytest.mark.parametrize("qtype,m,n,k", [(0, 7, 33, 320), (1, 5, 9, 768), (2, 5, 9, 768)])
+def test_naive_bit_exact(hip, torch_gpu, oracle, qtype, m, n, k):
+    torch = torch_gpu
+    say(f"naive type={qtype} {m}x{n}x{k}")
+    act, w = oracle.create_input(qtype, m, n, k, seed=21)
+    aq = oracle.quantize_activation(qtype, act)
+    got = run_mul_mat(hip, torch, qtype, w, aq, m, n, k, hip.PATH_NAIVE)
+    expect = oracle.matmul(qtype, w, aq, m, n, k)
+    assert np.array_equal(got.view(np.uint32), expect.view(np.uint32))
+
+
+# ------------------------------------------------------------------- GEMV ----
+
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (257, 1536), (64, 256), (33, 8192)])
+def test_gemv_q4_0(hip, torch_gpu, oracle, m, n, k):
+    torch = torch_gpu
+    say(f"gemv q4_0 m={m} n={n} k={k}")
+    act, w = oracle.create_input(0, m, n, k, seed=m * 31 + n)
+    aq = oracle.quantize_q8_0(act)
+    got = run_mul_mat(hip, torch, 0, w, aq, m, n, k, hip.PATH_GEMV)
+    check_close(oracle, 0, got, w, aq, m, n, k, label=f"gemv m={m} n={n} k={k}")
+
+
+# ------------------------------------------------------------------- MFMA ----
+
+@pytest.mark.parametrize("m,n,k", [(32, 32, 128), (100, 77, 256), (480, 1536, 1536), (9, 300, 640), (2048, 4096, 256)])
+def test_mfma_q4_0(hip, torch_gpu, oracle, m, n, k):
+    torch = torch_gpu
+    say(f"mfma q4_0 {m}x{n}x{k}")
+    act, w = oracle.create_input(0, m, n, k, seed=m + n + k)
+    aq = oracle.quantize_q8_0(act)
+    got = run_mul_mat(hip, torch, 0, w, aq, m, n, k, hip.PATH_MFMA)
+    rows = None if m * n * k <= 480 * 1536 * 1536 else np.sort(np.random.default_rng(1).choice(m, 64, replace=False))
+    check_close(oracle, 0, got, w, aq, m, n, k, rows=rows, label=f"mfma {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(32, 32, 128), (70, 45, 384), (64, 64, 1536)])
+def test_block_isums_q4_0_bit_exact(hip, torch_gpu, oracle, m, n, k):
+    torch = torch_gpu
+    say(f"block isums q4_0 {m}x{n}x{k}")
+    act, w = oracle.create_input(0, m, n, k, seed=5)
+    aq = oracle.quantize_q8_0(act)
+    got = hip.block_isums(0, dev(torch, w), dev(torch, aq), m, n, k)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), oracle.isums(0, w, aq, m, n, k))
+
+
+# ---------------------------------------------------- full baseline configs ----
+
+def test_config1_gemv_full_size(hip, torch_gpu, oracle):
+    """c1: q4_0 GEMV M=1 N=4096 K=4096, whole output checked."""
+    torch = torch_gpu
+    say("c1 gemv 1x4096x4096")
+    act, w = oracle.create_input(0, 1, 4096, 4096, seed=1)
+    got = hip.compute(0, dev(torch, act), dev(torch, w), 4096)
+    torch.cuda.synchronize()
+    aq = oracle.quantize_q8_0(act)
+    check_close(oracle, 0, got.cpu().numpy(), w, aq, 1, 4096, 4096, label="c1")
+
+
+def test_config4_prefill_full_size_sampled(hip, torch_gpu, oracle):
+    """c4: q4_0 GEMM M=2048 N=11008 K=4096; oracle on 24 seeded rows plus
+    size-independent checks on the whole output (finite, row-permutation equivariance)."""
+    torch = torch_gpu
+    m, n, k = 2048, 11008, 4096
+    say("c4 mfma 2048x11008x4096")
+    act, w = oracle.create_input(0, m, n, k, seed=1)
+    wt = dev(torch, w)
+    at = dev(torch, act)
+    aq_t = hip.quantize_q8_0(at)
+    got = hip.mul_mat(0, wt, aq_t, m, n, k)
+    torch.cuda.synchronize()
+    aq = oracle.quantize_q8_0(act)
+    assert np.array_equal(aq_t.cpu().numpy().reshape(-1), aq.view(np.uint8).reshape(-1))
+    g = got.cpu().numpy()
+    assert np.isfinite(g).all()
+    rows = np.sort(np.random.default_rng(4).choice(m, 24, replace=False))
+    check_close(oracle, 0, g, w, aq, m, n, k, rows=rows, label="c4")
+    # permuting activation rows permutes output rows exactly (tiles see the same blocks)
+    perm = torch.randperm(m, generator=torch.Generator().manual_seed(0)).cuda()
+    got_p = hip.mul_mat(0, wt, aq_t[perm].contiguous(), m, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(got_p, got[perm])
