@@ -151,6 +151,7 @@ def main():
     ap.add_argument("--steps", type=int, default=6400, help="timed GEMV steps (rounded up to a multiple of 32)")
     ap.add_argument("--warmup", type=int, default=640)
     ap.add_argument("--gemm-steps", type=int, default=2048)
+    ap.add_argument("--prefill-steps", type=int, default=64, help="timed c4 GEMM steps (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline budget (0 = skip)")
     args = ap.parse_args()
 
@@ -223,6 +224,32 @@ def main():
     log(f"[bench] c0 gemm: {steps0} steps, {tops:.2f} TOPS wall; kernel {gemm_kernel_us:.3f} us -> "
         f"{gemm_achieved:.2f} TOPS; verify c1={ok1} c0={ok0}")
 
+    # ---------------- config 4: Llama-7B FFN prefill GEMM M=2048 N=11008 K=4096 ----------------
+    prefill = None
+    if args.prefill_steps > 0:
+        m4, n4, k4 = 2048, 11008, 4096
+        act4, w4 = O.create_input(0, m4, n4, k4, seed=1, variant=1)
+        w4_t = torch.from_numpy(np.ascontiguousarray(w4).view(np.uint8).reshape(n4, -1)).cuda()
+        aq4 = pkg.quantize_q8_0(torch.from_numpy(act4).cuda())
+        out4 = torch.empty((m4, n4), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        g4 = capture(torch, lambda i: pkg.mul_mat(0, w4_t, aq4, m4, n4, k4, out=out4), 4)
+        wall4, ev4, steps4 = time_graph(torch, g4, 4, args.prefill_steps, 8)
+        ops4 = 2.0 * m4 * n4 * k4
+        k4_us = ev4 * 1e3 / steps4
+        rows = np.sort(np.random.default_rng(4).choice(m4, 16, replace=False))
+        aq4_h = O.quantize_q8_0(act4[rows])
+        ok4 = O.within_tolerance(out4.cpu().numpy()[rows], O.matmul(0, w4, aq4_h, 16, n4, k4),
+                                 O.abs_terms(0, w4, aq4_h, 16, n4, k4))[0]
+        prefill = {"workload": "c4: q4_0 x q8_0 GEMM M=2048 N=11008 K=4096", "value": round(ops4 * steps4 / wall4 / 1e12, 3),
+                   "unit": "TOPS", "steps": steps4, "ms_per_step": round(wall4 * 1e3 / steps4, 6), "verified_rows": ok4,
+                   "roofline": {"bound": "mfma", "achieved": round(ops4 / (k4_us * 1e-6) / 1e12, 3),
+                                "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                                "frac": round(ops4 / (k4_us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4), "traffic": None,
+                                "kernel": "gemm_q4_0_kernel", "kernel_us": round(k4_us, 3)}}
+        log(f"[bench] c4 gemm: {steps4} steps, {prefill['value']} TOPS wall, kernel {k4_us:.1f} us, verify={ok4}")
+        del w4_t, aq4, out4
+
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
     if cpu:
         log(f"[bench] cpu baseline: {cpu}")
@@ -252,7 +279,8 @@ def main():
                  "roofline": {"bound": "mfma", "achieved": round(gemm_achieved, 3), "peak": INT8_PEAK_TOPS,
                               "unit": "TFLOP/s", "frac": round(gemm_achieved / INT8_PEAK_TOPS, 4), "traffic": None,
                               "kernel": "gemm_q4_0_kernel", "kernel_us": round(gemm_kernel_us, 4)}},
-        "verified": bool(ok1 and ok0),
+        "prefill": prefill,
+        "verified": bool(ok1 and ok0 and (prefill is None or prefill["verified_rows"])),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

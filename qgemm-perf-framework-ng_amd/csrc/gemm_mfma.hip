@@ -3,20 +3,22 @@
 // q4_0 x q8_0: C[m][n] = sum_b S_b[m][n] * da[m][b] * dw[n][b], with S_b the
 // exact int32 dot of block b (llama_reference.cpp:134-146).
 //
-// Per workgroup tile BM x BN and per K stage of KB = 4 blocks (128 elements):
-//   * global -> registers: each thread loads one 68-byte q8_0 block pair and
-//     one 36-byte q4_0 block pair (4-byte aligned when k % 128 == 0), with the
-//     loads of stage s+1 in flight while stage s is computed;
-//   * registers -> LDS: activation int8 copied as is (realigned by 2 bytes for
-//     the even block of a pair); weight nibbles expanded to 16*(q-8) int8;
-//     padded 144-byte rows keep the 16-byte MFMA operand reads conflict free;
+// Workgroup tile BM x BN, K stages of KB blocks (32*KB elements):
+//   * global -> registers: every thread loads whole q8_0 and q4_0 block pairs
+//     (68 / 36 bytes, dword loads, 4-byte aligned when k % 64 == 0) into a ring
+//     of P register sets, so P-1 stages are in flight while one is computed.
+//     The loads are unconditional (rows clamped at the matrix edge) and a
+//     scheduling barrier keeps them ahead of the arithmetic.
+//   * registers -> LDS: activation int8 copied (the even block of a pair
+//     realigned by two bytes); weight nibbles expanded to 16*(q-8) int8; fp16
+//     scales kept per row. Rows are padded so the 16-byte MFMA operand reads
+//     are free of bank conflicts.
 //   * per block and 32x32 tile: S16 = v_mfma_i32_32x32x32_i8(act, w16) (= 16*S_b),
-//     P = v_mfma_f32_32x32x8_f16(da, dw) (= da*dw exactly, an outer product of
-//     two fp16 vectors on the matrix core), acc = fma(float(S16), P, acc).
-//     C = acc / 16 at the end (a power of two, so rounding is unaffected).
-// The epilogue costs two VALU operations per (m, n, block) item (cvt + fma); the
-// matrix core carries the scale products. This is the VALU-bound part of the
-// format: the int8 MFMA itself would finish the same items about twice as fast.
+//     P = v_mfma_f32_32x32x8_f16(da, dw) (the exact outer product da*dw on the
+//     matrix core), acc = fma(float(S16), P, acc); C = acc / 16 at the end.
+// The epilogue costs two VALU operations per (m, n, block) item; the int8
+// matrix core finishes the same items about twice as fast, so this format is
+// VALU-bound at roughly half of the int8 MFMA rate.
 //
 // A diagnostic instantiation writes S_b instead of accumulating (block isums).
 #include "device_common.h"
@@ -26,117 +28,207 @@ namespace pfng {
 
 namespace {
 
-constexpr int KB = 4;                     // blocks per K stage
-constexpr int kRowStride = KB * 32 + 16;  // LDS bytes per tile row (int8 + pad)
+constexpr int kXcds = 8;    // MI355X: 8 XCDs, each with its own L2
+constexpr int kGroupM = 8;  // m-tiles walked together inside an XCD's tile range
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int KB, int RING = 2, int MINW = 2>
 struct Q40Config {
-    static constexpr int kBM = BM, kBN = BN, kWM = WM, kWN = WN;
+    static constexpr int kBM = BM, kBN = BN, kWM = WM, kWN = WN, kKB = KB;
+    // register sets of loaded-but-not-stored stages (1 or 2); with 2 the loads
+    // of stage s+3 are issued while stage s is computed
+    static constexpr int kRing = RING;
+    // waves per SIMD the register budget must allow: the fp32 epilogue needs two
+    // resident waves per SIMD to keep the VALU issuing while the other waits
+    static constexpr int kMinWavesPerEU = MINW;
     static constexpr int kThreads = 64 * WM * WN;
     static constexpr int TM = BM / WM / 32;  // 32x32 tiles per wave along m
     static constexpr int TN = BN / WN / 32;  // along n
-    static constexpr int kActPairs = BM * KB / 2;
-    static constexpr int kWPairs = BN * KB / 2;
-    static constexpr int kActIters = (kActPairs + kThreads - 1) / kThreads;
-    static constexpr int kWIters = (kWPairs + kThreads - 1) / kThreads;
+    static constexpr int kPairsPerRow = KB / 2;
+    static constexpr int kActPairs = BM * kPairsPerRow;
+    static constexpr int kWPairs = BN * kPairsPerRow;
+    static constexpr int kActPT = kActPairs / kThreads;  // pairs per thread
+    static constexpr int kWPT = kWPairs / kThreads;
+    static constexpr int kRowStride = KB * 32 + 16;  // LDS bytes per tile row (int8 + pad)
     // LDS layout
     static constexpr int kAq = 0;
-    static constexpr int kAd = kAq + BM * kRowStride;
+    static constexpr int kAd = kAq + BM * kRowStride;       // fp16 da[row][KB]
     static constexpr int kWq = kAd + BM * KB * 2;
-    static constexpr int kWd = kWq + BN * kRowStride;
-    static constexpr int kZero = kWd + BN * KB * 8;
-    static constexpr int kLdsBytes = kZero + 16;
+    static constexpr int kWd = kWq + BN * kRowStride;       // fp16 dw[row][KB]
+    static constexpr int kBufBytes = kWd + BN * KB * 2;  // one stage
+    static constexpr int kLdsBytes = 2 * kBufBytes;          // double-buffered
     static_assert(TM >= 1 && TN >= 1, "tile too small");
+    static_assert(KB % 4 == 0, "KB must be a multiple of 4 (scale vectors are read four at a time)");
+    static_assert(kActPT * kThreads == kActPairs && kWPT * kThreads == kWPairs, "pairs must split evenly over threads");
+    static_assert(kActPT >= 1 && kWPT >= 1, "every thread loads at least one pair of each operand");
+    static_assert(kAd % 16 == 0 && kWq % 16 == 0 && kWd % 16 == 0, "LDS regions 16-byte aligned");
 };
 
-struct ActRegs {
-    uint32_t v[17];
-};
-struct WRegs {
-    uint32_t v[9];
+template <class C>
+struct StageRegs {
+    uint32_t a[C::kActPT][17];
+    uint32_t w[C::kWPT][9];
 };
 
 template <class C>
 __device__ __forceinline__ void load_stage(const uint8_t *__restrict__ a, const uint8_t *__restrict__ w, int m, int n,
-                                           int nb, int m0, int n0, int kb0, ActRegs (&ar)[C::kActIters],
-                                           WRegs (&wr)[C::kWIters]) {
+                                           int nb, int m0, int n0, int kb0, StageRegs<C> &r) {
 #pragma unroll
-    for (int it = 0; it < C::kActIters; ++it) {
+    for (int it = 0; it < C::kActPT; ++it) {
         const int task = threadIdx.x + it * C::kThreads;
-        if (task < C::kActPairs) {
-            const int r = task / (KB / 2), p = task % (KB / 2);
-            int row = m0 + r;
-            row = row < m ? row : m - 1;
-            const uint32_t *src = reinterpret_cast<const uint32_t *>(a + ((size_t)row * nb + kb0 + 2 * p) * 34);
+        const int row = m0 + task / C::kPairsPerRow;
+        const int p = task % C::kPairsPerRow;
+        const int lrow = row < m ? row : m - 1;
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(a + ((size_t)lrow * nb + kb0 + 2 * p) * 34);
 #pragma unroll
-            for (int i = 0; i < 17; ++i) ar[it].v[i] = src[i];
-        }
+        for (int i = 0; i < 17; ++i) r.a[it][i] = src[i];
     }
 #pragma unroll
-    for (int it = 0; it < C::kWIters; ++it) {
+    for (int it = 0; it < C::kWPT; ++it) {
         const int task = threadIdx.x + it * C::kThreads;
-        if (task < C::kWPairs) {
-            const int r = task / (KB / 2), p = task % (KB / 2);
-            int row = n0 + r;
-            row = row < n ? row : n - 1;
-            const uint32_t *src = reinterpret_cast<const uint32_t *>(w + ((size_t)row * nb + kb0 + 2 * p) * 18);
+        const int row = n0 + task / C::kPairsPerRow;
+        const int p = task % C::kPairsPerRow;
+        const int lrow = row < n ? row : n - 1;
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(w + ((size_t)lrow * nb + kb0 + 2 * p) * 18);
 #pragma unroll
-            for (int i = 0; i < 9; ++i) wr[it].v[i] = src[i];
-        }
+        for (int i = 0; i < 9; ++i) r.w[it][i] = src[i];
     }
 }
 
 template <class C>
-__device__ __forceinline__ void store_stage(uint8_t *lds, const ActRegs (&ar)[C::kActIters],
-                                            const WRegs (&wr)[C::kWIters]) {
+__device__ __forceinline__ void store_stage(uint8_t *lds, const StageRegs<C> &r) {
 #pragma unroll
-    for (int it = 0; it < C::kActIters; ++it) {
+    for (int it = 0; it < C::kActPT; ++it) {
         const int task = threadIdx.x + it * C::kThreads;
-        if (task < C::kActPairs) {
-            const int r = task / (KB / 2), p = task % (KB / 2);
-            const uint32_t *v = ar[it].v;
-            uint4 *dst = reinterpret_cast<uint4 *>(lds + C::kAq + r * kRowStride + 2 * p * 32);
-            dst[0] = make_uint4(shift2(v[0], v[1]), shift2(v[1], v[2]), shift2(v[2], v[3]), shift2(v[3], v[4]));
-            dst[1] = make_uint4(shift2(v[4], v[5]), shift2(v[5], v[6]), shift2(v[6], v[7]), shift2(v[7], v[8]));
-            dst[2] = make_uint4(v[9], v[10], v[11], v[12]);
-            dst[3] = make_uint4(v[13], v[14], v[15], v[16]);
-            *reinterpret_cast<uint32_t *>(lds + C::kAd + r * KB * 2 + 4 * p) = (v[0] & 0xffffu) | (v[8] & 0xffff0000u);
-        }
+        const int row = task / C::kPairsPerRow, p = task % C::kPairsPerRow;
+        const uint32_t *v = r.a[it];
+        uint4 *dst = reinterpret_cast<uint4 *>(lds + C::kAq + row * C::kRowStride + 2 * p * 32);
+        dst[0] = make_uint4(shift2(v[0], v[1]), shift2(v[1], v[2]), shift2(v[2], v[3]), shift2(v[3], v[4]));
+        dst[1] = make_uint4(shift2(v[4], v[5]), shift2(v[5], v[6]), shift2(v[6], v[7]), shift2(v[7], v[8]));
+        dst[2] = make_uint4(v[9], v[10], v[11], v[12]);
+        dst[3] = make_uint4(v[13], v[14], v[15], v[16]);
+        *reinterpret_cast<uint32_t *>(lds + C::kAd + (row * C::kKB + 2 * p) * 2) = (v[0] & 0xffffu) | (v[8] & 0xffff0000u);
     }
 #pragma unroll
-    for (int it = 0; it < C::kWIters; ++it) {
+    for (int it = 0; it < C::kWPT; ++it) {
         const int task = threadIdx.x + it * C::kThreads;
-        if (task < C::kWPairs) {
-            const int r = task / (KB / 2), p = task % (KB / 2);
-            const uint32_t *u = wr[it].v;
-            uint32_t q0[4] = {shift2(u[0], u[1]), shift2(u[1], u[2]), shift2(u[2], u[3]), shift2(u[3], u[4])};
-            uint32_t lo[4], hi[4];
+        const int row = task / C::kPairsPerRow, p = task % C::kPairsPerRow;
+        const uint32_t *u = r.w[it];
+        const uint32_t q0[4] = {shift2(u[0], u[1]), shift2(u[1], u[2]), shift2(u[2], u[3]), shift2(u[3], u[4])};
+        uint32_t lo[4], hi[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) q4_0_unpack16(q0[i], lo[i], hi[i]);
-            uint4 *dst = reinterpret_cast<uint4 *>(lds + C::kWq + r * kRowStride + 2 * p * 32);
-            dst[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            dst[1] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        for (int i = 0; i < 4; ++i) q4_0_unpack16(q0[i], lo[i], hi[i]);
+        uint4 *dst = reinterpret_cast<uint4 *>(lds + C::kWq + row * C::kRowStride + 2 * p * 32);
+        dst[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        dst[1] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) q4_0_unpack16(u[5 + i], lo[i], hi[i]);
-            dst[2] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            dst[3] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-            // scale of block t placed in fp16 slot t of an 8-byte entry (slot-expanded)
-            const uint32_t d0 = u[0] & 0xffffu, d1 = u[4] >> 16;
-            uint2 *wd = reinterpret_cast<uint2 *>(lds + C::kWd + (r * KB + 2 * p) * 8);
-            if (p == 0) {
-                wd[0] = make_uint2(d0, 0u);
-                wd[1] = make_uint2(d1 << 16, 0u);
-            } else {
-                wd[0] = make_uint2(0u, d0);
-                wd[1] = make_uint2(0u, d1 << 16);
+        for (int i = 0; i < 4; ++i) q4_0_unpack16(u[5 + i], lo[i], hi[i]);
+        dst[2] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        dst[3] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        *reinterpret_cast<uint32_t *>(lds + C::kWd + (row * C::kKB + 2 * p) * 2) = (u[0] & 0xffffu) | (u[4] & 0xffff0000u);
+    }
+}
+
+// f16x4 holding one fp16 value in slot `slot` (0..3) and zeros elsewhere.
+__device__ __forceinline__ f16x4 one_hot_half(uint32_t h16, int slot) {
+    const uint32_t lo = slot == 0 ? h16 : (slot == 1 ? h16 << 16 : 0u);
+    const uint32_t hi = slot == 2 ? h16 : (slot == 3 ? h16 << 16 : 0u);
+    return __builtin_bit_cast(f16x4, make_uint2(lo, hi));
+}
+
+// Operand fragments of one block t for the wave's TM x TN tiles.
+template <class C>
+struct Frags {
+    i32x4 av[C::TM];
+    i32x4 wv[C::TN];
+    f16x4 ad[C::TM];  // da of blocks t4..t4+3 in the four fp16 slots
+    f16x4 wd[C::TN];  // dw of block t in slot t % 4 (zero for K-half 1 lanes)
+};
+
+// Per-lane LDS base addresses of one stage buffer; every fragment read is a
+// base plus a compile-time offset (within the 16-bit ds_read immediate range).
+struct FragBases {
+    const uint8_t *aq, *ad, *wq, *wd;
+};
+
+template <class C>
+__device__ __forceinline__ FragBases frag_bases(const uint8_t *buf, int lane, int wave_m, int wave_n) {
+    const int li = lane & 31, lh = lane >> 5;
+    const int ra = wave_m * C::TM * 32 + li, rw = wave_n * C::TN * 32 + li;
+    FragBases b;
+    b.aq = buf + C::kAq + ra * C::kRowStride + lh * 16;
+    b.ad = buf + C::kAd + ra * C::kKB * 2;
+    b.wq = buf + C::kWq + rw * C::kRowStride + lh * 16;
+    b.wd = buf + C::kWd + rw * C::kKB * 2;
+    return b;
+}
+
+template <class C>
+__device__ __forceinline__ void load_frags(const FragBases &b, int t, int lh, Frags<C> &f) {
+    const int t4 = t & ~3, tt = t & 3;
+#pragma unroll
+    for (int tm = 0; tm < C::TM; ++tm) {
+        f.av[tm] = *reinterpret_cast<const i32x4 *>(b.aq + tm * 32 * C::kRowStride + t * 32);
+        f.ad[tm] = *reinterpret_cast<const f16x4 *>(b.ad + tm * 32 * C::kKB * 2 + t4 * 2);
+    }
+#pragma unroll
+    for (int tn = 0; tn < C::TN; ++tn) {
+        f.wv[tn] = *reinterpret_cast<const i32x4 *>(b.wq + tn * 32 * C::kRowStride + t * 32);
+        const uint32_t h16 = *reinterpret_cast<const uint16_t *>(b.wd + tn * 32 * C::kKB * 2 + t * 2);
+        f.wd[tn] = one_hot_half(lh ? 0u : h16, tt);
+    }
+}
+
+struct ItemRegs {
+    i32x16 s16;
+    f32x16 p;
+};
+
+// One K stage: KB blocks x TM x TN tiles = a flat list of items, software-
+// pipelined so the MFMAs of item i+1 are in flight while the VALU epilogue of
+// item i runs, and the LDS fragments of block t+1 load during block t.
+template <class C, bool kIsums>
+__device__ __forceinline__ void compute_stage(const uint8_t *buf, f32x16 (&acc)[C::TM][C::TN], int32_t *isums, int m,
+                                              int n, int nb, int m0, int n0, int s, int lane, int wave_m, int wave_n) {
+    constexpr int kTiles = C::TM * C::TN;
+    constexpr int kItems = C::kKB * kTiles;
+    const FragBases bases = frag_bases<C>(buf, lane, wave_m, wave_n);
+    const int lh = lane >> 5;
+    Frags<C> fr[2];
+    ItemRegs it[2];
+    load_frags<C>(bases, 0, lh, fr[0]);
+    auto issue = [&](int item) {
+        const int t = item / kTiles, tile = item % kTiles;
+        const int tm = tile / C::TN, tn = tile % C::TN;
+        const Frags<C> &f = fr[t & 1];
+        ItemRegs &r = it[item & 1];
+        r.s16 = mfma_i8_32x32x32(f.av[tm], f.wv[tn], (i32x16){});
+        if constexpr (!kIsums) r.p = mfma_f16_32x32x8(f.ad[tm], f.wd[tn], (f32x16){});
+    };
+    issue(0);
+#pragma unroll
+    for (int item = 0; item < kItems; ++item) {
+        const int t = item / kTiles, tile = item % kTiles;
+        const int tm = tile / C::TN, tn = tile % C::TN;
+        if (tile == 0 && t + 1 < C::kKB) load_frags<C>(bases, t + 1, lh, fr[(t + 1) & 1]);
+        if (item + 1 < kItems) issue(item + 1);
+        const ItemRegs &r = it[item & 1];
+        if constexpr (kIsums) {
+            const int col = n0 + wave_n * C::TN * 32 + tn * 32 + (lane & 31);
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int row = m0 + wave_m * C::TM * 32 + tm * 32 + mfma_row(lane, q);
+                if (row < m && col < n) isums[((size_t)row * n + col) * nb + s * C::kKB + t] = r.s16[q] / 16;
             }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[tm][tn][q] = fmaf((float)r.s16[q], r.p[q], acc[tm][tn][q]);
         }
     }
 }
 
 // kIsums == false: fp32 C. kIsums == true: int32 block sums (diagnostic).
 template <class C, bool kIsums>
-__global__ __launch_bounds__(C::kThreads) void gemm_q4_0_kernel(const uint8_t *__restrict__ w,
+__global__ __launch_bounds__(C::kThreads, C::kMinWavesPerEU) void gemm_q4_0_kernel(const uint8_t *__restrict__ w,
                                                                const uint8_t *__restrict__ a, float *__restrict__ c,
                                                                int32_t *__restrict__ isums, int m, int n, int nb) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -144,12 +236,23 @@ __global__ __launch_bounds__(C::kThreads) void gemm_q4_0_kernel(const uint8_t *_
     const int wave = threadIdx.x >> 6;
     const int wave_m = wave / C::kWN;
     const int wave_n = wave % C::kWN;
-    const int m0 = blockIdx.y * C::kBM;
-    const int n0 = blockIdx.x * C::kBN;
-    const int li = lane & 31;  // operand row within a 32x32 tile
-    const int lh = lane >> 5;  // K half of the operand
-
-    if (threadIdx.x < 4) reinterpret_cast<uint32_t *>(lds + C::kZero)[threadIdx.x] = 0u;
+    // XCD-aware tile order. Workgroup ids are dealt round-robin to the 8 XCDs
+    // (id % 8); regroup them so that each XCD owns a contiguous range of tiles,
+    // walked m-fastest in groups of kGroupM m-tiles, so the workgroups resident
+    // on one XCD at a time share weight and activation tiles in its L2.
+    const int mt = (m + C::kBM - 1) / C::kBM, nt = (n + C::kBN - 1) / C::kBN;
+    const int tiles = mt * nt;
+    const int id = blockIdx.x;
+    // bijection on [0, tiles): the first 8*q ids are regrouped (q tiles per
+    // XCD), the last tiles % 8 ids keep their own index
+    const int q = tiles / kXcds;
+    const int t = id < q * kXcds ? (id % kXcds) * q + id / kXcds : id;
+    const int gm = mt < kGroupM ? mt : kGroupM;
+    const int group = t / (gm * nt), in = t % (gm * nt);
+    const int gm_here = (mt - group * gm) < gm ? (mt - group * gm) : gm;
+    const int m0 = (group * gm + in % gm_here) * C::kBM;
+    const int n0 = (in / gm_here) * C::kBN;
+    const int li = lane & 31;  // operand row / result column within a 32x32 tile
 
     f32x16 acc[C::TM][C::TN];
 #pragma unroll
@@ -157,59 +260,35 @@ __global__ __launch_bounds__(C::kThreads) void gemm_q4_0_kernel(const uint8_t *_
 #pragma unroll
         for (int j = 0; j < C::TN; ++j) acc[i][j] = (f32x16){};
 
-    ActRegs ar[C::kActIters];
-    WRegs wr[C::kWIters];
-    load_stage<C>(a, w, m, n, nb, m0, n0, 0, ar, wr);
-
-    const int stages = nb / KB;
-    for (int s = 0; s < stages; ++s) {
+    // Double-buffered LDS with one barrier per stage: stage s is computed from
+    // buffer s % 2 while the registers of stage s+1 (loaded kRing stages ago)
+    // are stored into the other buffer and the loads of stage s+1+kRing are
+    // issued. Stores and loads are unconditional (clamped stage index) so the
+    // loop body has no divergent control flow.
+    const int stages = nb / C::kKB;
+    auto clampst = [&](int st) { return st < stages ? st : stages - 1; };
+    StageRegs<C> regs[C::kRing];
+    load_stage<C>(a, w, m, n, nb, m0, n0, 0, regs[0]);
+    store_stage<C>(lds, regs[0]);
+#pragma unroll
+    for (int r = 0; r < C::kRing; ++r) load_stage<C>(a, w, m, n, nb, m0, n0, clampst(1 + r) * C::kKB, regs[r]);
+    __syncthreads();
+    auto step = [&](int s, StageRegs<C> &rg) {
+        const uint8_t *cur = lds + (s & 1) * C::kBufBytes;
+        __builtin_amdgcn_sched_barrier(0);
+        compute_stage<C, kIsums>(cur, acc, isums, m, n, nb, m0, n0, s, lane, wave_m, wave_n);
+        __builtin_amdgcn_sched_barrier(0);
+        store_stage<C>(lds + ((s + 1) & 1) * C::kBufBytes, rg);
+        __builtin_amdgcn_sched_barrier(0);
+        load_stage<C>(a, w, m, n, nb, m0, n0, clampst(s + 1 + C::kRing) * C::kKB, rg);
+        __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
-        store_stage<C>(lds, ar, wr);
-        __syncthreads();
-        if (s + 1 < stages) load_stage<C>(a, w, m, n, nb, m0, n0, (s + 1) * KB, ar, wr);
-
-        // per-stage activation scales: da of blocks 0..3 in the four fp16 slots
-        f16x4 ad[C::TM];
+    };
+    // the dispatcher guarantees stages % kRing == 0, so each ring slot is
+    // consumed in a fixed position of the unrolled body
+    for (int s = 0; s < stages; s += C::kRing) {
 #pragma unroll
-        for (int tm = 0; tm < C::TM; ++tm) {
-            const int r = wave_m * C::TM * 32 + tm * 32 + li;
-            ad[tm] = *reinterpret_cast<const f16x4 *>(lds + C::kAd + r * KB * 2);
-        }
-#pragma unroll
-        for (int t = 0; t < KB; ++t) {
-            i32x4 av[C::TM], wv[C::TN];
-            f16x4 wd[C::TN];
-#pragma unroll
-            for (int tm = 0; tm < C::TM; ++tm) {
-                const int r = wave_m * C::TM * 32 + tm * 32 + li;
-                av[tm] = *reinterpret_cast<const i32x4 *>(lds + C::kAq + r * kRowStride + t * 32 + lh * 16);
-            }
-#pragma unroll
-            for (int tn = 0; tn < C::TN; ++tn) {
-                const int r = wave_n * C::TN * 32 + tn * 32 + li;
-                wv[tn] = *reinterpret_cast<const i32x4 *>(lds + C::kWq + r * kRowStride + t * 32 + lh * 16);
-                const int off = lh ? C::kZero : C::kWd + (r * KB + t) * 8;
-                wd[tn] = *reinterpret_cast<const f16x4 *>(lds + off);
-            }
-#pragma unroll
-            for (int tm = 0; tm < C::TM; ++tm)
-#pragma unroll
-                for (int tn = 0; tn < C::TN; ++tn) {
-                    const i32x16 s16 = mfma_i8_32x32x32(av[tm], wv[tn], (i32x16){});
-                    if constexpr (kIsums) {
-                        const int col = n0 + wave_n * C::TN * 32 + tn * 32 + li;
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int row = m0 + wave_m * C::TM * 32 + tm * 32 + mfma_row(lane, r);
-                            if (row < m && col < n) isums[((size_t)row * n + col) * nb + s * KB + t] = s16[r] / 16;
-                        }
-                    } else {
-                        const f32x16 p = mfma_f16_32x32x8(ad[tm], wd[tn], (f32x16){});
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) acc[tm][tn][r] = fmaf((float)s16[r], p[r], acc[tm][tn][r]);
-                    }
-                }
-        }
+        for (int r = 0; r < C::kRing; ++r) step(s + r, regs[r]);
     }
 
     if constexpr (!kIsums) {
@@ -232,21 +311,25 @@ __global__ __launch_bounds__(C::kThreads) void gemm_q4_0_kernel(const uint8_t *_
 template <class C, bool kIsums>
 hipError_t launch_q4_0(const void *w, const void *a, float *c, int32_t *isums, int64_t m, int64_t n, int64_t k,
                        hipStream_t stream) {
-    const dim3 grid((unsigned)((n + C::kBN - 1) / C::kBN), (unsigned)((m + C::kBM - 1) / C::kBM));
+    const dim3 grid((unsigned)(((n + C::kBN - 1) / C::kBN) * ((m + C::kBM - 1) / C::kBM)));
     hipLaunchKernelGGL((gemm_q4_0_kernel<C, kIsums>), grid, dim3(C::kThreads), C::kLdsBytes, stream,
                        static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(a), c, isums, (int)m, (int)n,
                        (int)(k / 32));
     return hipGetLastError();
 }
 
-using Q40Big = Q40Config<128, 128, 2, 2>;
-using Q40Small = Q40Config<64, 64, 2, 2>;
+// large problems: 128x128 tiles, 4 waves of 64x64, 4 blocks per stage
+using Q40Big = Q40Config<128, 128, 2, 2, 4, 1>;
+// small problems: 64x64 tiles, 4 waves of 32x32, 8 blocks per stage
+using Q40Small = Q40Config<64, 64, 2, 2, 8, 1>;
+// small problems with k % 256 != 0: 64x64 tiles, 2 waves of 64x32, 4 blocks per stage
+using Q40Small4 = Q40Config<64, 64, 1, 2, 4, 1>;
 
 }  // namespace
 
 bool mfma_supported(int type, int64_t m, int64_t k) {
     (void)m;
-    if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return k % (32 * KB) == 0;
+    if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return k % (32 * 4) == 0;  // Q40Small4 takes any k % 128 == 0
     return false;
 }
 
@@ -254,14 +337,18 @@ hipError_t launch_mfma_mul_mat(int type, const void *w, const void *a, float *c,
                                hipStream_t stream) {
     if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return hipErrorInvalidValue;
     const int64_t big_tiles = ((m + 127) / 128) * ((n + 127) / 128);
-    if (big_tiles >= 512) return launch_q4_0<Q40Big, false>(w, a, c, nullptr, m, n, k, stream);
-    return launch_q4_0<Q40Small, false>(w, a, c, nullptr, m, n, k, stream);
+    // a two-slot ring needs an even number of K stages
+    if (big_tiles >= 512 && k % (Q40Big::kRing * 32 * Q40Big::kKB) == 0)
+        return launch_q4_0<Q40Big, false>(w, a, c, nullptr, m, n, k, stream);
+    if (k % (Q40Small::kRing * 32 * Q40Small::kKB) == 0)
+        return launch_q4_0<Q40Small, false>(w, a, c, nullptr, m, n, k, stream);
+    return launch_q4_0<Q40Small4, false>(w, a, c, nullptr, m, n, k, stream);
 }
 
 hipError_t launch_mfma_block_isums(int type, const void *w, const void *a, int32_t *out, int64_t m, int64_t n,
                                    int64_t k, hipStream_t stream) {
     if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return hipErrorInvalidValue;
-    return launch_q4_0<Q40Small, true>(w, a, nullptr, out, m, n, k, stream);
+    return launch_q4_0<Q40Small4, true>(w, a, nullptr, out, m, n, k, stream);
 }
 
 }  // namespace pfng

@@ -77,6 +77,24 @@ __device__ __forceinline__ void load_q4_0_group(const uint8_t *__restrict__ w, b
     }
 }
 
+// 16 * (dot of one q4_0 block with one q8_0 block) * dw * da, from the block's
+// four nibble dwords q and the activation's eight int8 dwords x (element order).
+__device__ __forceinline__ float q4_0_block_dot16(const uint32_t (&q)[4], uint32_t dw16, const uint32_t (&x)[8],
+                                                  uint32_t da16) {
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q4_0_unpack16(q[i], lo[i], hi[i]);
+    int s = __builtin_amdgcn_sdot4((int)lo[0], (int)x[0], 0, false);
+    s = __builtin_amdgcn_sdot4((int)lo[1], (int)x[1], s, false);
+    s = __builtin_amdgcn_sdot4((int)lo[2], (int)x[2], s, false);
+    s = __builtin_amdgcn_sdot4((int)lo[3], (int)x[3], s, false);
+    s = __builtin_amdgcn_sdot4((int)hi[0], (int)x[4], s, false);
+    s = __builtin_amdgcn_sdot4((int)hi[1], (int)x[5], s, false);
+    s = __builtin_amdgcn_sdot4((int)hi[2], (int)x[6], s, false);
+    s = __builtin_amdgcn_sdot4((int)hi[3], (int)x[7], s, false);
+    return (float)s * (fp16_to_f32(dw16) * fp16_to_f32(da16));
+}
+
 // Block j of a group sits at byte 18*j: fp16 d, then 16 bytes of nibbles.
 template <int M>
 __device__ __forceinline__ void gemv_q4_0_group(const uint32_t (&wv)[36], const uint8_t *gbase, float (&acc)[M]) {
@@ -172,6 +190,45 @@ __global__ __launch_bounds__(kThreads) void gemv_q4_0_kernel(const uint8_t *__re
     }
 }
 
+// m == 1: no LDS staging and no barrier. Each lane owns one q4_0 block pair of
+// its row (36 bytes, nine dword loads) and the matching q8_0 block pair of the
+// activation row (68 bytes, seventeen dword loads); both are 4-byte aligned when
+// k % 64 == 0. All 26 loads are issued before any arithmetic, so each lane pays
+// one memory round trip. One wavefront covers 64 block pairs of one row (a
+// whole row at k = 4096); 4096 rows give 4096 waves, four per SIMD.
+__global__ __launch_bounds__(kThreads) void gemv_q4_0_m1_kernel(const uint8_t *__restrict__ w,
+                                                               const uint8_t *__restrict__ a, float *__restrict__ c,
+                                                               int n, int nb) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int lrow = row < n ? row : n - 1;  // clamped: loads stay unconditional, the store is guarded
+    float acc = 0.0f;
+    for (int p = lane; p < nb / 2; p += 64) {
+        const uint32_t *ws = reinterpret_cast<const uint32_t *>(w + ((size_t)lrow * nb + 2 * p) * 18);
+        const uint32_t *as = reinterpret_cast<const uint32_t *>(a + (size_t)(2 * p) * 34);
+        uint32_t u[9], v[17];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) u[i] = ws[i];
+#pragma unroll
+        for (int i = 0; i < 17; ++i) v[i] = as[i];
+        __builtin_amdgcn_sched_barrier(0);
+        // block 2p: d at byte 0, qs at 2 (realign by two bytes); block 2p+1: d at 18 / 34, qs at 20 / 36
+        const uint32_t q0[4] = {shift2(u[0], u[1]), shift2(u[1], u[2]), shift2(u[2], u[3]), shift2(u[3], u[4])};
+        const uint32_t q1[4] = {u[5], u[6], u[7], u[8]};
+        uint32_t x0[8], x1[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            x0[i] = shift2(v[i], v[i + 1]);
+            x1[i] = v[9 + i];
+        }
+        acc += q4_0_block_dot16(q0, u[0] & 0xffffu, x0, v[0] & 0xffffu);
+        acc += q4_0_block_dot16(q1, u[4] >> 16, x1, v[8] >> 16);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (row < n && lane == 0) c[row] = acc * 0.0625f;
+}
+
 template <int M>
 hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n, int64_t k, hipStream_t stream) {
     const int nb = (int)(k / 32);
@@ -191,7 +248,7 @@ hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n,
 
 bool gemv_supported(int type, int64_t m, int64_t k) {
     if (m < 1 || m > 8) return false;
-    if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return k % 256 == 0;
+    if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return m == 1 ? k % 64 == 0 : k % 256 == 0;
     return false;
 }
 
@@ -199,7 +256,12 @@ hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t
                        hipStream_t stream) {
     if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return hipErrorInvalidValue;
     switch (m) {
-    case 1: return launch_gemv_q4_0_m<1>(w, a, c, n, k, stream);
+    case 1: {
+        const int grid = (int)((n + kThreads / 64 - 1) / (kThreads / 64));
+        hipLaunchKernelGGL(gemv_q4_0_m1_kernel, dim3(grid), dim3(kThreads), 0, stream, static_cast<const uint8_t *>(w),
+                           static_cast<const uint8_t *>(a), c, (int)n, (int)(k / 32));
+        return hipGetLastError();
+    }
     case 2: return launch_gemv_q4_0_m<2>(w, a, c, n, k, stream);
     case 3: return launch_gemv_q4_0_m<3>(w, a, c, n, k, stream);
     case 4: return launch_gemv_q4_0_m<4>(w, a, c, n, k, stream);
