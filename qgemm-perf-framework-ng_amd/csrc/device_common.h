@@ -104,6 +104,27 @@ __device__ __forceinline__ f32x16 mfma_f16_32x32x16(f16x8 a, f16x8 b, f32x16 c) 
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// XCD-aware tile order for a 1-D grid of mt x nt output tiles. Workgroup ids
+// are dealt round-robin to MI355X's 8 XCDs (id % 8), each with its own L2;
+// regroup them so that each XCD owns a contiguous range of tiles, walked
+// m-fastest in groups of kGroupM m-tiles, so the workgroups resident on one XCD
+// at a time share weight and activation tiles in its L2. The map is a bijection
+// on [0, mt*nt): the first 8*q ids are regrouped (q tiles per XCD), the last
+// (mt*nt) % 8 ids keep their own index.
+struct TileOrigin {
+    int mi, ni;  // tile coordinates
+};
+__device__ __forceinline__ TileOrigin xcd_tile(int id, int mt, int nt) {
+    constexpr int kXcds = 8, kGroupM = 8;
+    const int tiles = mt * nt;
+    const int q = tiles / kXcds;
+    const int t = id < q * kXcds ? (id % kXcds) * q + id / kXcds : id;
+    const int gm = mt < kGroupM ? mt : kGroupM;
+    const int group = t / (gm * nt), in = t % (gm * nt);
+    const int gm_here = (mt - group * gm) < gm ? (mt - group * gm) : gm;
+    return {group * gm + in % gm_here, in / gm_here};
+}
+
 // Row of result register r for lane l of a 32x32 MFMA tile.
 __device__ __forceinline__ int mfma_row(int lane, int r) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 

@@ -1,0 +1,501 @@
+// int8-MFMA GEMM for the 256-element super-block formats against q8_K
+// activations: q4_K (llama_reference.cpp:113-132) and iq2_xxs
+// (llama_reference.cpp:148-161 with kernels/common/iq2_xxs.h:29-41).
+//
+// Both formats carry a small integer scale per 32-element sub-block j and an
+// fp16 scale per super-block, so each super-block reduces to exact int32 sums
+// before any floating-point work:
+//   q4_K:    IS = sum_j sc_j * S_j,  IM = sum_j m_j * (bsum_2j + bsum_2j+1)
+//            C += ad * (d * IS - dmin * IM)
+//   iq2_xxs: IS = sum_j (2 s_j + 1) * S_j
+//            C += (0.125 * d * ad) * IS
+// with S_j the int8 dot of sub-block j.
+//
+// A K stage is half a super-block (4 sub-blocks, 128 elements). Per stage the
+// workgroup stages into LDS:
+//   * activation int8 rows as they are, the q8_K scale and (q4_K) the eight
+//     16-element bsums of the half as fp16 (|bsum| <= 2032 is exact in fp16);
+//   * weight values expanded to one int8 per element (q4_K nibble 0..15,
+//     iq2_xxs signed grid value), the sub-block scales and the fp16 scales.
+// q4_K: sc (0..63) = 8*h + l with octal digits h, l. Two int8 weight planes
+// q*l and q*h (both <= 105) are formed per fragment with one packed 16-bit
+// multiply per dword (the byte products cannot carry), and two int8 MFMAs per
+// sub-block accumulate S_L and S_H over the whole super-block, so IS = 8*S_H +
+// S_L with no per-sub-block VALU work. IM is one fp16 MFMA per stage over the
+// bsums and the mins (exact: every product and partial sum is an integer below
+// 2^24).
+// iq2_xxs: the scale times a grid value does not fit int8 in two digits, so
+// S_j comes from one int8 MFMA and IS += S_j * (2 s_j + 1) is an exact 24-bit
+// multiply-add per result.
+// A diagnostic instantiation writes the int32 super-block sums instead of C.
+#include "device_common.h"
+#include "kernels.h"
+#include "pfng_iq2xxs_grid.h"
+
+namespace pfng {
+
+namespace {
+
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+__constant__ uint16_t kIq2GridCodes[256] = PFNG_IQ2XXS_GRID_CODES_INIT;
+
+enum class Kq { Q4K, IQ2 };
+
+template <Kq T, int BM, int BN, int WM, int WN>
+struct KqConfig {
+    static constexpr Kq kType = T;
+    static constexpr bool kQ4K = T == Kq::Q4K;
+    static constexpr int kBM = BM, kBN = BN, kWM = WM, kWN = WN;
+    static constexpr int kThreads = 64 * WM * WN;
+    static constexpr int TM = BM / WM / 32;  // 32x32 tiles per wave along m
+    static constexpr int TN = BN / WN / 32;  // along n
+    static constexpr int kSub = 4;                    // sub-blocks per stage
+    static constexpr int kRowStride = kSub * 32 + 16;  // LDS bytes per int8 row (+ pad against bank conflicts)
+    // LDS layout of one stage buffer
+    static constexpr int kAq = 0;                                   // int8 [BM][kRowStride]
+    static constexpr int kAd = kAq + BM * kRowStride;               // fp32 [BM] activation scale
+    static constexpr int kAb = kAd + BM * 4;                        // q4_K: fp16 [BM][8] bsums of the half
+    static constexpr int kWq = kAb + (kQ4K ? BM * 16 : 0);          // int8 [BN][kRowStride]
+    static constexpr int kWs = kWq + BN * kRowStride;               // q4_K: u32 [BN][4][2] digit pairs; iq2: i32 [BN][4]
+    static constexpr int kWd = kWs + BN * (kQ4K ? 32 : 16);         // fp32 [BN] d (iq2: 0.125 * d)
+    static constexpr int kWdm = kWd + BN * 4;                       // q4_K: fp32 [BN] dmin
+    static constexpr int kWmin = kWdm + (kQ4K ? BN * 4 : 0);        // q4_K: fp16 [BN][8] mins, each twice
+    static constexpr int kBufBytes = kWmin + (kQ4K ? BN * 16 : 0);
+    static constexpr int kGrid = 2 * kBufBytes;                      // iq2: 256 x 8-byte grid magnitudes
+    static constexpr int kLdsBytes = kGrid + (kQ4K ? 0 : 256 * 8);
+    // global -> register tasks per stage: activation rows in halves of 64
+    // bytes, weight rows per sub-block
+    static constexpr int kActPT = BM * 2 / kThreads;
+    static constexpr int kWPT = BN * kSub / kThreads;
+    static_assert(TM >= 1 && TN >= 1, "tile too small");
+    static_assert(kActPT * kThreads == BM * 2 && kWPT * kThreads == BN * kSub, "tasks must split evenly");
+    static_assert(kActPT >= 1 && kWPT >= 1, "every thread takes at least one task of each operand");
+    static_assert(kAd % 16 == 0 && kAb % 16 == 0 && kWq % 16 == 0 && kWs % 16 == 0 && kWd % 16 == 0 &&
+                      kWdm % 16 == 0 && kWmin % 16 == 0 && kBufBytes % 16 == 0,
+                  "LDS regions 16-byte aligned");
+};
+
+template <class C>
+struct KqRegs {
+    uint32_t aq[C::kActPT][16];  // 64 activation bytes
+    uint32_t ab[C::kActPT][2];   // 4 bsums (q4_K)
+    float ad[C::kActPT];
+    // q4_K: 16 nibble bytes + the 16-byte header (d, dmin, scales)
+    // iq2_xxs: the 8 bytes of one sub-block + d
+    uint32_t wq[C::kWPT][C::kQ4K ? 4 : 2];
+    uint32_t wh[C::kWPT][C::kQ4K ? 4 : 1];
+};
+
+constexpr int kQ8KBytes = 292, kQ4KBytes = 144, kIq2Bytes = 66;
+
+// Loads of stage (b, h): super-block b, half h. Rows are clamped at the matrix
+// edge so that every load is unconditional and in bounds.
+template <class C>
+__device__ __forceinline__ void kq_load(const uint8_t *__restrict__ a, const uint8_t *__restrict__ w, int m, int n,
+                                        int nb, int m0, int n0, int b, int h, KqRegs<C> &r) {
+#pragma unroll
+    for (int it = 0; it < C::kActPT; ++it) {
+        const int task = threadIdx.x + it * C::kThreads;
+        const int row = m0 + task / 2, e = task % 2;
+        const int lrow = row < m ? row : m - 1;
+        const uint8_t *blk = a + ((size_t)lrow * nb + b) * kQ8KBytes;
+        const uint32_t *qs = reinterpret_cast<const uint32_t *>(blk + 4 + 128 * h + 64 * e);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) r.aq[it][i] = qs[i];
+        const uint32_t *bs = reinterpret_cast<const uint32_t *>(blk + 260 + 16 * h + 8 * e);
+        if constexpr (C::kQ4K) {
+            r.ab[it][0] = bs[0];
+            r.ab[it][1] = bs[1];
+        }
+        r.ad[it] = *reinterpret_cast<const float *>(blk);
+    }
+#pragma unroll
+    for (int it = 0; it < C::kWPT; ++it) {
+        const int task = threadIdx.x + it * C::kThreads;
+        const int row = n0 + task / C::kSub, e = task % C::kSub;
+        const int lrow = row < n ? row : n - 1;
+        if constexpr (C::kQ4K) {
+            const uint8_t *blk = w + ((size_t)lrow * nb + b) * kQ4KBytes;
+            const uint32_t *qs = reinterpret_cast<const uint32_t *>(blk + 16 + 64 * h + 16 * e);
+            const uint32_t *hd = reinterpret_cast<const uint32_t *>(blk);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                r.wq[it][i] = qs[i];
+                r.wh[it][i] = hd[i];
+            }
+        } else {
+            // 66-byte blocks are only 2-byte aligned: read the covering dwords
+            // and a trailing half-word, never past the sub-block's last byte
+            const size_t base = ((size_t)lrow * nb + b) * kIq2Bytes;
+            const size_t o = base + 2 + 32 * h + 8 * e;
+            const uint32_t *p4 = reinterpret_cast<const uint32_t *>(w + (o & ~(size_t)3));
+            const uint32_t d0 = p4[0], d1 = p4[1];
+            const uint32_t tail = *reinterpret_cast<const uint16_t *>(w + o + 6);
+            const uint32_t sh = (uint32_t)(o & 3) * 8;  // 0 or 16 bits
+            r.wq[it][0] = sh ? __builtin_amdgcn_alignbyte(d1, d0, 2) : d0;
+            r.wq[it][1] = sh ? ((d1 >> 16) | (tail << 16)) : d1;
+            r.wh[it][0] = *reinterpret_cast<const uint16_t *>(w + base);
+        }
+    }
+}
+
+// q4_K scale and min of sub-block j (0..7) from the 12 packed bytes, with the
+// reference's decode (llama_reference.cpp:116-121).
+__device__ __forceinline__ void q4_K_scale_min(const uint32_t hd[4], int j, uint32_t &sc, uint32_t &mn) {
+    auto byte = [&](int i) { return (hd[1 + i / 4] >> (8 * (i % 4))) & 0xffu; };
+    if (j < 4) {
+        sc = byte(j) & 63;
+        mn = byte(j + 4) & 63;
+    } else {
+        sc = (byte(j + 4) & 15) | ((byte(j - 4) >> 6) << 4);
+        mn = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+    }
+}
+
+template <class C>
+__device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int h, const KqRegs<C> &r) {
+#pragma unroll
+    for (int it = 0; it < C::kActPT; ++it) {
+        const int task = threadIdx.x + it * C::kThreads;
+        const int row = task / 2, e = task % 2;
+        const uint32_t *v = r.aq[it];
+        uint4 *dst = reinterpret_cast<uint4 *>(lds + C::kAq + row * C::kRowStride + 64 * e);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i] = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+        *reinterpret_cast<float *>(lds + C::kAd + row * 4) = r.ad[it];  // both halves write the same value
+        if constexpr (C::kQ4K) {
+            uint32_t hb[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const _Float16 lo = (_Float16)(float)(int16_t)(r.ab[it][i] & 0xffffu);
+                const _Float16 hi = (_Float16)(float)(int16_t)(r.ab[it][i] >> 16);
+                hb[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+            }
+            *reinterpret_cast<uint2 *>(lds + C::kAb + row * 16 + 8 * e) = make_uint2(hb[0], hb[1]);
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < C::kWPT; ++it) {
+        const int task = threadIdx.x + it * C::kThreads;
+        const int row = task / C::kSub, e = task % C::kSub;
+        uint8_t *wrow = lds + C::kWq + row * C::kRowStride;
+        if constexpr (C::kQ4K) {
+            // bytes 16e..16e+15 of the half's 64 nibble bytes: pair p = e/2
+            // holds local sub-block 2p (low nibbles) and 2p+1 (high nibbles),
+            // elements 16*(e%2) .. +15
+            const int p = e / 2, i0 = 16 * (e % 2);
+            uint32_t lo[4], hi[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                lo[i] = r.wq[it][i] & 0x0f0f0f0fu;
+                hi[i] = (r.wq[it][i] >> 4) & 0x0f0f0f0fu;
+            }
+            *reinterpret_cast<uint4 *>(wrow + (2 * p) * 32 + i0) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            *reinterpret_cast<uint4 *>(wrow + (2 * p + 1) * 32 + i0) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            // scale digits and min of local sub-block e
+            uint32_t sc, mn;
+            q4_K_scale_min(r.wh[it], 4 * h + e, sc, mn);
+            const uint32_t l = sc & 7u, hh = sc >> 3;
+            *reinterpret_cast<uint2 *>(lds + C::kWs + row * 32 + 8 * e) = make_uint2(l * 0x10001u, hh * 0x10001u);
+            const uint32_t mh = __builtin_bit_cast(uint16_t, (_Float16)(float)mn);
+            *reinterpret_cast<uint32_t *>(lds + C::kWmin + row * 16 + 4 * e) = mh | (mh << 16);
+            *reinterpret_cast<float *>(lds + C::kWd + row * 4) = fp16_to_f32(r.wh[it][0] & 0xffffu);
+            *reinterpret_cast<float *>(lds + C::kWdm + row * 4) = fp16_to_f32(r.wh[it][0] >> 16);
+        } else {
+            // iq2_xxs sub-block (kernels/common/iq2_xxs.h:29-41): four groups of
+            // 8 values, magnitudes from the grid, sign bit j of group g is bit
+            // j of (idx | parity(idx) << 7) with idx the 7-bit field g of the
+            // last dword, scale 2 * (bits 28..31) + 1
+            const uint32_t gidx = r.wq[it][0], ss = r.wq[it][1];
+            uint32_t out[8];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint2 mag = *reinterpret_cast<const uint2 *>(grid + ((gidx >> (8 * g)) & 0xffu) * 8);
+                const uint32_t idx = (ss >> (7 * g)) & 0x7fu;
+                const uint32_t sgn = idx | ((__builtin_popcount(idx) & 1u) << 7);
+                // spread sign bits 0..3 / 4..7 to the low bit of each byte
+                const uint32_t b0 = ((sgn & 0xfu) * 0x00204081u) & 0x01010101u;
+                const uint32_t b1 = (((sgn >> 4) & 0xfu) * 0x00204081u) & 0x01010101u;
+                // magnitudes are >= 8, so (x ^ 0xff) + 1 negates a byte without
+                // a carry into its neighbour
+                out[2 * g] = (mag.x ^ (b0 * 0xffu)) + b0;
+                out[2 * g + 1] = (mag.y ^ (b1 * 0xffu)) + b1;
+            }
+            uint4 *dst = reinterpret_cast<uint4 *>(wrow + 32 * e);
+            dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
+            dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
+            *reinterpret_cast<int32_t *>(lds + C::kWs + row * 16 + 4 * e) = 2 * (int32_t)(ss >> 28) + 1;
+            *reinterpret_cast<float *>(lds + C::kWd + row * 4) = 0.125f * fp16_to_f32(r.wh[it][0]);
+        }
+    }
+}
+
+// Per-wave accumulators.
+template <class C>
+struct KqAcc {
+    f32x16 acc[C::TM][C::TN];  // fp32 output
+    i32x16 s0[C::TM][C::TN];   // q4_K: S_L; iq2_xxs: IS
+    i32x16 s1[C::TM][C::TN];   // q4_K: S_H
+    f32x16 im[C::TM][C::TN];   // q4_K: IM (exact integers)
+};
+
+__device__ __forceinline__ i32x4 mul_planes(i32x4 v, uint32_t digit2) {
+    i32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const u16x2 x = __builtin_bit_cast(u16x2, (uint32_t)v[i]) * __builtin_bit_cast(u16x2, digit2);
+        o[i] = (int32_t)__builtin_bit_cast(uint32_t, x);
+    }
+    return o;
+}
+
+// Sub-block sums of one stage (half h of the super-block).
+template <class C, int H>
+__device__ __forceinline__ void kq_compute(const uint8_t *buf, KqAcc<C> &A, int lane, int wave_m, int wave_n) {
+    const int li = lane & 31, lh = lane >> 5;
+    const uint8_t *aq = buf + C::kAq + (wave_m * C::TM * 32 + li) * C::kRowStride + lh * 16;
+    const uint8_t *wq = buf + C::kWq + (wave_n * C::TN * 32 + li) * C::kRowStride + lh * 16;
+    const int wrow = wave_n * C::TN * 32 + li;
+    if constexpr (C::kQ4K) {
+        uint4 dg[C::TN][2];  // digit pairs of the 4 sub-blocks: (l, h) per sub-block
+#pragma unroll
+        for (int tn = 0; tn < C::TN; ++tn) {
+            const uint4 *s = reinterpret_cast<const uint4 *>(buf + C::kWs + (wrow + tn * 32) * 32);
+            dg[tn][0] = s[0];
+            dg[tn][1] = s[1];
+        }
+#pragma unroll
+        for (int t = 0; t < C::kSub; ++t) {
+            i32x4 av[C::TM], vl[C::TN], vh[C::TN];
+#pragma unroll
+            for (int tm = 0; tm < C::TM; ++tm)
+                av[tm] = *reinterpret_cast<const i32x4 *>(aq + tm * 32 * C::kRowStride + t * 32);
+#pragma unroll
+            for (int tn = 0; tn < C::TN; ++tn) {
+                const i32x4 v = *reinterpret_cast<const i32x4 *>(wq + tn * 32 * C::kRowStride + t * 32);
+                const uint4 &d = dg[tn][t / 2];
+                const uint32_t dl = (t % 2) ? d.z : d.x, dh = (t % 2) ? d.w : d.y;
+                vl[tn] = mul_planes(v, dl);
+                vh[tn] = mul_planes(v, dh);
+            }
+#pragma unroll
+            for (int tm = 0; tm < C::TM; ++tm)
+#pragma unroll
+                for (int tn = 0; tn < C::TN; ++tn) {
+                    const bool first = H == 0 && t == 0;
+                    A.s0[tm][tn] = mfma_i8_32x32x32(av[tm], vl[tn], first ? (i32x16){} : A.s0[tm][tn]);
+                    A.s1[tm][tn] = mfma_i8_32x32x32(av[tm], vh[tn], first ? (i32x16){} : A.s1[tm][tn]);
+                }
+        }
+        // IM over the half's 8 bsums: lane supplies row li, k = 4*lh .. 4*lh+3
+        f16x4 ab[C::TM], wm[C::TN];
+#pragma unroll
+        for (int tm = 0; tm < C::TM; ++tm)
+            ab[tm] = *reinterpret_cast<const f16x4 *>(buf + C::kAb + (wave_m * C::TM * 32 + tm * 32 + li) * 16 + lh * 8);
+#pragma unroll
+        for (int tn = 0; tn < C::TN; ++tn)
+            wm[tn] = *reinterpret_cast<const f16x4 *>(buf + C::kWmin + (wrow + tn * 32) * 16 + lh * 8);
+#pragma unroll
+        for (int tm = 0; tm < C::TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < C::TN; ++tn)
+                A.im[tm][tn] = mfma_f16_32x32x8(ab[tm], wm[tn], H == 0 ? (f32x16){} : A.im[tm][tn]);
+    } else {
+        int4 sc[C::TN];
+#pragma unroll
+        for (int tn = 0; tn < C::TN; ++tn) sc[tn] = *reinterpret_cast<const int4 *>(buf + C::kWs + (wrow + tn * 32) * 16);
+#pragma unroll
+        for (int t = 0; t < C::kSub; ++t) {
+            i32x4 av[C::TM], wv[C::TN];
+#pragma unroll
+            for (int tm = 0; tm < C::TM; ++tm)
+                av[tm] = *reinterpret_cast<const i32x4 *>(aq + tm * 32 * C::kRowStride + t * 32);
+#pragma unroll
+            for (int tn = 0; tn < C::TN; ++tn)
+                wv[tn] = *reinterpret_cast<const i32x4 *>(wq + tn * 32 * C::kRowStride + t * 32);
+#pragma unroll
+            for (int tm = 0; tm < C::TM; ++tm)
+#pragma unroll
+                for (int tn = 0; tn < C::TN; ++tn) {
+                    const i32x16 s = mfma_i8_32x32x32(av[tm], wv[tn], (i32x16){});
+                    const int scale = t == 0 ? sc[tn].x : t == 1 ? sc[tn].y : t == 2 ? sc[tn].z : sc[tn].w;
+#pragma unroll
+                    for (int q = 0; q < 16; ++q)
+                        A.s0[tm][tn][q] = (H == 0 && t == 0) ? __mul24(s[q], scale)
+                                                             : __mul24(s[q], scale) + A.s0[tm][tn][q];
+                }
+        }
+    }
+}
+
+// End of super-block b: fold the exact sums into C (or write them out).
+template <class C, bool kIsums>
+__device__ __forceinline__ void kq_epilogue(const uint8_t *buf, KqAcc<C> &A, int32_t *isums, int m, int n, int nb,
+                                            int m0, int n0, int b, int lane, int wave_m, int wave_n) {
+    const int li = lane & 31, lh = lane >> 5;
+    if constexpr (kIsums) {
+#pragma unroll
+        for (int tm = 0; tm < C::TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < C::TN; ++tn) {
+                const int col = n0 + wave_n * C::TN * 32 + tn * 32 + li;
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const int row = m0 + wave_m * C::TM * 32 + tm * 32 + mfma_row(lane, q);
+                    if (row < m && col < n) {
+                        const size_t o = ((size_t)row * n + col) * nb + b;
+                        if constexpr (C::kQ4K) {
+                            isums[2 * o] = 8 * A.s1[tm][tn][q] + A.s0[tm][tn][q];
+                            isums[2 * o + 1] = (int32_t)A.im[tm][tn][q];
+                        } else {
+                            isums[o] = A.s0[tm][tn][q];
+                        }
+                    }
+                }
+            }
+    } else {
+#pragma unroll
+        for (int tm = 0; tm < C::TM; ++tm) {
+            // activation scales of the lane's 16 rows: rows 8g + 4lh + 0..3
+            const float *adp = reinterpret_cast<const float *>(buf + C::kAd) + wave_m * C::TM * 32 + tm * 32 + 4 * lh;
+            f32x4 ad4[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) ad4[g] = *reinterpret_cast<const f32x4 *>(adp + 8 * g);
+#pragma unroll
+            for (int tn = 0; tn < C::TN; ++tn) {
+                const int wr = wave_n * C::TN * 32 + tn * 32 + li;
+                const float d = reinterpret_cast<const float *>(buf + C::kWd)[wr];
+                if constexpr (C::kQ4K) {
+                    const float dmin = reinterpret_cast<const float *>(buf + C::kWdm)[wr];
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) {
+                        const int is = 8 * A.s1[tm][tn][q] + A.s0[tm][tn][q];
+                        const float x = fmaf(-dmin, A.im[tm][tn][q], d * (float)is);
+                        A.acc[tm][tn][q] = fmaf(ad4[q / 4][q % 4], x, A.acc[tm][tn][q]);
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 16; ++q)
+                        A.acc[tm][tn][q] = fmaf(d * ad4[q / 4][q % 4], (float)A.s0[tm][tn][q], A.acc[tm][tn][q]);
+                }
+            }
+        }
+    }
+}
+
+template <class C, bool kIsums>
+__global__ __launch_bounds__(C::kThreads, 2) void gemm_kq_kernel(const uint8_t *__restrict__ w,
+                                                                 const uint8_t *__restrict__ a, float *__restrict__ c,
+                                                                 int32_t *__restrict__ isums, int m, int n, int nb) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wave_m = wave / C::kWN;
+    const int wave_n = wave % C::kWN;
+    const TileOrigin to = xcd_tile(blockIdx.x, (m + C::kBM - 1) / C::kBM, (n + C::kBN - 1) / C::kBN);
+    const int m0 = to.mi * C::kBM, n0 = to.ni * C::kBN;
+    uint8_t *grid = lds + C::kGrid;
+    if constexpr (!C::kQ4K) {
+        // grid magnitudes (kernels/iq2_xxs-q8_K-RVV-common/ggml_min.h:69-134):
+        // two bits per byte select 8, 25 or 43
+        for (int e = threadIdx.x; e < 256; e += C::kThreads) {
+            const uint32_t code = kIq2GridCodes[e];
+            uint32_t v[2] = {0, 0};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t c2 = (code >> (2 * j)) & 3u;
+                const uint32_t mag = c2 == 0 ? 8u : (c2 == 1 ? 25u : 43u);
+                v[j / 4] |= mag << (8 * (j % 4));
+            }
+            *reinterpret_cast<uint2 *>(grid + 8 * e) = make_uint2(v[0], v[1]);
+        }
+        __syncthreads();
+    }
+
+    KqAcc<C> A;
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) A.acc[i][j] = (f32x16){};
+
+    // Double-buffered LDS with one barrier per stage. Stage 2b+h is computed
+    // from buffer h while the registers of the next stage are stored into the
+    // other buffer and the loads of the stage after it are issued. Stores and
+    // loads are unconditional (the stage index is clamped at the end).
+    KqRegs<C> regs;
+    kq_load<C>(a, w, m, n, nb, m0, n0, 0, 0, regs);
+    kq_store<C>(lds, grid, 0, regs);
+    kq_load<C>(a, w, m, n, nb, m0, n0, 0, 1, regs);
+    __syncthreads();
+    for (int b = 0; b < nb; ++b) {
+        const int bn = b + 1 < nb ? b + 1 : nb - 1;
+        __builtin_amdgcn_sched_barrier(0);
+        kq_compute<C, 0>(lds, A, lane, wave_m, wave_n);
+        __builtin_amdgcn_sched_barrier(0);
+        kq_store<C>(lds + C::kBufBytes, grid, 1, regs);
+        __builtin_amdgcn_sched_barrier(0);
+        kq_load<C>(a, w, m, n, nb, m0, n0, bn, 0, regs);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        kq_compute<C, 1>(lds + C::kBufBytes, A, lane, wave_m, wave_n);
+        kq_epilogue<C, kIsums>(lds + C::kBufBytes, A, isums, m, n, nb, m0, n0, b, lane, wave_m, wave_n);
+        __builtin_amdgcn_sched_barrier(0);
+        kq_store<C>(lds, grid, 0, regs);
+        __builtin_amdgcn_sched_barrier(0);
+        kq_load<C>(a, w, m, n, nb, m0, n0, bn, 1, regs);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+    }
+
+    if constexpr (!kIsums) {
+        const int li = lane & 31;
+#pragma unroll
+        for (int tm = 0; tm < C::TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < C::TN; ++tn) {
+                const int col = n0 + wave_n * C::TN * 32 + tn * 32 + li;
+                if (col < n) {
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) {
+                        const int row = m0 + wave_m * C::TM * 32 + tm * 32 + mfma_row(lane, q);
+                        if (row < m) c[(size_t)row * n + col] = A.acc[tm][tn][q];
+                    }
+                }
+            }
+    }
+}
+
+template <class C, bool kIsums>
+hipError_t launch_kq(const void *w, const void *a, float *c, int32_t *isums, int64_t m, int64_t n, int64_t k,
+                     hipStream_t stream) {
+    const dim3 grid((unsigned)(((n + C::kBN - 1) / C::kBN) * ((m + C::kBM - 1) / C::kBM)));
+    hipLaunchKernelGGL((gemm_kq_kernel<C, kIsums>), grid, dim3(C::kThreads), C::kLdsBytes, stream,
+                       static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(a), c, isums, (int)m, (int)n,
+                       (int)(k / 256));
+    return hipGetLastError();
+}
+
+// 128 x 64 tiles, 4 waves of 64 x 32
+using Q4KTile = KqConfig<Kq::Q4K, 128, 64, 2, 2>;
+using Iq2Tile = KqConfig<Kq::IQ2, 128, 64, 2, 2>;
+
+}  // namespace
+
+hipError_t launch_kquant_mul_mat(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
+                                 hipStream_t stream) {
+    if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K) return launch_kq<Q4KTile, false>(w, a, c, nullptr, m, n, k, stream);
+    if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K)
+        return launch_kq<Iq2Tile, false>(w, a, c, nullptr, m, n, k, stream);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_kquant_block_isums(int type, const void *w, const void *a, int32_t *out, int64_t m, int64_t n,
+                                     int64_t k, hipStream_t stream) {
+    if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K) return launch_kq<Q4KTile, true>(w, a, nullptr, out, m, n, k, stream);
+    if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K)
+        return launch_kq<Iq2Tile, true>(w, a, nullptr, out, m, n, k, stream);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace pfng

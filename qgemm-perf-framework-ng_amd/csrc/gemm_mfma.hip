@@ -28,9 +28,6 @@ namespace pfng {
 
 namespace {
 
-constexpr int kXcds = 8;    // MI355X: 8 XCDs, each with its own L2
-constexpr int kGroupM = 8;  // m-tiles walked together inside an XCD's tile range
-
 template <int BM, int BN, int WM, int WN, int KB, int RING = 2, int MINW = 2>
 struct Q40Config {
     static constexpr int kBM = BM, kBN = BN, kWM = WM, kWN = WN, kKB = KB;
@@ -236,22 +233,8 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWavesPerEU) void gemm_q4_0_kern
     const int wave = threadIdx.x >> 6;
     const int wave_m = wave / C::kWN;
     const int wave_n = wave % C::kWN;
-    // XCD-aware tile order. Workgroup ids are dealt round-robin to the 8 XCDs
-    // (id % 8); regroup them so that each XCD owns a contiguous range of tiles,
-    // walked m-fastest in groups of kGroupM m-tiles, so the workgroups resident
-    // on one XCD at a time share weight and activation tiles in its L2.
-    const int mt = (m + C::kBM - 1) / C::kBM, nt = (n + C::kBN - 1) / C::kBN;
-    const int tiles = mt * nt;
-    const int id = blockIdx.x;
-    // bijection on [0, tiles): the first 8*q ids are regrouped (q tiles per
-    // XCD), the last tiles % 8 ids keep their own index
-    const int q = tiles / kXcds;
-    const int t = id < q * kXcds ? (id % kXcds) * q + id / kXcds : id;
-    const int gm = mt < kGroupM ? mt : kGroupM;
-    const int group = t / (gm * nt), in = t % (gm * nt);
-    const int gm_here = (mt - group * gm) < gm ? (mt - group * gm) : gm;
-    const int m0 = (group * gm + in % gm_here) * C::kBM;
-    const int n0 = (in / gm_here) * C::kBN;
+    const TileOrigin to = xcd_tile(blockIdx.x, (m + C::kBM - 1) / C::kBM, (n + C::kBN - 1) / C::kBN);
+    const int m0 = to.mi * C::kBM, n0 = to.ni * C::kBN;
     const int li = lane & 31;  // operand row / result column within a 32x32 tile
 
     f32x16 acc[C::TM][C::TN];
@@ -330,12 +313,13 @@ using Q40Small4 = Q40Config<64, 64, 1, 2, 4, 1>;
 bool mfma_supported(int type, int64_t m, int64_t k) {
     (void)m;
     if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return k % (32 * 4) == 0;  // Q40Small4 takes any k % 128 == 0
-    return false;
+    // the super-block formats take any k % 256 == 0 (gemm_kquant.hip)
+    return (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K || type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K) && k % 256 == 0;
 }
 
 hipError_t launch_mfma_mul_mat(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                                hipStream_t stream) {
-    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return hipErrorInvalidValue;
+    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return launch_kquant_mul_mat(type, w, a, c, m, n, k, stream);
     const int64_t big_tiles = ((m + 127) / 128) * ((n + 127) / 128);
     // a two-slot ring needs an even number of K stages
     if (big_tiles >= 512 && k % (Q40Big::kRing * 32 * Q40Big::kKB) == 0)
@@ -347,7 +331,7 @@ hipError_t launch_mfma_mul_mat(int type, const void *w, const void *a, float *c,
 
 hipError_t launch_mfma_block_isums(int type, const void *w, const void *a, int32_t *out, int64_t m, int64_t n,
                                    int64_t k, hipStream_t stream) {
-    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return hipErrorInvalidValue;
+    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return launch_kquant_block_isums(type, w, a, out, m, n, k, stream);
     return launch_q4_0<Q40Small4, true>(w, a, nullptr, out, m, n, k, stream);
 }
 

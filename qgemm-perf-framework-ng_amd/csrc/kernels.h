@@ -27,4 +27,10 @@ hipError_t launch_mfma_mul_mat(int type, const void *w, const void *a, float *c,
 hipError_t launch_mfma_block_isums(int type, const void *w, const void *a, int32_t *out, int64_t m, int64_t n,
                                    int64_t k, hipStream_t stream);
 
+// gemm_kquant.hip — q4_K and iq2_xxs against q8_K
+hipError_t launch_kquant_mul_mat(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
+                                 hipStream_t stream);
+hipError_t launch_kquant_block_isums(int type, const void *w, const void *a, int32_t *out, int64_t m, int64_t n,
+                                     int64_t k, hipStream_t stream);
+
 }  // namespace pfng

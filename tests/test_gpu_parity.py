@@ -205,3 +205,99 @@ def test_config4_prefill_full_size_sampled(hip, torch_gpu, oracle):
     got_p = hip.mul_mat(0, wt, aq_t[perm].contiguous(), m, n, k)
     torch.cuda.synchronize()
     assert torch.equal(got_p, got[perm])
+
+
+# ------------------------------------------------- q4_K / iq2_xxs MFMA ----
+
+def random_weight_blocks(oracle, qtype, n, k, seed):
+    """Weights with uniformly random bytes (every 6-bit scale and min, every
+    grid index, sign index and scale nibble) and sane fp16 super-block scales."""
+    rng = np.random.default_rng(seed)
+    dt = oracle.WEIGHT_DTYPE[qtype]
+    nb = k // oracle.QK[qtype]
+    raw = rng.integers(0, 256, n * nb * dt.itemsize, dtype=np.uint8)
+    w = raw.view(dt).reshape(n, nb).copy()
+    w["d"] = oracle.fp32_to_fp16(rng.uniform(1e-3, 1e-2, (n, nb)).astype(np.float32))
+    if qtype == oracle.Q4_K:
+        w["dmin"] = oracle.fp32_to_fp16(rng.uniform(1e-3, 1e-2, (n, nb)).astype(np.float32))
+    return w
+
+
+def extreme_activation(oracle, m, k, seed):
+    """q8_K rows at the int8 limits: every value +-127 (bsums +-2032)."""
+    rng = np.random.default_rng(seed)
+    x = np.where(rng.random((m, k)) < 0.5, -1.0, 1.0).astype(np.float32)
+    return oracle.quantize_q8_K(x)
+
+
+@pytest.mark.parametrize("qtype", [1, 2])
+@pytest.mark.parametrize("m,n,k", [(32, 64, 256), (100, 77, 512), (1, 1, 256), (130, 65, 768), (480, 64, 1536)])
+def test_block_isums_kquant_bit_exact(hip, torch_gpu, oracle, qtype, m, n, k):
+    torch = torch_gpu
+    say(f"block isums type={qtype} {m}x{n}x{k}")
+    act, w = oracle.create_input(qtype, m, n, k, seed=m + 3 * n)
+    aq = oracle.quantize_q8_K(act)
+    got = hip.block_isums(qtype, dev(torch, w), dev(torch, aq), m, n, k)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), oracle.isums(qtype, w, aq, m, n, k))
+
+
+@pytest.mark.parametrize("qtype", [1, 2])
+def test_block_isums_kquant_random_bytes_and_extremes(hip, torch_gpu, oracle, qtype):
+    torch = torch_gpu
+    m, n, k = 96, 130, 1024
+    say(f"block isums random bytes type={qtype} {m}x{n}x{k}")
+    w = random_weight_blocks(oracle, qtype, n, k, seed=17 + qtype)
+    for aq in (oracle.quantize_q8_K(oracle.create_input(qtype, m, 1, k, seed=9)[0]),
+               extreme_activation(oracle, m, k, seed=3)):
+        got = hip.block_isums(qtype, dev(torch, w), dev(torch, aq), m, n, k)
+        torch.cuda.synchronize()
+        assert np.array_equal(got.cpu().numpy(), oracle.isums(qtype, w, aq, m, n, k))
+        out = run_mul_mat(hip, torch, qtype, w, aq, m, n, k, hip.PATH_MFMA)
+        check_close(oracle, qtype, out, w, aq, m, n, k, label=f"random bytes type={qtype}")
+
+
+@pytest.mark.parametrize("qtype", [1, 2])
+@pytest.mark.parametrize("m,n,k", [(32, 64, 256), (100, 77, 512), (1, 300, 768), (9, 1, 256), (257, 129, 1280)])
+def test_mfma_kquant(hip, torch_gpu, oracle, qtype, m, n, k):
+    torch = torch_gpu
+    say(f"mfma type={qtype} {m}x{n}x{k}")
+    act, w = oracle.create_input(qtype, m, n, k, seed=m * 13 + n + qtype)
+    aq = oracle.quantize_q8_K(act)
+    got = run_mul_mat(hip, torch, qtype, w, aq, m, n, k, hip.PATH_MFMA)
+    check_close(oracle, qtype, got, w, aq, m, n, k, label=f"mfma type={qtype} {m}x{n}x{k}")
+
+
+def test_config2_q4_K_full_size(hip, torch_gpu, oracle):
+    """c2: q4_K x q8_K M=480 N=1536 K=1536 through pfng_hip_compute, whole output checked."""
+    torch = torch_gpu
+    m, n, k = 480, 1536, 1536
+    say("c2 q4_K 480x1536x1536")
+    act, w = oracle.create_input(1, m, n, k, seed=1)
+    got = hip.compute(1, dev(torch, act), dev(torch, w), n)
+    torch.cuda.synchronize()
+    aq = oracle.quantize_q8_K(act)
+    check_close(oracle, 1, got.cpu().numpy(), w, aq, m, n, k, label="c2")
+
+
+def test_config3_iq2_xxs_full_size_sampled(hip, torch_gpu, oracle):
+    """c3: iq2_xxs x q8_K M=512 N=4096 K=4096 with the baseline weight generator;
+    oracle on 48 seeded rows, exact block sums on a corner, row-permutation equivariance."""
+    torch = torch_gpu
+    m, n, k = 512, 4096, 4096
+    say("c3 iq2_xxs 512x4096x4096")
+    act, w = oracle.create_input(2, m, n, k, seed=1, variant=1)
+    wt, at = dev(torch, w), dev(torch, act)
+    aq_t = hip.quantize_q8_K(at)
+    got = hip.mul_mat(2, wt, aq_t, m, n, k)
+    torch.cuda.synchronize()
+    aq = oracle.quantize_q8_K(act)
+    assert np.array_equal(aq_t.cpu().numpy().reshape(-1), aq.view(np.uint8).reshape(-1))
+    g = got.cpu().numpy()
+    assert np.isfinite(g).all()
+    rows = np.sort(np.random.default_rng(6).choice(m, 48, replace=False))
+    check_close(oracle, 2, g, w, aq, m, n, k, rows=rows, label="c3")
+    perm = torch.randperm(m, generator=torch.Generator().manual_seed(0)).cuda()
+    got_p = hip.mul_mat(2, wt, aq_t[perm].contiguous(), m, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(got_p, got[perm])
