@@ -3,20 +3,26 @@
 
 Metric (BASELINE.json): "q4_0×q8_0 GEMM TOPS @480×1536×1536; M=1 GEMV GB/s @4096×4096".
 One step = one pass of the hot path over one batch of synthetic input:
-  * value  : config 1 — q4_0 x q8_0 GEMV, M=1 N=4096 K=4096, GB/s of algorithmic
-             bytes (weights + q8_0 activation + fp32 output) per second. The step
-             rotates over 32 weight copies (302 MB > the 256 MB Infinity Cache), so
-             the weights stream from HBM as in decode.
-  * gemm   : config 0 — q4_0 x q8_0 GEMM, M=480 N=1536 K=1536, TOPS = 2*M*N*K/s,
-             the other half of the compound metric.
-Activations are quantized once before the timed region (the reference quantizes
-in prepare(), kernels/*/adapter.cpp); an end-to-end figure that includes the GPU
+  * value   : config 1 — q4_0 x q8_0 GEMV, M=1 N=4096 K=4096, GB/s of algorithmic
+              bytes (weights + q8_0 activation + fp32 output) per second. The step
+              rotates over 32 weight copies (302 MB > the 256 MB Infinity Cache), so
+              the weights stream from HBM as in decode.
+  * gemm    : config 0 — q4_0 x q8_0 GEMM, M=480 N=1536 K=1536, TOPS = 2*M*N*K/s,
+              the other half of the compound metric.
+  * q4_K, iq2_xxs, prefill: configs 2, 3 and 4 in the same form.
+Inputs come from the product's own generator (pfng_host_create_input, the
+reference harness's mt19937 draws and host quantizers). Activations are
+quantized once before the timed region (the reference quantizes in prepare(),
+kernels/*/adapter.cpp); an end-to-end GEMV figure that includes the GPU
 quantizer is reported beside it. Inputs are resident in HBM when timing starts.
 
 Timed region: W warm-up steps, then K steps bracketed by torch.cuda.synchronize().
-Launches are replayed from a captured graph (32 launches per replay) so that
-host launch overhead does not pace the GPU. Kernel time is measured with HIP
-events on the launch stream over the same region.
+Launches are replayed from a captured graph (up to 32 launches per replay) so
+that host launch overhead does not pace the GPU. Kernel time per launch is
+measured with HIP events on the launch stream over the same region.
+Every measured configuration is verified with the reference harness's
+criterion (benchmark.cpp:144-156) against the device naive path, which
+reproduces llama_reference::compute bit for bit.
 
 cpu_baseline: the reference's own llama_reference::compute (oracle/_ref, built
 from /root/reference sources) timed on this host, one thread, on a bounded
@@ -29,6 +35,8 @@ import json
 import os
 import sys
 import time
+
+import numpy as np
 
 REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, REPO)
@@ -53,6 +61,22 @@ def load_package():
     sys.modules[name] = mod
     spec.loader.exec_module(mod)
     return mod
+
+
+def traffic_for(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` from the committed
+    rocprofv3 --pmc summary (profiles/traffic.json, FETCH_SIZE + WRITE_SIZE
+    scaled by a copy-kernel calibration), or None when it was not measured."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            table = json.load(f)
+    except (OSError, ValueError):
+        return None
+    for entry in table.get("entries", []):
+        if kernel.startswith(entry.get("kernel", "\0")) and workload.startswith(entry.get("workload", "\0")):
+            return entry.get("hbm_bytes_per_launch")
+    return None
 
 
 def gemv_bytes(m, n, k):
@@ -145,12 +169,65 @@ def cpu_baseline(budget_s):
     }
 
 
+def upload_weights(torch, w_bytes):
+    return torch.from_numpy(np.ascontiguousarray(w_bytes)).cuda()
+
+
+def verify_against_naive(torch, pkg, qtype, w_t, aq_t, m, n, k, got, rows=None):
+    """The reference harness's criterion (benchmark.cpp:144-156): an element fails
+    when both |err| and |err|/|expected| exceed 1e-3. The expected output is the
+    device naive path, which evaluates llama_reference::compute's dot products in
+    their exact fp32 order. `rows` restricts the check to a row sample."""
+    if rows is not None:
+        aq_t = aq_t[rows].contiguous()
+        got = got[rows]
+        m = len(rows)
+    ref = pkg.mul_mat(qtype, w_t, aq_t, m, n, k, path=pkg.PATH_NAIVE)
+    torch.cuda.synchronize()
+    err = (got.double() - ref.double()).abs()
+    rel = err / ref.double().abs().clamp_min(1e-6)
+    bad = ((err > 1e-3) & (rel > 1e-3)) | ~torch.isfinite(got)
+    return {"passed": bool(bad.sum().item() == 0), "error_elements": int(bad.sum().item()),
+            "compared_elements": int(got.numel()), "max_abs": float(err.max().item()),
+            "max_rel": float(rel.max().item())}
+
+
+def gemm_item(torch, pkg, label, qtype, m, n, k, steps, warmup, variant, kernel, rows_to_verify=None):
+    """One GEMM configuration: TOPS over `steps` graph-replayed launches."""
+    act, w = pkg.create_input(qtype, m, n, k, seed=1, variant=variant)
+    w_t = upload_weights(torch, w)
+    aq_t = pkg.quantize_activation(qtype, torch.from_numpy(act).cuda())
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    per_replay = min(32, max(1, steps))
+    g = capture(torch, lambda i: pkg.mul_mat(qtype, w_t, aq_t, m, n, k, out=out), per_replay)
+    wall, ev, steps_run = time_graph(torch, g, per_replay, steps, warmup)
+    ops = 2.0 * m * n * k
+    k_us = ev * 1e3 / steps_run
+    rows = None
+    if rows_to_verify is not None and rows_to_verify < m:
+        rows = torch.from_numpy(np.sort(np.random.default_rng(4).choice(m, rows_to_verify, replace=False))).cuda()
+    ver = verify_against_naive(torch, pkg, qtype, w_t, aq_t, m, n, k, out, rows)
+    achieved = ops / (k_us * 1e-6) / 1e12
+    item = {"workload": label, "value": round(ops * steps_run / wall / 1e12, 3), "unit": "TOPS", "steps": steps_run,
+            "ms_per_step": round(wall * 1e3 / steps_run, 6), "verify": ver,
+            "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                         "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": traffic_for(kernel, label),
+                         "kernel": kernel, "kernel_us": round(k_us, 3)}}
+    log(f"[bench] {label}: {steps_run} steps, {item['value']} TOPS wall, kernel {k_us:.2f} us -> {achieved:.1f} TOPS, "
+        f"verify={ver['passed']} (max_abs {ver['max_abs']:.3g})")
+    del w_t, aq_t, out, g
+    torch.cuda.empty_cache()
+    return item
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=6400, help="timed GEMV steps (rounded up to a multiple of 32)")
     ap.add_argument("--warmup", type=int, default=640)
-    ap.add_argument("--gemm-steps", type=int, default=2048)
+    ap.add_argument("--gemm-steps", type=int, default=2048, help="timed steps of the c0/c2 GEMMs")
+    ap.add_argument("--iq2-steps", type=int, default=512, help="timed c3 GEMM steps (0 = skip)")
     ap.add_argument("--prefill-steps", type=int, default=64, help="timed c4 GEMM steps (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline budget (0 = skip)")
     args = ap.parse_args()
@@ -162,9 +239,7 @@ def main():
     if int(os.environ.get("RANK", "0")) != 0:
         return
 
-    import numpy as np
     import torch
-    import oracle as O
 
     pkg = load_package()
     arch, cus = pkg.device_check()
@@ -173,16 +248,15 @@ def main():
     # ---------------- config 1: GEMV M=1 N=4096 K=4096, rotating weights ----------------
     m, n, k = 1, 4096, 4096
     copies = 32
-    act, w = O.create_input(0, m, n, k, seed=1, variant=1)
-    wbytes = np.ascontiguousarray(w).view(np.uint8).reshape(n, -1)
-    base = torch.from_numpy(wbytes).cuda()
+    act, w = pkg.create_input(0, m, n, k, seed=1, variant=pkg.INPUT_REFERENCE)
+    base = upload_weights(torch, w)
     weights = [base] + [base.clone() for _ in range(copies - 1)]
     act_t = torch.from_numpy(act).cuda()
     aq = pkg.quantize_q8_0(act_t)
     outs = [torch.empty((m, n), dtype=torch.float32, device="cuda") for _ in range(copies)]
     ws = torch.empty(pkg.lib().pfng_hip_compute_workspace_size(0, m, k), dtype=torch.uint8, device="cuda")
     torch.cuda.synchronize()
-    log(f"[bench] c1 gemv {m}x{n}x{k}: {copies} weight copies, {copies * wbytes.nbytes / 1e6:.0f} MB resident")
+    log(f"[bench] c1 gemv {m}x{n}x{k}: {copies} weight copies, {copies * w.nbytes / 1e6:.0f} MB resident")
 
     g = capture(torch, lambda i: pkg.mul_mat(0, weights[i % copies], aq, m, n, k, out=outs[i % copies]), copies)
     wall, ev_ms, steps = time_graph(torch, g, copies, args.steps, args.warmup)
@@ -197,63 +271,30 @@ def main():
                  copies)
     wall2, ev2, steps2 = time_graph(torch, g2, copies, args.steps, args.warmup)
     e2e_gbs = (per_call + m * k * 4) * steps2 / wall2 / 1e9
+    got = pkg.mul_mat(0, weights[0], aq, m, n, k)
+    ver1 = verify_against_naive(torch, pkg, 0, weights[0], aq, m, n, k, got)
+    del g, g2, weights, outs
+    torch.cuda.empty_cache()
 
-    # correctness of the measured configuration against the oracle
-    ref = O.matmul(0, w, O.quantize_q8_0(act), m, n, k)
-    terms = O.abs_terms(0, w, O.quantize_q8_0(act), m, n, k)
-    got = pkg.mul_mat(0, weights[0], aq, m, n, k).cpu().numpy()
-    ok1 = O.within_tolerance(got, ref, terms)[0]
-
-    # ---------------- config 0: GEMM M=480 N=1536 K=1536 ----------------
-    m0, n0, k0 = 480, 1536, 1536
-    act0, w0 = O.create_input(0, m0, n0, k0, seed=1, variant=1)
-    w0_t = torch.from_numpy(np.ascontiguousarray(w0).view(np.uint8).reshape(n0, -1)).cuda()
-    act0_t = torch.from_numpy(act0).cuda()
-    aq0 = pkg.quantize_q8_0(act0_t)
-    out0 = torch.empty((m0, n0), dtype=torch.float32, device="cuda")
-    torch.cuda.synchronize()
-    gg = capture(torch, lambda i: pkg.mul_mat(0, w0_t, aq0, m0, n0, k0, out=out0), 32)
-    wall0, ev0, steps0 = time_graph(torch, gg, 32, args.gemm_steps, 256)
-    ops = 2.0 * m0 * n0 * k0
-    tops = ops * steps0 / wall0 / 1e12
-    gemm_kernel_us = ev0 * 1e3 / steps0
-    gemm_achieved = ops / (gemm_kernel_us * 1e-6) / 1e12
-    ref0 = O.matmul(0, w0, O.quantize_q8_0(act0), m0, n0, k0)
-    terms0 = O.abs_terms(0, w0, O.quantize_q8_0(act0), m0, n0, k0)
-    ok0 = O.within_tolerance(out0.cpu().numpy(), ref0, terms0)[0]
-    log(f"[bench] c0 gemm: {steps0} steps, {tops:.2f} TOPS wall; kernel {gemm_kernel_us:.3f} us -> "
-        f"{gemm_achieved:.2f} TOPS; verify c1={ok1} c0={ok0}")
-
-    # ---------------- config 4: Llama-7B FFN prefill GEMM M=2048 N=11008 K=4096 ----------------
+    # ---------------- GEMM configs ----------------
+    gemm = gemm_item(torch, pkg, "c0: q4_0 x q8_0 GEMM M=480 N=1536 K=1536", 0, 480, 1536, 1536, args.gemm_steps, 256,
+                     pkg.INPUT_REFERENCE, "gemm_q4_0_kernel")
+    q4k = gemm_item(torch, pkg, "c2: q4_K x q8_K GEMM M=480 N=1536 K=1536", 1, 480, 1536, 1536, args.gemm_steps, 256,
+                    pkg.INPUT_REFERENCE, "gemm_kq_kernel<q4_K>")
+    iq2 = None
+    if args.iq2_steps > 0:
+        iq2 = gemm_item(torch, pkg, "c3: iq2_xxs x q8_K GEMM M=512 N=4096 K=4096 (baseline weight generator)", 2, 512,
+                        4096, 4096, args.iq2_steps, 32, pkg.INPUT_BASELINE, "gemm_kq_kernel<iq2_xxs>")
     prefill = None
     if args.prefill_steps > 0:
-        m4, n4, k4 = 2048, 11008, 4096
-        act4, w4 = O.create_input(0, m4, n4, k4, seed=1, variant=1)
-        w4_t = torch.from_numpy(np.ascontiguousarray(w4).view(np.uint8).reshape(n4, -1)).cuda()
-        aq4 = pkg.quantize_q8_0(torch.from_numpy(act4).cuda())
-        out4 = torch.empty((m4, n4), dtype=torch.float32, device="cuda")
-        torch.cuda.synchronize()
-        g4 = capture(torch, lambda i: pkg.mul_mat(0, w4_t, aq4, m4, n4, k4, out=out4), 4)
-        wall4, ev4, steps4 = time_graph(torch, g4, 4, args.prefill_steps, 8)
-        ops4 = 2.0 * m4 * n4 * k4
-        k4_us = ev4 * 1e3 / steps4
-        rows = np.sort(np.random.default_rng(4).choice(m4, 16, replace=False))
-        aq4_h = O.quantize_q8_0(act4[rows])
-        ok4 = O.within_tolerance(out4.cpu().numpy()[rows], O.matmul(0, w4, aq4_h, 16, n4, k4),
-                                 O.abs_terms(0, w4, aq4_h, 16, n4, k4))[0]
-        prefill = {"workload": "c4: q4_0 x q8_0 GEMM M=2048 N=11008 K=4096", "value": round(ops4 * steps4 / wall4 / 1e12, 3),
-                   "unit": "TOPS", "steps": steps4, "ms_per_step": round(wall4 * 1e3 / steps4, 6), "verified_rows": ok4,
-                   "roofline": {"bound": "mfma", "achieved": round(ops4 / (k4_us * 1e-6) / 1e12, 3),
-                                "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                                "frac": round(ops4 / (k4_us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4), "traffic": None,
-                                "kernel": "gemm_q4_0_kernel", "kernel_us": round(k4_us, 3)}}
-        log(f"[bench] c4 gemm: {steps4} steps, {prefill['value']} TOPS wall, kernel {k4_us:.1f} us, verify={ok4}")
-        del w4_t, aq4, out4
+        prefill = gemm_item(torch, pkg, "c4: q4_0 x q8_0 GEMM M=2048 N=11008 K=4096", 0, 2048, 11008, 4096,
+                            args.prefill_steps, 8, pkg.INPUT_REFERENCE, "gemm_q4_0_kernel", rows_to_verify=256)
 
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
     if cpu:
         log(f"[bench] cpu baseline: {cpu}")
 
+    items = [x for x in (gemm, q4k, iq2, prefill) if x is not None]
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -270,17 +311,16 @@ def main():
         "config": {"workload": "c1: q4_0 x q8_0 GEMV M=1 N=4096 K=4096, 32 rotating weight copies (302 MB)",
                    "m": m, "n": n, "k": k, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_q4_0_kernel<1>", "kernel_us": round(kernel_us, 4),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for("gemv_q4_0_m1_kernel", "c1"),
+                     "kernel": "gemv_q4_0_m1_kernel", "kernel_us": round(kernel_us, 4),
                      "bytes_per_launch": per_call},
         "e2e_with_quantize_gbs": round(e2e_gbs, 2),
-        "gemm": {"workload": "c0: q4_0 x q8_0 GEMM M=480 N=1536 K=1536", "value": round(tops, 3), "unit": "TOPS",
-                 "steps": steps0, "ms_per_step": round(wall0 * 1e3 / steps0, 6),
-                 "roofline": {"bound": "mfma", "achieved": round(gemm_achieved, 3), "peak": INT8_PEAK_TOPS,
-                              "unit": "TFLOP/s", "frac": round(gemm_achieved / INT8_PEAK_TOPS, 4), "traffic": None,
-                              "kernel": "gemm_q4_0_kernel", "kernel_us": round(gemm_kernel_us, 4)}},
+        "verify": ver1,
+        "gemm": gemm,
+        "q4_K": q4k,
+        "iq2_xxs": iq2,
         "prefill": prefill,
-        "verified": bool(ok1 and ok0 and (prefill is None or prefill["verified_rows"])),
+        "verified": bool(ver1["passed"] and all(x["verify"]["passed"] for x in items)),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

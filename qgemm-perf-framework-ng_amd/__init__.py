@@ -65,6 +65,14 @@ def lib() -> ctypes.CDLL:
         L.pfng_hip_compute_workspace_size.argtypes = [ci, i64, i64]
         L.pfng_hip_compute.argtypes = [ci, vp, vp, vp, i64, i64, i64, vp, sz, ci, vp]
         L.pfng_hip_block_isums.argtypes = [ci, vp, vp, vp, i64, i64, i64, vp]
+        L.pfng_host_create_input.argtypes = [ci, ci, ctypes.c_uint32, sz, sz, sz, vp, vp]
+        L.pfng_host_quantize_weights.argtypes = [ci, vp, vp, sz, sz]
+        L.pfng_host_fp32_to_fp16.restype = ctypes.c_uint16
+        L.pfng_host_fp32_to_fp16.argtypes = [ctypes.c_float]
+        L.pfng_host_fp16_to_fp32.restype = ctypes.c_float
+        L.pfng_host_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        L.pfng_host_checksum.restype = ctypes.c_double
+        L.pfng_host_checksum.argtypes = [vp, sz]
         _lib = L
     return _lib
 
@@ -76,6 +84,12 @@ EXPORTED_SYMBOLS = (
     "pfng_hip_mul_mat_q4_0_q8_0", "pfng_hip_mul_mat_q4_K_q8_K", "pfng_hip_mul_mat_iq2_xxs_q8_K",
     "pfng_hip_mul_mat", "pfng_hip_compute_workspace_size", "pfng_hip_compute", "pfng_hip_block_isums",
 )
+# host-side C-ABI declared in include/pfng_host.h
+HOST_SYMBOLS = (
+    "pfng_host_create_input", "pfng_host_quantize_weights", "pfng_host_fp32_to_fp16", "pfng_host_fp16_to_fp32",
+    "pfng_host_checksum",
+)
+INPUT_REFERENCE, INPUT_BASELINE = 0, 1
 
 
 def last_error() -> str:
@@ -96,6 +110,42 @@ def device_check() -> tuple[str, int]:
     cus = ctypes.c_int(0)
     check(lib().pfng_hip_device_check(arch, 64, ctypes.byref(cus)))
     return arch.value.decode(), cus.value
+
+
+# ---------------------------------------------------------------------------
+# host-side input generation (bench/framework/benchmark.cpp:29-94)
+# ---------------------------------------------------------------------------
+
+def create_input(qtype: int, m: int, n: int, k: int, seed: int = 1, variant: int = INPUT_BASELINE):
+    """Synthetic inputs as the reference harness makes them: returns (activation
+    float32 (m, k), weight uint8 (n, k/QK * block_bytes)) as numpy arrays."""
+    import numpy as np
+    act = np.empty((m, k), np.float32)
+    w = np.empty((n, (k // QK[qtype]) * WEIGHT_BLOCK_BYTES[qtype]), np.uint8)
+    rc = lib().pfng_host_create_input(qtype, variant, seed, m, n, k, act.ctypes.data, w.ctypes.data)
+    if rc != 0:
+        raise ValueError(f"pfng_host_create_input({TYPE_NAMES.get(qtype, qtype)}, m={m}, n={n}, k={k}) failed: {rc}")
+    return act, w
+
+
+def quantize_weights(qtype: int, x):
+    """Host weight quantizer of the reference (q4_0 or q4_K): float32 (rows, k)
+    -> uint8 (rows, k/QK * block_bytes)."""
+    import numpy as np
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.shape
+    y = np.empty((rows, (k // QK[qtype]) * WEIGHT_BLOCK_BYTES[qtype]), np.uint8)
+    rc = lib().pfng_host_quantize_weights(qtype, x.ctypes.data, y.ctypes.data, rows, k)
+    if rc != 0:
+        raise ValueError(f"pfng_host_quantize_weights({TYPE_NAMES.get(qtype, qtype)}, k={k}) failed: {rc}")
+    return y
+
+
+def checksum(out) -> float:
+    """Sum of every 257th output (kernels/common/adapter_common.cpp:18-23)."""
+    import numpy as np
+    out = np.ascontiguousarray(out, dtype=np.float32)
+    return float(lib().pfng_host_checksum(out.ctypes.data, out.size))
 
 
 # ---------------------------------------------------------------------------

@@ -1,0 +1,190 @@
+#!/usr/bin/env python3
+"""rocprofv3 evidence for the MI355X backend: one configuration, one counter
+set, a Markdown/JSON report with roofline fractions.
+
+Two sub-commands, so that the profiler itself is started from the command line
+(the program goes right after `rocprofv3 ... --`):
+
+  workload   runs one baseline configuration with plain launches on the
+             current stream, then one device copy of 256 MiB (the calibration
+             kernel: it must fetch and write exactly that many bytes).
+  summarize  reads the CSV output of one --kernel-trace --stats run and of
+             two --pmc runs (FETCH_SIZE, then WRITE_SIZE), and reports for the
+             configuration's kernel: average duration, algorithmic bytes and
+             ops, HBM bytes per launch (counter KiB x the copy calibration
+             factor), and the fractions of the 8 TB/s and 5.0 POPS peaks.
+
+Example (the three profiler passes, then the summary):
+  python3 qgemm-perf-framework-ng_amd/evidence.py workload --config c1 --iters 200   # under rocprofv3
+  python3 qgemm-perf-framework-ng_amd/evidence.py summarize --config c1 \\
+      --trace OUT/trace --fetch OUT/fetch --write OUT/write --md profiles/x.md --json profiles/traffic.json
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import json
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+COPY_BYTES = 256 << 20
+
+# name, qtype, m, n, k, input variant, kernel-name substring, bound
+CONFIGS = {
+    "c0": ("q4_0 x q8_0 GEMM M=480 N=1536 K=1536", 0, 480, 1536, 1536, 0, "gemm_q4_0_kernel", "mfma"),
+    "c1": ("q4_0 x q8_0 GEMV M=1 N=4096 K=4096, 32 rotating weight copies", 0, 1, 4096, 4096, 0,
+           "gemv_q4_0_m1_kernel", "hbm"),
+    "c2": ("q4_K x q8_K GEMM M=480 N=1536 K=1536", 1, 480, 1536, 1536, 0, "gemm_kq_kernel", "mfma"),
+    "c3": ("iq2_xxs x q8_K GEMM M=512 N=4096 K=4096 (baseline weight generator)", 2, 512, 4096, 4096, 1,
+           "gemm_kq_kernel", "mfma"),
+    "c4": ("q4_0 x q8_0 GEMM M=2048 N=11008 K=4096", 0, 2048, 11008, 4096, 0, "gemm_q4_0_kernel", "mfma"),
+}
+WB = {0: 18, 1: 144, 2: 66}
+AB = {0: 34, 1: 292, 2: 292}
+QK = {0: 32, 1: 256, 2: 256}
+
+
+def algorithmic(cfg):
+    _, qt, m, n, k, _, _, _ = CONFIGS[cfg]
+    nb = k // QK[qt]
+    return {"bytes": n * nb * WB[qt] + m * nb * AB[qt] + m * n * 4, "ops": 2.0 * m * n * k}
+
+
+def load_package():
+    import importlib.util
+    name = "qgemm_perf_framework_ng_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    spec = importlib.util.spec_from_file_location(name, os.path.join(HERE, "__init__.py"),
+                                                  submodule_search_locations=[HERE])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def run_workload(cfg, iters):
+    import torch
+    pkg = load_package()
+    label, qt, m, n, k, variant, _, _ = CONFIGS[cfg]
+    print(f"[evidence] {cfg}: {label}, {iters} launches", flush=True)
+    act, w = pkg.create_input(qt, m, n, k, seed=1, variant=variant)
+    copies = 32 if cfg == "c1" else 1
+    base = torch.from_numpy(w).cuda()
+    weights = [base] + [base.clone() for _ in range(copies - 1)]
+    aq = pkg.quantize_activation(qt, torch.from_numpy(act).cuda())
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    for i in range(iters):
+        pkg.mul_mat(qt, weights[i % copies], aq, m, n, k, out=out)
+    torch.cuda.synchronize()
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"[evidence] done ({COPY_BYTES >> 20} MiB calibration copy)", flush=True)
+
+
+def read_csvs(root, suffix):
+    rows = []
+    for path in sorted(glob.glob(os.path.join(root, "**", f"*{suffix}"), recursive=True)):
+        with open(path, newline="") as f:
+            rows.extend(csv.DictReader(f))
+    return rows
+
+
+def is_copy(name):
+    return "copy" in name.lower()
+
+
+def counter_per_dispatch(rows, counter, match):
+    vals = [float(r["Counter_Value"]) for r in rows if r.get("Counter_Name") == counter and match(r["Kernel_Name"])]
+    return (sum(vals) / len(vals), len(vals)) if vals else (None, 0)
+
+
+def summarize(args):
+    label, qt, m, n, k, _, kname, bound = CONFIGS[args.config]
+    alg = algorithmic(args.config)
+    stats = read_csvs(args.trace, "kernel_stats.csv")
+    kstat = [r for r in stats if kname in r["Name"]]
+    if not kstat:
+        raise SystemExit(f"no kernel matching {kname} in {args.trace}")
+    calls = sum(int(r["Calls"]) for r in kstat)
+    avg_ns = sum(float(r["TotalDurationNs"]) for r in kstat) / calls
+    kernel_full = max(kstat, key=lambda r: int(r["Calls"]))["Name"]
+    report = {"config": args.config, "workload": label, "kernel": kname, "kernel_symbol": kernel_full[:160],
+              "calls": calls, "avg_us": round(avg_ns / 1e3, 4), "algorithmic_bytes": alg["bytes"],
+              "algorithmic_ops": alg["ops"]}
+    if bound == "hbm":
+        a = alg["bytes"] / (avg_ns * 1e-9) / 1e9
+        report.update({"bound": "hbm", "achieved_gbs": round(a, 2), "frac": round(a / HBM_PEAK_GBS, 4)})
+    else:
+        a = alg["ops"] / (avg_ns * 1e-9) / 1e12
+        report.update({"bound": "mfma", "achieved_tops": round(a, 2), "frac": round(a / INT8_PEAK_TOPS, 4)})
+    hbm = None
+    if args.fetch and args.write:
+        fr, wr = read_csvs(args.fetch, "counter_collection.csv"), read_csvs(args.write, "counter_collection.csv")
+        f_k, nf = counter_per_dispatch(fr, "FETCH_SIZE", lambda s: kname in s)
+        w_k, nw = counter_per_dispatch(wr, "WRITE_SIZE", lambda s: kname in s)
+        f_c, _ = counter_per_dispatch(fr, "FETCH_SIZE", is_copy)
+        w_c, _ = counter_per_dispatch(wr, "WRITE_SIZE", is_copy)
+        if None not in (f_k, w_k, f_c, w_c) and f_c > 0 and w_c > 0:
+            ff, fw = COPY_BYTES / (f_c * 1024), COPY_BYTES / (w_c * 1024)
+            hbm = f_k * 1024 * ff + w_k * 1024 * fw
+            report.update({"fetch_kib_per_dispatch": round(f_k, 1), "write_kib_per_dispatch": round(w_k, 1),
+                           "dispatches_counted": [nf, nw], "copy_fetch_kib": round(f_c, 1),
+                           "copy_write_kib": round(w_c, 1), "calibration_fetch": round(ff, 4),
+                           "calibration_write": round(fw, 4), "hbm_bytes_per_launch": int(round(hbm)),
+                           "hbm_over_algorithmic": round(hbm / alg["bytes"], 3)})
+    lines = [f"# {kname} — {args.config}: {label}", "",
+             "Produced by `qgemm-perf-framework-ng_amd/evidence.py summarize` from rocprofv3 runs of",
+             f"`evidence.py workload --config {args.config}`.", "", "Commands:", "```"]
+    lines += [c for c in (args.command or [])]
+    lines += ["```", "", "| quantity | value |", "|---|---|"]
+    for key, val in report.items():
+        lines.append(f"| {key} | {val} |")
+    if args.md:
+        os.makedirs(os.path.dirname(os.path.abspath(args.md)), exist_ok=True)
+        with open(args.md, "w") as f:
+            f.write("\n".join(lines) + "\n")
+    if args.json:
+        table = {"entries": []}
+        if os.path.exists(args.json):
+            with open(args.json) as f:
+                table = json.load(f)
+        entry = {"kernel": kname if args.config != "c1" else "gemv_q4_0_m1_kernel", "workload": args.config,
+                 "hbm_bytes_per_launch": report.get("hbm_bytes_per_launch"), "report": report}
+        table["entries"] = [e for e in table["entries"] if e.get("workload") != args.config] + [entry]
+        with open(args.json, "w") as f:
+            json.dump(table, f, indent=1)
+    print(json.dumps(report))
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    w = sub.add_parser("workload")
+    w.add_argument("--config", choices=sorted(CONFIGS), required=True)
+    w.add_argument("--iters", type=int, default=100)
+    s = sub.add_parser("summarize")
+    s.add_argument("--config", choices=sorted(CONFIGS), required=True)
+    s.add_argument("--trace", required=True, help="output directory of the --kernel-trace --stats run")
+    s.add_argument("--fetch", help="output directory of the --pmc FETCH_SIZE run")
+    s.add_argument("--write", help="output directory of the --pmc WRITE_SIZE run")
+    s.add_argument("--md", help="Markdown summary to write")
+    s.add_argument("--json", help="traffic table to update")
+    s.add_argument("--command", action="append", help="profiler command line to record in the summary")
+    args = ap.parse_args()
+    if args.cmd == "workload":
+        run_workload(args.config, args.iters)
+    else:
+        summarize(args)
+
+
+if __name__ == "__main__":
+    main()
