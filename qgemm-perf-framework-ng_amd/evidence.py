@@ -98,13 +98,19 @@ def read_csvs(root, suffix):
     return rows
 
 
-def is_copy(name):
-    return "copy" in name.lower()
-
-
 def counter_per_dispatch(rows, counter, match):
     vals = [float(r["Counter_Value"]) for r in rows if r.get("Counter_Name") == counter and match(r["Kernel_Name"])]
     return (sum(vals) / len(vals), len(vals)) if vals else (None, 0)
+
+
+def calibration_copy(rows, counter):
+    """Counter value of the workload's final dispatch, the 256 MiB device copy
+    (earlier copy kernels are the uploads and weight clones)."""
+    mine = [r for r in rows if r.get("Counter_Name") == counter]
+    if not mine:
+        return None
+    last = max(mine, key=lambda r: int(r["Dispatch_Id"]))
+    return float(last["Counter_Value"]) if "copy" in last["Kernel_Name"].lower() else None
 
 
 def summarize(args):
@@ -131,8 +137,8 @@ def summarize(args):
         fr, wr = read_csvs(args.fetch, "counter_collection.csv"), read_csvs(args.write, "counter_collection.csv")
         f_k, nf = counter_per_dispatch(fr, "FETCH_SIZE", lambda s: kname in s)
         w_k, nw = counter_per_dispatch(wr, "WRITE_SIZE", lambda s: kname in s)
-        f_c, _ = counter_per_dispatch(fr, "FETCH_SIZE", is_copy)
-        w_c, _ = counter_per_dispatch(wr, "WRITE_SIZE", is_copy)
+        f_c = calibration_copy(fr, "FETCH_SIZE")
+        w_c = calibration_copy(wr, "WRITE_SIZE")
         if None not in (f_k, w_k, f_c, w_c) and f_c > 0 and w_c > 0:
             ff, fw = COPY_BYTES / (f_c * 1024), COPY_BYTES / (w_c * 1024)
             hbm = f_k * 1024 * ff + w_k * 1024 * fw
