@@ -105,7 +105,8 @@ def time_graph(torch, graph, launches_per_replay, steps, warmup):
 
 
 def capture(torch, fn, count):
-    """Capture `count` calls fn(i) into one graph on a side stream."""
+    """Capture `count` calls fn(i) into one graph on a side stream, after an
+    eager warm-up on the same stream."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -114,7 +115,7 @@ def capture(torch, fn, count):
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):
         for i in range(count):
             fn(i)
     torch.cuda.synchronize()

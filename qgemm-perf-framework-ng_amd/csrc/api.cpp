@@ -7,6 +7,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
 
 #include "kernels.h"
 #include "pfng_hip.h"
@@ -54,6 +56,29 @@ int check_shape(int type, int64_t m, int64_t n, int64_t k) {
         return fail(PFNG_ERR_INVALID_ARGUMENT, "shape too large (m=%lld n=%lld k=%lld)", (long long)m, (long long)n,
                     (long long)k);
     return PFNG_OK;
+}
+
+std::mutex g_cus_mu;
+std::map<int, int> g_cus;
+
+// Compute units of device `dev` (queried once per device).
+int device_cus(int dev) {
+    std::lock_guard<std::mutex> lock(g_cus_mu);
+    auto it = g_cus.find(dev);
+    if (it != g_cus.end()) return it->second;
+    int cus = 256;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0) cus = prop.multiProcessorCount;
+    g_cus[dev] = cus;
+    return cus;
+}
+
+int launch_mfma(int type, const void *weight, const void *act_q, float *out, int64_t m, int64_t n, int64_t k,
+                hipStream_t s) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(PFNG_ERR_HIP, "hipGetDevice failed");
+    const pfng::MfmaPlan plan = pfng::plan_mfma(type, m, n, k, device_cus(dev));
+    return hip_status(pfng::launch_mfma_mul_mat(type, weight, act_q, out, m, n, k, plan, s), "mfma launch");
 }
 
 }  // namespace
@@ -110,14 +135,14 @@ int pfng_hip_mul_mat(int type, const void *weight, const void *act_q, float *out
     switch (path) {
     case PFNG_PATH_AUTO:
         if (gemv_ok) return hip_status(pfng::launch_gemv(type, weight, act_q, out, m, n, k, s), "gemv launch");
-        if (mfma_ok) return hip_status(pfng::launch_mfma_mul_mat(type, weight, act_q, out, m, n, k, s), "mfma launch");
+        if (mfma_ok) return launch_mfma(type, weight, act_q, out, m, n, k, s);
         return hip_status(pfng::launch_naive_mul_mat(type, weight, act_q, out, m, n, k, s), "naive launch");
     case PFNG_PATH_GEMV:
         if (!gemv_ok) return fail(PFNG_ERR_UNSUPPORTED, "%s GEMV path needs q4_0, m<=8, k%%64==0 (m==1) or k%%256==0, and 16-byte aligned operands (m=%lld k=%lld)", type_name(type), (long long)m, (long long)k);
         return hip_status(pfng::launch_gemv(type, weight, act_q, out, m, n, k, s), "gemv launch");
     case PFNG_PATH_MFMA:
         if (!mfma_ok) return fail(PFNG_ERR_UNSUPPORTED, "%s MFMA path not available for m=%lld k=%lld", type_name(type), (long long)m, (long long)k);
-        return hip_status(pfng::launch_mfma_mul_mat(type, weight, act_q, out, m, n, k, s), "mfma launch");
+        return launch_mfma(type, weight, act_q, out, m, n, k, s);
     case PFNG_PATH_NAIVE:
         return hip_status(pfng::launch_naive_mul_mat(type, weight, act_q, out, m, n, k, s), "naive launch");
     default: return fail(PFNG_ERR_INVALID_ARGUMENT, "unknown path %d", path);

@@ -42,15 +42,19 @@ __constant__ uint16_t kIq2GridCodes[256] = PFNG_IQ2XXS_GRID_CODES_INIT;
 
 enum class Kq { Q4K, IQ2 };
 
-template <Kq T, int BM, int BN, int WM, int WN>
+// BM x BN workgroup tile, WM x WN waves over it, the 4 sub-blocks of each
+// stage divided among WK waves (WK > 1: partial accumulators added through LDS
+// at the end, in wave order).
+template <Kq T, int BM, int BN, int WM, int WN, int WK = 1>
 struct KqConfig {
     static constexpr Kq kType = T;
     static constexpr bool kQ4K = T == Kq::Q4K;
-    static constexpr int kBM = BM, kBN = BN, kWM = WM, kWN = WN;
-    static constexpr int kThreads = 64 * WM * WN;
+    static constexpr int kBM = BM, kBN = BN, kWM = WM, kWN = WN, kWK = WK;
+    static constexpr int kThreads = 64 * WM * WN * WK;
     static constexpr int TM = BM / WM / 32;  // 32x32 tiles per wave along m
     static constexpr int TN = BN / WN / 32;  // along n
     static constexpr int kSub = 4;                    // sub-blocks per stage
+    static constexpr int kWaveSub = kSub / WK;        // sub-blocks per stage of one wave
     static constexpr int kRowStride = kSub * 32 + 16;  // LDS bytes per int8 row (+ pad against bank conflicts)
     // LDS layout of one stage buffer
     static constexpr int kAq = 0;                                   // int8 [BM][kRowStride]
@@ -64,22 +68,28 @@ struct KqConfig {
     static constexpr int kBufBytes = kWmin + (kQ4K ? BN * 16 : 0);
     static constexpr int kGrid = 2 * kBufBytes;                      // iq2: 256 x 8-byte grid magnitudes
     static constexpr int kLdsBytes = kGrid + (kQ4K ? 0 : 256 * 8);
-    // global -> register tasks per stage: activation rows in halves of 64
-    // bytes, weight rows per sub-block
-    static constexpr int kActPT = BM * 2 / kThreads;
+    // global -> register tasks per stage: each activation row in kActE parts
+    // (2 or 4) of its 128 int8 and 8 bsums, each weight row per sub-block
+    static constexpr int kActE = BM * 2 >= kThreads ? 2 : kThreads / BM;
+    static constexpr int kQsDw = 32 / kActE;  // activation dwords per task
+    static constexpr int kBsDw = 4 / kActE;   // bsum dwords per task
+    static constexpr int kActPT = BM * kActE / kThreads;
     static constexpr int kWPT = BN * kSub / kThreads;
     static_assert(TM >= 1 && TN >= 1, "tile too small");
-    static_assert(kActPT * kThreads == BM * 2 && kWPT * kThreads == BN * kSub, "tasks must split evenly");
+    static_assert(kActE == 2 || kActE == 4, "activation rows split in 2 or 4 parts");
+    static_assert(kActPT * kThreads == BM * kActE && kWPT * kThreads == BN * kSub, "tasks must split evenly");
     static_assert(kActPT >= 1 && kWPT >= 1, "every thread takes at least one task of each operand");
     static_assert(kAd % 16 == 0 && kAb % 16 == 0 && kWq % 16 == 0 && kWs % 16 == 0 && kWd % 16 == 0 &&
                       kWdm % 16 == 0 && kWmin % 16 == 0 && kBufBytes % 16 == 0,
                   "LDS regions 16-byte aligned");
+    static_assert(kWaveSub * WK == kSub, "the stage's sub-blocks split evenly over the K-waves");
+    static_assert((WK - 1) * WM * WN * TM * TN * 16 * 64 * 4 <= 2 * kBufBytes, "K-wave reduction fits in LDS");
 };
 
 template <class C>
 struct KqRegs {
-    uint32_t aq[C::kActPT][16];  // 64 activation bytes
-    uint32_t ab[C::kActPT][2];   // 4 bsums (q4_K)
+    uint32_t aq[C::kActPT][C::kQsDw];  // 128 / kActE activation bytes
+    uint32_t ab[C::kActPT][C::kBsDw];  // 8 / kActE bsums (q4_K)
     float ad[C::kActPT];
     // q4_K: 16 nibble bytes + the 16-byte header (d, dmin, scales)
     // iq2_xxs: the 8 bytes of one sub-block + d
@@ -97,16 +107,16 @@ __device__ __forceinline__ void kq_load(const uint8_t *__restrict__ a, const uin
 #pragma unroll
     for (int it = 0; it < C::kActPT; ++it) {
         const int task = threadIdx.x + it * C::kThreads;
-        const int row = m0 + task / 2, e = task % 2;
+        const int row = m0 + task / C::kActE, e = task % C::kActE;
         const int lrow = row < m ? row : m - 1;
         const uint8_t *blk = a + ((size_t)lrow * nb + b) * kQ8KBytes;
-        const uint32_t *qs = reinterpret_cast<const uint32_t *>(blk + 4 + 128 * h + 64 * e);
+        const uint32_t *qs = reinterpret_cast<const uint32_t *>(blk + 4 + 128 * h + 4 * C::kQsDw * e);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) r.aq[it][i] = qs[i];
-        const uint32_t *bs = reinterpret_cast<const uint32_t *>(blk + 260 + 16 * h + 8 * e);
+        for (int i = 0; i < C::kQsDw; ++i) r.aq[it][i] = qs[i];
+        const uint32_t *bs = reinterpret_cast<const uint32_t *>(blk + 260 + 16 * h + 4 * C::kBsDw * e);
         if constexpr (C::kQ4K) {
-            r.ab[it][0] = bs[0];
-            r.ab[it][1] = bs[1];
+#pragma unroll
+            for (int i = 0; i < C::kBsDw; ++i) r.ab[it][i] = bs[i];
         }
         r.ad[it] = *reinterpret_cast<const float *>(blk);
     }
@@ -158,21 +168,23 @@ __device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int 
 #pragma unroll
     for (int it = 0; it < C::kActPT; ++it) {
         const int task = threadIdx.x + it * C::kThreads;
-        const int row = task / 2, e = task % 2;
+        const int row = task / C::kActE, e = task % C::kActE;
         const uint32_t *v = r.aq[it];
-        uint4 *dst = reinterpret_cast<uint4 *>(lds + C::kAq + row * C::kRowStride + 64 * e);
+        uint4 *dst = reinterpret_cast<uint4 *>(lds + C::kAq + row * C::kRowStride + 4 * C::kQsDw * e);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dst[i] = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-        *reinterpret_cast<float *>(lds + C::kAd + row * 4) = r.ad[it];  // both halves write the same value
+        for (int i = 0; i < C::kQsDw / 4; ++i) dst[i] = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+        *reinterpret_cast<float *>(lds + C::kAd + row * 4) = r.ad[it];  // every part writes the same value
         if constexpr (C::kQ4K) {
-            uint32_t hb[2];
+            uint32_t hb[C::kBsDw];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < C::kBsDw; ++i) {
                 const _Float16 lo = (_Float16)(float)(int16_t)(r.ab[it][i] & 0xffffu);
                 const _Float16 hi = (_Float16)(float)(int16_t)(r.ab[it][i] >> 16);
                 hb[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
             }
-            *reinterpret_cast<uint2 *>(lds + C::kAb + row * 16 + 8 * e) = make_uint2(hb[0], hb[1]);
+            uint32_t *bdst = reinterpret_cast<uint32_t *>(lds + C::kAb + row * 16 + 4 * C::kBsDw * e);
+#pragma unroll
+            for (int i = 0; i < C::kBsDw; ++i) bdst[i] = hb[i];
         }
     }
 #pragma unroll
@@ -250,23 +262,19 @@ __device__ __forceinline__ i32x4 mul_planes(i32x4 v, uint32_t digit2) {
     return o;
 }
 
-// Sub-block sums of one stage (half h of the super-block).
+// Sub-block sums of one stage (half H of the super-block) for one wave: its
+// kWaveSub sub-blocks tb .. tb + kWaveSub - 1 (tb a multiple of kWaveSub).
 template <class C, int H>
-__device__ __forceinline__ void kq_compute(const uint8_t *buf, KqAcc<C> &A, int lane, int wave_m, int wave_n) {
+__device__ __forceinline__ void kq_compute(const uint8_t *buf, KqAcc<C> &A, int tb, int lane, int wave_m,
+                                           int wave_n) {
     const int li = lane & 31, lh = lane >> 5;
     const uint8_t *aq = buf + C::kAq + (wave_m * C::TM * 32 + li) * C::kRowStride + lh * 16;
     const uint8_t *wq = buf + C::kWq + (wave_n * C::TN * 32 + li) * C::kRowStride + lh * 16;
     const int wrow = wave_n * C::TN * 32 + li;
     if constexpr (C::kQ4K) {
-        uint4 dg[C::TN][2];  // digit pairs of the 4 sub-blocks: (l, h) per sub-block
 #pragma unroll
-        for (int tn = 0; tn < C::TN; ++tn) {
-            const uint4 *s = reinterpret_cast<const uint4 *>(buf + C::kWs + (wrow + tn * 32) * 32);
-            dg[tn][0] = s[0];
-            dg[tn][1] = s[1];
-        }
-#pragma unroll
-        for (int t = 0; t < C::kSub; ++t) {
+        for (int j = 0; j < C::kWaveSub; ++j) {
+            const int t = tb + j;
             i32x4 av[C::TM], vl[C::TN], vh[C::TN];
 #pragma unroll
             for (int tm = 0; tm < C::TM; ++tm)
@@ -274,39 +282,42 @@ __device__ __forceinline__ void kq_compute(const uint8_t *buf, KqAcc<C> &A, int 
 #pragma unroll
             for (int tn = 0; tn < C::TN; ++tn) {
                 const i32x4 v = *reinterpret_cast<const i32x4 *>(wq + tn * 32 * C::kRowStride + t * 32);
-                const uint4 &d = dg[tn][t / 2];
-                const uint32_t dl = (t % 2) ? d.z : d.x, dh = (t % 2) ? d.w : d.y;
-                vl[tn] = mul_planes(v, dl);
-                vh[tn] = mul_planes(v, dh);
+                // digit pair (l, h) of sub-block t, each replicated in both 16-bit halves
+                const uint2 d = *reinterpret_cast<const uint2 *>(buf + C::kWs + (wrow + tn * 32) * 32 + 8 * t);
+                vl[tn] = mul_planes(v, d.x);
+                vh[tn] = mul_planes(v, d.y);
             }
 #pragma unroll
             for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
                 for (int tn = 0; tn < C::TN; ++tn) {
-                    const bool first = H == 0 && t == 0;
+                    const bool first = H == 0 && j == 0;
                     A.s0[tm][tn] = mfma_i8_32x32x32(av[tm], vl[tn], first ? (i32x16){} : A.s0[tm][tn]);
                     A.s1[tm][tn] = mfma_i8_32x32x32(av[tm], vh[tn], first ? (i32x16){} : A.s1[tm][tn]);
                 }
         }
-        // IM over the half's 8 bsums: lane supplies row li, k = 4*lh .. 4*lh+3
+        // IM over the half's 8 bsums: lane supplies row li and k = 4*lh .. 4*lh+3,
+        // i.e. the bsums of sub-blocks 2*lh and 2*lh+1; lanes whose sub-blocks
+        // belong to another K-wave contribute zero
+        const bool mine = C::kWaveSub >= 4 || (2 * lh >= tb && 2 * lh < tb + C::kWaveSub);
         f16x4 ab[C::TM], wm[C::TN];
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm)
             ab[tm] = *reinterpret_cast<const f16x4 *>(buf + C::kAb + (wave_m * C::TM * 32 + tm * 32 + li) * 16 + lh * 8);
 #pragma unroll
-        for (int tn = 0; tn < C::TN; ++tn)
+        for (int tn = 0; tn < C::TN; ++tn) {
             wm[tn] = *reinterpret_cast<const f16x4 *>(buf + C::kWmin + (wrow + tn * 32) * 16 + lh * 8);
+            if (!mine) wm[tn] = (f16x4){};
+        }
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
             for (int tn = 0; tn < C::TN; ++tn)
                 A.im[tm][tn] = mfma_f16_32x32x8(ab[tm], wm[tn], H == 0 ? (f32x16){} : A.im[tm][tn]);
     } else {
-        int4 sc[C::TN];
 #pragma unroll
-        for (int tn = 0; tn < C::TN; ++tn) sc[tn] = *reinterpret_cast<const int4 *>(buf + C::kWs + (wrow + tn * 32) * 16);
-#pragma unroll
-        for (int t = 0; t < C::kSub; ++t) {
+        for (int j = 0; j < C::kWaveSub; ++j) {
+            const int t = tb + j;
             i32x4 av[C::TM], wv[C::TN];
 #pragma unroll
             for (int tm = 0; tm < C::TM; ++tm)
@@ -318,12 +329,12 @@ __device__ __forceinline__ void kq_compute(const uint8_t *buf, KqAcc<C> &A, int 
             for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
                 for (int tn = 0; tn < C::TN; ++tn) {
-                    const i32x16 s = mfma_i8_32x32x32(av[tm], wv[tn], (i32x16){});
-                    const int scale = t == 0 ? sc[tn].x : t == 1 ? sc[tn].y : t == 2 ? sc[tn].z : sc[tn].w;
+                    const i32x16 sb = mfma_i8_32x32x32(av[tm], wv[tn], (i32x16){});
+                    const int scale = *reinterpret_cast<const int32_t *>(buf + C::kWs + (wrow + tn * 32) * 16 + 4 * t);
 #pragma unroll
                     for (int q = 0; q < 16; ++q)
-                        A.s0[tm][tn][q] = (H == 0 && t == 0) ? __mul24(s[q], scale)
-                                                             : __mul24(s[q], scale) + A.s0[tm][tn][q];
+                        A.s0[tm][tn][q] = (H == 0 && j == 0) ? __mul24(sb[q], scale)
+                                                             : __mul24(sb[q], scale) + A.s0[tm][tn][q];
                 }
         }
     }
@@ -391,8 +402,11 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_kq_kernel(const uint8_t *
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int wave_m = wave / C::kWN;
-    const int wave_n = wave % C::kWN;
+    const int wk = wave / (C::kWM * C::kWN);   // which share of each stage's sub-blocks
+    const int wmn = wave % (C::kWM * C::kWN);  // which TM x TN sub-tile
+    const int wave_m = wmn / C::kWN;
+    const int wave_n = wmn % C::kWN;
+    const int tb = wk * C::kWaveSub;
     const TileOrigin to = xcd_tile(blockIdx.x, (m + C::kBM - 1) / C::kBM, (n + C::kBN - 1) / C::kBN);
     const int m0 = to.mi * C::kBM, n0 = to.ni * C::kBN;
     uint8_t *grid = lds + C::kGrid;
@@ -431,14 +445,14 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_kq_kernel(const uint8_t *
     for (int b = 0; b < nb; ++b) {
         const int bn = b + 1 < nb ? b + 1 : nb - 1;
         __builtin_amdgcn_sched_barrier(0);
-        kq_compute<C, 0>(lds, A, lane, wave_m, wave_n);
+        kq_compute<C, 0>(lds, A, tb, lane, wave_m, wave_n);
         __builtin_amdgcn_sched_barrier(0);
         kq_store<C>(lds + C::kBufBytes, grid, 1, regs);
         __builtin_amdgcn_sched_barrier(0);
         kq_load<C>(a, w, m, n, nb, m0, n0, bn, 0, regs);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
-        kq_compute<C, 1>(lds + C::kBufBytes, A, lane, wave_m, wave_n);
+        kq_compute<C, 1>(lds + C::kBufBytes, A, tb, lane, wave_m, wave_n);
         kq_epilogue<C, kIsums>(lds + C::kBufBytes, A, isums, m, n, nb, m0, n0, b, lane, wave_m, wave_n);
         __builtin_amdgcn_sched_barrier(0);
         kq_store<C>(lds, grid, 0, regs);
@@ -449,6 +463,33 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_kq_kernel(const uint8_t *
     }
 
     if constexpr (!kIsums) {
+        if constexpr (C::kWK > 1) {
+            // add the other K-waves' partials to wave wk == 0's, in wave order;
+            // the stage buffers are free after the loop's last barrier
+            constexpr int kRegs = C::TM * C::TN * 16;
+            float *red = reinterpret_cast<float *>(lds);
+            if (wk > 0) {
+                float *dst = red + ((wk - 1) * C::kWM * C::kWN + wmn) * kRegs * 64 + lane;
+#pragma unroll
+                for (int tm = 0; tm < C::TM; ++tm)
+#pragma unroll
+                    for (int tn = 0; tn < C::TN; ++tn)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) dst[((tm * C::TN + tn) * 16 + r) * 64] = A.acc[tm][tn][r];
+            }
+            __syncthreads();
+            if (wk > 0) return;
+#pragma unroll
+            for (int w2 = 1; w2 < C::kWK; ++w2) {
+                const float *src = red + ((w2 - 1) * C::kWM * C::kWN + wmn) * kRegs * 64 + lane;
+#pragma unroll
+                for (int tm = 0; tm < C::TM; ++tm)
+#pragma unroll
+                    for (int tn = 0; tn < C::TN; ++tn)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) A.acc[tm][tn][r] += src[((tm * C::TN + tn) * 16 + r) * 64];
+            }
+        }
         const int li = lane & 31;
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm)
@@ -476,25 +517,65 @@ hipError_t launch_kq(const void *w, const void *a, float *c, int32_t *isums, int
     return hipGetLastError();
 }
 
-// 128 x 64 tiles, 4 waves of 64 x 32
-using Q4KTile = KqConfig<Kq::Q4K, 128, 64, 2, 2>;
-using Iq2Tile = KqConfig<Kq::IQ2, 128, 64, 2, 2>;
+// large problems: 128 x 64 tiles, 4 waves of 64 x 32
+template <Kq T>
+using KqBig = KqConfig<T, 128, 64, 2, 2>;
+// medium problems: 64 x 64 tiles, 4 waves of 32 x 32
+template <Kq T>
+using KqSmall = KqConfig<T, 64, 64, 2, 2>;
+// small problems: 32 x 32 tiles. q4_K: 2 waves each taking 2 of the stage's 4
+// sub-blocks (its accuracy bound is per element, so partial super-block sums
+// may be scaled separately). iq2_xxs: one wave, since its bound is per
+// super-block: the integer sum must be complete before it is scaled, or
+// partial sums that nearly cancel would be rounded against a small total.
+template <Kq T>
+using KqTiny = KqConfig<T, 32, 32, 1, 1, T == Kq::Q4K ? 2 : 1>;
+
+enum { kCfgBig = 0, kCfgSmall = 1, kCfgTiny = 2 };
+
+int64_t tiles_of(int64_t m, int64_t n, int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); }
+
+template <Kq T>
+hipError_t dispatch(const void *w, const void *a, float *c, const MfmaPlan &plan, int64_t m, int64_t n, int64_t k,
+                    hipStream_t stream) {
+    switch (plan.config) {
+    case kCfgBig: return launch_kq<KqBig<T>, false>(w, a, c, nullptr, m, n, k, stream);
+    case kCfgSmall: return launch_kq<KqSmall<T>, false>(w, a, c, nullptr, m, n, k, stream);
+    default: return launch_kq<KqTiny<T>, false>(w, a, c, nullptr, m, n, k, stream);
+    }
+}
 
 }  // namespace
 
+// The largest tile that still gives at least two workgroups per CU, else the
+// 32 x 32 tile with two K-waves.
+MfmaPlan plan_kquant(int type, int64_t m, int64_t n, int64_t k, int cus) {
+    (void)type;
+    (void)k;
+    MfmaPlan p;
+    const int64_t enough = 2 * (int64_t)cus;
+    if (tiles_of(m, n, 128, 64) >= enough)
+        p.config = kCfgBig;
+    else if (tiles_of(m, n, 64, 64) >= enough)
+        p.config = kCfgSmall;
+    else
+        p.config = kCfgTiny;
+    return p;
+}
+
 hipError_t launch_kquant_mul_mat(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
-                                 hipStream_t stream) {
-    if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K) return launch_kq<Q4KTile, false>(w, a, c, nullptr, m, n, k, stream);
-    if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K)
-        return launch_kq<Iq2Tile, false>(w, a, c, nullptr, m, n, k, stream);
+                                 const MfmaPlan &plan, hipStream_t stream) {
+    if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K) return dispatch<Kq::Q4K>(w, a, c, plan, m, n, k, stream);
+    if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K) return dispatch<Kq::IQ2>(w, a, c, plan, m, n, k, stream);
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_kquant_block_isums(int type, const void *w, const void *a, int32_t *out, int64_t m, int64_t n,
                                      int64_t k, hipStream_t stream) {
-    if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K) return launch_kq<Q4KTile, true>(w, a, nullptr, out, m, n, k, stream);
+    if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K)
+        return launch_kq<KqBig<Kq::Q4K>, true>(w, a, nullptr, out, m, n, k, stream);
     if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K)
-        return launch_kq<Iq2Tile, true>(w, a, nullptr, out, m, n, k, stream);
+        return launch_kq<KqBig<Kq::IQ2>, true>(w, a, nullptr, out, m, n, k, stream);
     return hipErrorInvalidValue;
 }
 

@@ -5,10 +5,10 @@
 //
 // Workgroup tile BM x BN, K stages of KB blocks (32*KB elements):
 //   * global -> registers: every thread loads whole q8_0 and q4_0 block pairs
-//     (68 / 36 bytes, dword loads, 4-byte aligned when k % 64 == 0) into a ring
-//     of P register sets, so P-1 stages are in flight while one is computed.
-//     The loads are unconditional (rows clamped at the matrix edge) and a
-//     scheduling barrier keeps them ahead of the arithmetic.
+//     (68 / 36 bytes, dword loads, 4-byte aligned when k % 64 == 0) one stage
+//     ahead of the stage being computed. The loads are unconditional (rows
+//     clamped at the matrix edge) and a scheduling barrier keeps them ahead of
+//     the arithmetic.
 //   * registers -> LDS: activation int8 copied (the even block of a pair
 //     realigned by two bytes); weight nibbles expanded to 16*(q-8) int8; fp16
 //     scales kept per row. Rows are padded so the 16-byte MFMA operand reads
@@ -17,8 +17,11 @@
 //     P = v_mfma_f32_32x32x8_f16(da, dw) (the exact outer product da*dw on the
 //     matrix core), acc = fma(float(S16), P, acc); C = acc / 16 at the end.
 // The epilogue costs two VALU operations per (m, n, block) item; the int8
-// matrix core finishes the same items about twice as fast, so this format is
-// VALU-bound at roughly half of the int8 MFMA rate.
+// matrix core finishes the same items about four times as fast (a wave64 VALU
+// op takes 4 cycles, packed fp32 is not used), so this format is VALU-bound.
+// Small problems use 32x32 tiles whose stage blocks are shared by two waves
+// (their partial sums are added through LDS at the end), so that even a few
+// hundred output tiles keep several waves resident on every CU.
 //
 // A diagnostic instantiation writes S_b instead of accumulating (block isums).
 #include "device_common.h"
@@ -28,16 +31,20 @@ namespace pfng {
 
 namespace {
 
-template <int BM, int BN, int WM, int WN, int KB, int RING = 2, int MINW = 2>
+// BM x BN workgroup tile, WM x WN waves over it, each wave's stage blocks
+// divided among WK waves (WK > 1: the WK partial accumulators are added
+// through LDS at the end, in wave order), KB q4_0 blocks per K stage.
+// DEPTH register sets of loaded-but-not-stored stages: the loads of stage
+// s+DEPTH+1 are issued while stage s is computed (deep prefetch for the small
+// tiles, whose stages are too short to cover a memory round trip).
+template <int BM, int BN, int WM, int WN, int KB, int WK = 1, int DEPTH = 1, int MINW = 2>
 struct Q40Config {
-    static constexpr int kBM = BM, kBN = BN, kWM = WM, kWN = WN, kKB = KB;
-    // register sets of loaded-but-not-stored stages (1 or 2); with 2 the loads
-    // of stage s+3 are issued while stage s is computed
-    static constexpr int kRing = RING;
+    static constexpr int kBM = BM, kBN = BN, kWM = WM, kWN = WN, kKB = KB, kWK = WK, kDepth = DEPTH;
     // waves per SIMD the register budget must allow: the fp32 epilogue needs two
     // resident waves per SIMD to keep the VALU issuing while the other waits
     static constexpr int kMinWavesPerEU = MINW;
-    static constexpr int kThreads = 64 * WM * WN;
+    static constexpr int kThreads = 64 * WM * WN * WK;
+    static constexpr int kWaveBlocks = KB / WK;  // blocks per stage of one wave
     static constexpr int TM = BM / WM / 32;  // 32x32 tiles per wave along m
     static constexpr int TN = BN / WN / 32;  // along n
     static constexpr int kPairsPerRow = KB / 2;
@@ -58,6 +65,8 @@ struct Q40Config {
     static_assert(kActPT * kThreads == kActPairs && kWPT * kThreads == kWPairs, "pairs must split evenly over threads");
     static_assert(kActPT >= 1 && kWPT >= 1, "every thread loads at least one pair of each operand");
     static_assert(kAd % 16 == 0 && kWq % 16 == 0 && kWd % 16 == 0, "LDS regions 16-byte aligned");
+    static_assert(kWaveBlocks * WK == KB && kWaveBlocks % 4 == 0, "each wave takes a multiple of 4 blocks");
+    static_assert((WK - 1) * WM * WN * TM * TN * 16 * 64 * 4 <= kLdsBytes, "K-wave reduction fits in LDS");
 };
 
 template <class C>
@@ -159,9 +168,10 @@ __device__ __forceinline__ FragBases frag_bases(const uint8_t *buf, int lane, in
     return b;
 }
 
+// Fragments of block tb + j (tb a multiple of 4, j known at compile time).
 template <class C>
-__device__ __forceinline__ void load_frags(const FragBases &b, int t, int lh, Frags<C> &f) {
-    const int t4 = t & ~3, tt = t & 3;
+__device__ __forceinline__ void load_frags(const FragBases &b, int tb, int j, int lh, Frags<C> &f) {
+    const int t = tb + j, t4 = tb + (j & ~3), tt = j & 3;
 #pragma unroll
     for (int tm = 0; tm < C::TM; ++tm) {
         f.av[tm] = *reinterpret_cast<const i32x4 *>(b.aq + tm * 32 * C::kRowStride + t * 32);
@@ -180,23 +190,35 @@ struct ItemRegs {
     f32x16 p;
 };
 
-// One K stage: KB blocks x TM x TN tiles = a flat list of items, software-
-// pipelined so the MFMAs of item i+1 are in flight while the VALU epilogue of
-// item i runs, and the LDS fragments of block t+1 load during block t.
+// One K stage of one wave: its kWaveBlocks blocks (from tb) x TM x TN tiles
+// = a flat list of items, software-pipelined so the MFMAs of item i+1 are in
+// flight while the VALU epilogue of item i runs, and the LDS fragments of
+// block t+1 load during block t.
 template <class C, bool kIsums>
 __device__ __forceinline__ void compute_stage(const uint8_t *buf, f32x16 (&acc)[C::TM][C::TN], int32_t *isums, int m,
-                                              int n, int nb, int m0, int n0, int s, int lane, int wave_m, int wave_n) {
+                                              int n, int nb, int m0, int n0, int s, int tb, int lane, int wave_m,
+                                              int wave_n) {
     constexpr int kTiles = C::TM * C::TN;
-    constexpr int kItems = C::kKB * kTiles;
+    constexpr int kItems = C::kWaveBlocks * kTiles;
+    // With several tiles per block, the fragments of block t+1 are read while
+    // the items of block t run (two sets). With one tile per block there is no
+    // such slack, so all of the stage's fragments are read up front.
+    constexpr bool kAllFrags = kTiles == 1;
+    constexpr int kSets = kAllFrags ? C::kWaveBlocks : 2;
     const FragBases bases = frag_bases<C>(buf, lane, wave_m, wave_n);
     const int lh = lane >> 5;
-    Frags<C> fr[2];
+    Frags<C> fr[kSets];
     ItemRegs it[2];
-    load_frags<C>(bases, 0, lh, fr[0]);
+    if constexpr (kAllFrags) {
+#pragma unroll
+        for (int j = 0; j < C::kWaveBlocks; ++j) load_frags<C>(bases, tb, j, lh, fr[j]);
+    } else {
+        load_frags<C>(bases, tb, 0, lh, fr[0]);
+    }
     auto issue = [&](int item) {
         const int t = item / kTiles, tile = item % kTiles;
         const int tm = tile / C::TN, tn = tile % C::TN;
-        const Frags<C> &f = fr[t & 1];
+        const Frags<C> &f = fr[kAllFrags ? t : (t & 1)];
         ItemRegs &r = it[item & 1];
         r.s16 = mfma_i8_32x32x32(f.av[tm], f.wv[tn], (i32x16){});
         if constexpr (!kIsums) r.p = mfma_f16_32x32x8(f.ad[tm], f.wd[tn], (f32x16){});
@@ -206,33 +228,42 @@ __device__ __forceinline__ void compute_stage(const uint8_t *buf, f32x16 (&acc)[
     for (int item = 0; item < kItems; ++item) {
         const int t = item / kTiles, tile = item % kTiles;
         const int tm = tile / C::TN, tn = tile % C::TN;
-        if (tile == 0 && t + 1 < C::kKB) load_frags<C>(bases, t + 1, lh, fr[(t + 1) & 1]);
+        if (!kAllFrags && tile == 0 && t + 1 < C::kWaveBlocks) load_frags<C>(bases, tb, t + 1, lh, fr[(t + 1) & 1]);
         if (item + 1 < kItems) issue(item + 1);
+        // keep the order: without the fences the scheduler sinks the MFMAs of
+        // item+1 below this epilogue and reuses their result registers, which
+        // exposes every MFMA's latency
+        __builtin_amdgcn_sched_barrier(0);
         const ItemRegs &r = it[item & 1];
         if constexpr (kIsums) {
             const int col = n0 + wave_n * C::TN * 32 + tn * 32 + (lane & 31);
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 const int row = m0 + wave_m * C::TM * 32 + tm * 32 + mfma_row(lane, q);
-                if (row < m && col < n) isums[((size_t)row * n + col) * nb + s * C::kKB + t] = r.s16[q] / 16;
+                if (row < m && col < n) isums[((size_t)row * n + col) * nb + s * C::kKB + tb + t] = r.s16[q] / 16;
             }
         } else {
 #pragma unroll
             for (int q = 0; q < 16; ++q) acc[tm][tn][q] = fmaf((float)r.s16[q], r.p[q], acc[tm][tn][q]);
         }
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
 // kIsums == false: fp32 C. kIsums == true: int32 block sums (diagnostic).
 template <class C, bool kIsums>
 __global__ __launch_bounds__(C::kThreads, C::kMinWavesPerEU) void gemm_q4_0_kernel(const uint8_t *__restrict__ w,
-                                                               const uint8_t *__restrict__ a, float *__restrict__ c,
-                                                               int32_t *__restrict__ isums, int m, int n, int nb) {
+                                                                                  const uint8_t *__restrict__ a,
+                                                                                  float *__restrict__ c,
+                                                                                  int32_t *__restrict__ isums, int m,
+                                                                                  int n, int nb) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int wave_m = wave / C::kWN;
-    const int wave_n = wave % C::kWN;
+    const int wk = wave / (C::kWM * C::kWN);   // which share of each stage's blocks
+    const int wmn = wave % (C::kWM * C::kWN);  // which TM x TN sub-tile
+    const int wave_m = wmn / C::kWN;
+    const int wave_n = wmn % C::kWN;
     const TileOrigin to = xcd_tile(blockIdx.x, (m + C::kBM - 1) / C::kBM, (n + C::kBN - 1) / C::kBN);
     const int m0 = to.mi * C::kBM, n0 = to.ni * C::kBN;
     const int li = lane & 31;  // operand row / result column within a 32x32 tile
@@ -244,37 +275,65 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWavesPerEU) void gemm_q4_0_kern
         for (int j = 0; j < C::TN; ++j) acc[i][j] = (f32x16){};
 
     // Double-buffered LDS with one barrier per stage: stage s is computed from
-    // buffer s % 2 while the registers of stage s+1 (loaded kRing stages ago)
-    // are stored into the other buffer and the loads of stage s+1+kRing are
-    // issued. Stores and loads are unconditional (clamped stage index) so the
-    // loop body has no divergent control flow.
+    // one buffer while the registers of stage s+1 (loaded a stage earlier) are
+    // stored into the other and the loads of stage s+2 are issued. Stores and
+    // loads are unconditional (clamped stage index), so the loop body has no
+    // divergent control flow.
+    // regs[r] holds stage s+1 while stage s (s % kDepth == r) is computed.
     const int stages = nb / C::kKB;
     auto clampst = [&](int st) { return st < stages ? st : stages - 1; };
-    StageRegs<C> regs[C::kRing];
+    StageRegs<C> regs[C::kDepth];
     load_stage<C>(a, w, m, n, nb, m0, n0, 0, regs[0]);
     store_stage<C>(lds, regs[0]);
 #pragma unroll
-    for (int r = 0; r < C::kRing; ++r) load_stage<C>(a, w, m, n, nb, m0, n0, clampst(1 + r) * C::kKB, regs[r]);
+    for (int r = 0; r < C::kDepth; ++r) load_stage<C>(a, w, m, n, nb, m0, n0, clampst(1 + r) * C::kKB, regs[r]);
     __syncthreads();
-    auto step = [&](int s, StageRegs<C> &rg) {
-        const uint8_t *cur = lds + (s & 1) * C::kBufBytes;
-        __builtin_amdgcn_sched_barrier(0);
-        compute_stage<C, kIsums>(cur, acc, isums, m, n, nb, m0, n0, s, lane, wave_m, wave_n);
-        __builtin_amdgcn_sched_barrier(0);
-        store_stage<C>(lds + ((s + 1) & 1) * C::kBufBytes, rg);
-        __builtin_amdgcn_sched_barrier(0);
-        load_stage<C>(a, w, m, n, nb, m0, n0, clampst(s + 1 + C::kRing) * C::kKB, rg);
-        __builtin_amdgcn_sched_barrier(0);
-        __syncthreads();
-    };
-    // the dispatcher guarantees stages % kRing == 0, so each ring slot is
-    // consumed in a fixed position of the unrolled body
-    for (int s = 0; s < stages; s += C::kRing) {
+    for (int s0 = 0; s0 < stages; s0 += C::kDepth) {
 #pragma unroll
-        for (int r = 0; r < C::kRing; ++r) step(s + r, regs[r]);
+        for (int r = 0; r < C::kDepth; ++r) {
+            const int s = s0 + r;
+            if (C::kDepth > 1 && s >= stages) break;  // uniform across the workgroup
+            const int buf = s & 1;
+            __builtin_amdgcn_sched_barrier(0);
+            compute_stage<C, kIsums>(lds + buf * C::kBufBytes, acc, isums, m, n, nb, m0, n0, s, wk * C::kWaveBlocks,
+                                     lane, wave_m, wave_n);
+            __builtin_amdgcn_sched_barrier(0);
+            store_stage<C>(lds + (buf ^ 1) * C::kBufBytes, regs[r]);
+            __builtin_amdgcn_sched_barrier(0);
+            load_stage<C>(a, w, m, n, nb, m0, n0, clampst(s + 1 + C::kDepth) * C::kKB, regs[r]);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+        }
     }
 
     if constexpr (!kIsums) {
+        if constexpr (C::kWK > 1) {
+            // add the other K-waves' partials to wave wk == 0's, in wave order;
+            // the stage buffers are free after the loop's last barrier
+            constexpr int kRegs = C::TM * C::TN * 16;
+            float *red = reinterpret_cast<float *>(lds);
+            if (wk > 0) {
+                float *dst = red + ((wk - 1) * C::kWM * C::kWN + wmn) * kRegs * 64 + lane;
+#pragma unroll
+                for (int tm = 0; tm < C::TM; ++tm)
+#pragma unroll
+                    for (int tn = 0; tn < C::TN; ++tn)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) dst[((tm * C::TN + tn) * 16 + r) * 64] = acc[tm][tn][r];
+            }
+            __syncthreads();
+            if (wk > 0) return;
+#pragma unroll
+            for (int w2 = 1; w2 < C::kWK; ++w2) {
+                const float *src = red + ((w2 - 1) * C::kWM * C::kWN + wmn) * kRegs * 64 + lane;
+#pragma unroll
+                for (int tm = 0; tm < C::TM; ++tm)
+#pragma unroll
+                    for (int tn = 0; tn < C::TN; ++tn)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[tm][tn][r] += src[((tm * C::TN + tn) * 16 + r) * 64];
+            }
+        }
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
@@ -302,11 +361,18 @@ hipError_t launch_q4_0(const void *w, const void *a, float *c, int32_t *isums, i
 }
 
 // large problems: 128x128 tiles, 4 waves of 64x64, 4 blocks per stage
-using Q40Big = Q40Config<128, 128, 2, 2, 4, 1>;
-// small problems: 64x64 tiles, 4 waves of 32x32, 8 blocks per stage
-using Q40Small = Q40Config<64, 64, 2, 2, 8, 1>;
-// small problems with k % 256 != 0: 64x64 tiles, 2 waves of 64x32, 4 blocks per stage
-using Q40Small4 = Q40Config<64, 64, 1, 2, 4, 1>;
+using Q40Big = Q40Config<128, 128, 2, 2, 4>;
+// medium problems: 64x64 tiles, 4 waves of 32x32, 8 blocks per stage
+using Q40Small = Q40Config<64, 64, 2, 2, 8>;
+// medium problems with k % 256 != 0: 64x64 tiles, 2 waves of 64x32, 4 blocks per stage
+using Q40Small4 = Q40Config<64, 64, 1, 2, 4>;
+// small problems: 32x32 tiles, 2 waves each taking 4 of the stage's 8 blocks,
+// loads three stages ahead
+using Q40Tiny = Q40Config<32, 32, 1, 1, 8, 2, 3>;
+
+enum { kCfgBig = 0, kCfgSmall = 1, kCfgSmall4 = 2, kCfgTiny = 3 };
+
+int64_t tiles_of(int64_t m, int64_t n, int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); }
 
 }  // namespace
 
@@ -317,21 +383,40 @@ bool mfma_supported(int type, int64_t m, int64_t k) {
     return (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K || type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K) && k % 256 == 0;
 }
 
+// Tile choice: the largest tile that still gives at least two workgroups per
+// CU (to hide latency, each CU needs several resident waves), else the 32x32
+// tile whose two K-waves double the waves per output.
+MfmaPlan plan_mfma(int type, int64_t m, int64_t n, int64_t k, int cus) {
+    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return plan_kquant(type, m, n, k, cus);
+    MfmaPlan p;
+    const int64_t enough = 2 * (int64_t)cus;
+    if (tiles_of(m, n, 128, 128) >= enough) {
+        p.config = kCfgBig;
+    } else if (k % (32 * Q40Small::kKB) != 0) {
+        p.config = kCfgSmall4;
+    } else if (tiles_of(m, n, 64, 64) >= enough) {
+        p.config = kCfgSmall;
+    } else {
+        p.config = kCfgTiny;
+    }
+    return p;
+}
+
 hipError_t launch_mfma_mul_mat(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
-                               hipStream_t stream) {
-    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return launch_kquant_mul_mat(type, w, a, c, m, n, k, stream);
-    const int64_t big_tiles = ((m + 127) / 128) * ((n + 127) / 128);
-    // a two-slot ring needs an even number of K stages
-    if (big_tiles >= 512 && k % (Q40Big::kRing * 32 * Q40Big::kKB) == 0)
-        return launch_q4_0<Q40Big, false>(w, a, c, nullptr, m, n, k, stream);
-    if (k % (Q40Small::kRing * 32 * Q40Small::kKB) == 0)
-        return launch_q4_0<Q40Small, false>(w, a, c, nullptr, m, n, k, stream);
-    return launch_q4_0<Q40Small4, false>(w, a, c, nullptr, m, n, k, stream);
+                               const MfmaPlan &plan, hipStream_t stream) {
+    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return launch_kquant_mul_mat(type, w, a, c, m, n, k, plan, stream);
+    switch (plan.config) {
+    case kCfgBig: return launch_q4_0<Q40Big, false>(w, a, c, nullptr, m, n, k, stream);
+    case kCfgSmall: return launch_q4_0<Q40Small, false>(w, a, c, nullptr, m, n, k, stream);
+    case kCfgTiny: return launch_q4_0<Q40Tiny, false>(w, a, c, nullptr, m, n, k, stream);
+    default: return launch_q4_0<Q40Small4, false>(w, a, c, nullptr, m, n, k, stream);
+    }
 }
 
 hipError_t launch_mfma_block_isums(int type, const void *w, const void *a, int32_t *out, int64_t m, int64_t n,
                                    int64_t k, hipStream_t stream) {
     if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return launch_kquant_block_isums(type, w, a, out, m, n, k, stream);
+    if (k % (32 * Q40Tiny::kKB) == 0) return launch_q4_0<Q40Tiny, true>(w, a, nullptr, out, m, n, k, stream);
     return launch_q4_0<Q40Small4, true>(w, a, nullptr, out, m, n, k, stream);
 }
 

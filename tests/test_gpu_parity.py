@@ -301,3 +301,53 @@ def test_config3_iq2_xxs_full_size_sampled(hip, torch_gpu, oracle):
     got_p = hip.mul_mat(2, wt, aq_t[perm].contiguous(), m, n, k)
     torch.cuda.synchronize()
     assert torch.equal(got_p, got[perm])
+
+
+# ------------------------------------------------- small-shape configs ----
+
+@pytest.mark.parametrize("qtype,m,n,k", [(0, 480, 1536, 1536), (0, 9, 300, 640), (0, 200, 130, 1024),
+                                         (0, 33, 65, 256), (1, 480, 1536, 1536), (1, 100, 77, 512),
+                                         (2, 130, 200, 2048), (2, 31, 33, 256)])
+def test_small_shapes_deterministic_and_correct(hip, torch_gpu, oracle, qtype, m, n, k):
+    """Shapes that take the 32x32-tile configurations (two waves share each
+    stage's blocks and add their partials through LDS): within tolerance, and
+    bit-identical across repeated launches and after a launch of another shape."""
+    torch = torch_gpu
+    say(f"small shape type={qtype} {m}x{n}x{k}")
+    act, w = oracle.create_input(qtype, m, n, k, seed=m + n + k + qtype)
+    aq = oracle.quantize_activation(qtype, act)
+    wt, at = dev(torch, w), dev(torch, aq)
+    first = hip.mul_mat(qtype, wt, at, m, n, k, path=hip.PATH_MFMA)
+    torch.cuda.synchronize()
+    check_close(oracle, qtype, first.cpu().numpy(), w, aq, m, n, k, label=f"small type={qtype} {m}x{n}x{k}")
+    for _ in range(3):
+        again = hip.mul_mat(qtype, wt, at, m, n, k, path=hip.PATH_MFMA)
+    act2, w2 = oracle.create_input(qtype, 64, 96, k, seed=3)
+    hip.mul_mat(qtype, dev(torch, w2), dev(torch, oracle.quantize_activation(qtype, act2)), 64, 96, k,
+                path=hip.PATH_MFMA)
+    last = hip.mul_mat(qtype, wt, at, m, n, k, path=hip.PATH_MFMA)
+    torch.cuda.synchronize()
+    assert torch.equal(first, again) and torch.equal(first, last)
+
+
+def test_mfma_in_graph_replays(hip, torch_gpu, oracle):
+    """c0 captured into a graph: every replay equals the eager result."""
+    torch = torch_gpu
+    m, n, k = 480, 1536, 1536
+    say("graph replay c0")
+    act, w = oracle.create_input(0, m, n, k, seed=1)
+    wt, at = dev(torch, w), dev(torch, oracle.quantize_q8_0(act))
+    s = torch.cuda.Stream()
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    with torch.cuda.stream(s):
+        hip.mul_mat(0, wt, at, m, n, k, out=out)
+    s.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        hip.mul_mat(0, wt, at, m, n, k, out=out)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
