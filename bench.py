@@ -10,6 +10,8 @@ One step = one pass of the hot path over one batch of synthetic input:
   * gemm    : config 0 — q4_0 x q8_0 GEMM, M=480 N=1536 K=1536, TOPS = 2*M*N*K/s,
               the other half of the compound metric.
   * q4_K, iq2_xxs, prefill: configs 2, 3 and 4 in the same form.
+  * gemv_q4_K, gemv_iq2_xxs: the M=1 GEMV of the super-block formats at
+    N=K=4096 (not baseline configs; reported beside the headline).
 Inputs come from the product's own generator (pfng_host_create_input, the
 reference harness's mt19937 draws and host quantizers). Activations are
 quantized once before the timed region (the reference quantizes in prepare(),
@@ -193,6 +195,33 @@ def verify_against_naive(torch, pkg, qtype, w_t, aq_t, m, n, k, got, rows=None):
             "max_rel": float(rel.max().item())}
 
 
+def gemv_item(torch, pkg, label, qtype, m, n, k, steps, warmup, variant, kernel, copies=32):
+    """One GEMV configuration: GB/s of algorithmic bytes over `steps` launches
+    rotating over `copies` weight copies (so the weights stream from HBM)."""
+    act, w = pkg.create_input(qtype, m, n, k, seed=1, variant=variant)
+    base = upload_weights(torch, w)
+    weights = [base] + [base.clone() for _ in range(copies - 1)]
+    aq = pkg.quantize_activation(qtype, torch.from_numpy(act).cuda())
+    outs = [torch.empty((m, n), dtype=torch.float32, device="cuda") for _ in range(copies)]
+    torch.cuda.synchronize()
+    g = capture(torch, lambda i: pkg.mul_mat(qtype, weights[i % copies], aq, m, n, k, out=outs[i % copies]), copies)
+    wall, ev_ms, steps_run = time_graph(torch, g, copies, steps, warmup)
+    qk, wb, ab = pkg.QK[qtype], pkg.WEIGHT_BLOCK_BYTES[qtype], pkg.ACT_BLOCK_BYTES[qtype]
+    per_call = n * (k // qk) * wb + m * (k // qk) * ab + m * n * 4
+    k_us = ev_ms * 1e3 / steps_run
+    achieved = per_call / (k_us * 1e-6) / 1e9
+    ver = verify_against_naive(torch, pkg, qtype, weights[0], aq, m, n, k, outs[0])
+    item = {"workload": label, "value": round(per_call * steps_run / wall / 1e9, 2), "unit": "GB/s",
+            "steps": steps_run, "ms_per_step": round(wall * 1e3 / steps_run, 6), "verify": ver,
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for(kernel, label),
+                         "kernel": kernel, "kernel_us": round(k_us, 4), "bytes_per_launch": per_call}}
+    log(f"[bench] {label}: {steps_run} steps, kernel {k_us:.3f} us -> {achieved:.1f} GB/s, verify={ver['passed']}")
+    del g, weights, outs
+    torch.cuda.empty_cache()
+    return item
+
+
 def gemm_item(torch, pkg, label, qtype, m, n, k, steps, warmup, variant, kernel, rows_to_verify=None):
     """One GEMM configuration: TOPS over `steps` graph-replayed launches."""
     act, w = pkg.create_input(qtype, m, n, k, seed=1, variant=variant)
@@ -291,11 +320,15 @@ def main():
         prefill = gemm_item(torch, pkg, "c4: q4_0 x q8_0 GEMM M=2048 N=11008 K=4096", 0, 2048, 11008, 4096,
                             args.prefill_steps, 8, pkg.INPUT_REFERENCE, "gemm_q4_0_kernel", rows_to_verify=256)
 
+    gemv_kq = [gemv_item(torch, pkg, f"{name} x q8_K GEMV M=1 N=4096 K=4096, 32 rotating weight copies", qt, 1, 4096,
+                         4096, args.steps // 4, args.warmup // 4, variant, f"gemv_{name}_kernel<1>")
+               for qt, name, variant in ((1, "q4_K", pkg.INPUT_REFERENCE), (2, "iq2_xxs", pkg.INPUT_BASELINE))]
+
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
     if cpu:
         log(f"[bench] cpu baseline: {cpu}")
 
-    items = [x for x in (gemm, q4k, iq2, prefill) if x is not None]
+    items = [x for x in (gemm, q4k, iq2, prefill, *gemv_kq) if x is not None]
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -321,6 +354,8 @@ def main():
         "q4_K": q4k,
         "iq2_xxs": iq2,
         "prefill": prefill,
+        "gemv_q4_K": gemv_kq[0],
+        "gemv_iq2_xxs": gemv_kq[1],
         "verified": bool(ver1["passed"] and all(x["verify"]["passed"] for x in items)),
         "cpu_baseline": cpu,
     }

@@ -44,8 +44,9 @@ typedef enum {
 /* Matrix-product implementations; PFNG_PATH_AUTO picks per shape. */
 typedef enum {
     PFNG_PATH_AUTO = 0,
-    PFNG_PATH_GEMV = 1,  /* wavefront-per-row GEMV, no MFMA: q4_0, m <= 8,
-                            k % 64 == 0 for m == 1, k % 256 == 0 otherwise */
+    PFNG_PATH_GEMV = 1,  /* wavefront-per-row GEMV, no MFMA, m <= 8: q4_0 with
+                            k % 64 == 0 for m == 1, k % 256 == 0 otherwise;
+                            q4_K and iq2_xxs for every k % 256 == 0 */
     PFNG_PATH_MFMA = 2,  /* int8-MFMA GEMM, LDS-staged tiles: q4_0 with k % 128 == 0,
                             q4_K and iq2_xxs for every k % 256 == 0 */
     PFNG_PATH_NAIVE = 3  /* one thread per output, the reference's exact fp32 order */

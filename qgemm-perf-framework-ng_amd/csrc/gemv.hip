@@ -249,12 +249,13 @@ hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n,
 bool gemv_supported(int type, int64_t m, int64_t k) {
     if (m < 1 || m > 8) return false;
     if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return m == 1 ? k % 64 == 0 : k % 256 == 0;
-    return false;
+    // q4_K and iq2_xxs (gemv_kquant.hip) take every k % 256 == 0
+    return (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K || type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K) && k % 256 == 0;
 }
 
 hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                        hipStream_t stream) {
-    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return hipErrorInvalidValue;
+    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return launch_kquant_gemv(type, w, a, c, m, n, k, stream);
     switch (m) {
     case 1: {
         const int grid = (int)((n + kThreads / 64 - 1) / (kThreads / 64));

@@ -1,0 +1,232 @@
+// GEMV path (m <= 8) for the super-block formats against q8_K activations:
+// q4_K (llama_reference.cpp:113-132) and iq2_xxs (llama_reference.cpp:148-161,
+// kernels/common/iq2_xxs.h:29-41). No MFMA: one wavefront per weight row,
+// the weight stream read with aligned 16-byte (q4_K) or realigned dword
+// (iq2_xxs, 66-byte blocks) loads, all loads of a step issued before any
+// arithmetic, int8 dots with v_dot4_i32_i8.
+//
+// q4_K: four lanes per super-block, lane e owning sub-blocks 2e and 2e+1 (the
+// 32 nibble bytes qs[32e .. 32e+32): low nibbles of sub-block 2e, high of
+// 2e+1). Its part ad * (d * (sc_2e S_2e + sc_2e+1 S_2e+1) - dmin * (m_2e B_2e +
+// m_2e+1 B_2e+1)) with B_j the two bsums of sub-block j is exact up to the
+// final fp32 steps (the accuracy bound of this format is per element).
+// iq2_xxs: eight lanes per super-block, one sub-block each; the eight integer
+// parts (2 s_j + 1) * S_j are added across the lanes first, so the super-block
+// sum is complete and exact before it is scaled by 0.125 * d * ad (the bound
+// of this format is per super-block).
+#include "device_common.h"
+#include "kernels.h"
+#include "pfng_iq2xxs_grid.h"
+
+namespace pfng {
+
+namespace {
+
+constexpr int kThreads = 256;  // four rows per workgroup, one per wave
+constexpr int kQ8KBytes = 292, kQ4KBytes = 144, kIq2Bytes = 66;
+
+__constant__ uint16_t kIq2GridCodes[256] = PFNG_IQ2XXS_GRID_CODES_INIT;
+
+__device__ __forceinline__ int dot8(const uint32_t *w, const uint32_t *x) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s = __builtin_amdgcn_sdot4((int)w[i], (int)x[i], s, false);
+    return s;
+}
+
+// Scale and min of q4_K sub-block j from the 12 packed bytes (dwords 1..3 of
+// the block header), with the reference's decode (llama_reference.cpp:116-121).
+__device__ __forceinline__ void q4_K_scale_min(const uint4 &hd, int j, int &sc, int &mn) {
+    const uint32_t words[3] = {hd.y, hd.z, hd.w};
+    auto byte = [&](int i) { return (int)((words[i / 4] >> (8 * (i % 4))) & 0xffu); };
+    if (j < 4) {
+        sc = byte(j) & 63;
+        mn = byte(j + 4) & 63;
+    } else {
+        sc = (byte(j + 4) & 15) | ((byte(j - 4) >> 6) << 4);
+        mn = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+    }
+}
+
+template <int M>
+__global__ __launch_bounds__(kThreads) void gemv_q4_K_kernel(const uint8_t *__restrict__ w,
+                                                            const uint8_t *__restrict__ a, float *__restrict__ c,
+                                                            int n, int nb) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int lrow = row < n ? row : n - 1;  // clamped: loads stay unconditional, the store is guarded
+    const int slot = lane >> 2, e = lane & 3;
+    float acc[M];
+#pragma unroll
+    for (int mi = 0; mi < M; ++mi) acc[mi] = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += 16) {
+        const int b = b0 + slot;
+        const bool valid = b < nb;
+        const int lb = valid ? b : nb - 1;
+        const uint8_t *blk = w + ((size_t)lrow * nb + lb) * kQ4KBytes;
+        const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
+        const uint4 qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * e);
+        const uint4 qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * e);
+        uint32_t x[M][16], bs[M][2];
+        float ad[M];
+#pragma unroll
+        for (int mi = 0; mi < M; ++mi) {
+            const uint8_t *ab = a + ((size_t)mi * nb + lb) * kQ8KBytes;
+            const uint32_t *xs = reinterpret_cast<const uint32_t *>(ab + 4 + 64 * e);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) x[mi][i] = xs[i];
+            const uint32_t *bp = reinterpret_cast<const uint32_t *>(ab + 260 + 8 * e);
+            bs[mi][0] = bp[0];
+            bs[mi][1] = bp[1];
+            ad[mi] = *reinterpret_cast<const float *>(ab);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            lo[i] = q[i] & 0x0f0f0f0fu;
+            hi[i] = (q[i] >> 4) & 0x0f0f0f0fu;
+        }
+        int sc0, m0, sc1, m1;
+        q4_K_scale_min(hd, 2 * e, sc0, m0);
+        q4_K_scale_min(hd, 2 * e + 1, sc1, m1);
+        const float d = fp16_to_f32(hd.x & 0xffffu), dmin = fp16_to_f32(hd.x >> 16);
+#pragma unroll
+        for (int mi = 0; mi < M; ++mi) {
+            const int is = sc0 * dot8(lo, x[mi]) + sc1 * dot8(hi, x[mi] + 8);
+            const int b0s = (int)(int16_t)(bs[mi][0] & 0xffffu) + (int)(int16_t)(bs[mi][0] >> 16);
+            const int b1s = (int)(int16_t)(bs[mi][1] & 0xffffu) + (int)(int16_t)(bs[mi][1] >> 16);
+            const int im = m0 * b0s + m1 * b1s;
+            const float part = ad[mi] * fmaf(-dmin, (float)im, d * (float)is);
+            acc[mi] += valid ? part : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int mi = 0; mi < M; ++mi) acc[mi] = group_sumf<64>(acc[mi]);
+    if (row < n && lane < M) {
+        float v = acc[0];
+#pragma unroll
+        for (int mi = 1; mi < M; ++mi) v = lane == mi ? acc[mi] : v;
+        c[(size_t)lane * n + row] = v;
+    }
+}
+
+template <int M>
+__global__ __launch_bounds__(kThreads) void gemv_iq2_xxs_kernel(const uint8_t *__restrict__ w,
+                                                               const uint8_t *__restrict__ a, float *__restrict__ c,
+                                                               int n, int nb) {
+    __shared__ __align__(16) uint8_t grid[256 * 8];
+    // grid magnitudes (kernels/iq2_xxs-q8_K-RVV-common/ggml_min.h:69-134): two
+    // bits per byte select 8, 25 or 43
+    {
+        const uint32_t code = kIq2GridCodes[threadIdx.x];
+        uint32_t v[2] = {0, 0};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t c2 = (code >> (2 * j)) & 3u;
+            v[j / 4] |= (c2 == 0 ? 8u : (c2 == 1 ? 25u : 43u)) << (8 * (j % 4));
+        }
+        *reinterpret_cast<uint2 *>(grid + 8 * threadIdx.x) = make_uint2(v[0], v[1]);
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int lrow = row < n ? row : n - 1;
+    const int slot = lane >> 3, j = lane & 7;
+    float acc[M];
+#pragma unroll
+    for (int mi = 0; mi < M; ++mi) acc[mi] = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += 8) {
+        const int b = b0 + slot;
+        const bool valid = b < nb;
+        const int lb = valid ? b : nb - 1;
+        // 66-byte blocks are 2-byte aligned: the covering dwords plus a
+        // trailing half-word, never past the sub-block's last byte
+        const size_t base = ((size_t)lrow * nb + lb) * kIq2Bytes;
+        const size_t o = base + 2 + 8 * j;
+        const uint32_t *p4 = reinterpret_cast<const uint32_t *>(w + (o & ~(size_t)3));
+        const uint32_t d0 = p4[0], d1 = p4[1];
+        const uint32_t tail = *reinterpret_cast<const uint16_t *>(w + o + 6);
+        const uint32_t dh = *reinterpret_cast<const uint16_t *>(w + base);
+        uint32_t x[M][8];
+        float ad[M];
+#pragma unroll
+        for (int mi = 0; mi < M; ++mi) {
+            const uint8_t *ab = a + ((size_t)mi * nb + lb) * kQ8KBytes;
+            const uint32_t *xs = reinterpret_cast<const uint32_t *>(ab + 4 + 32 * j);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[mi][i] = xs[i];
+            ad[mi] = *reinterpret_cast<const float *>(ab);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const bool sh = (o & 3) != 0;
+        const uint32_t gidx = sh ? __builtin_amdgcn_alignbyte(d1, d0, 2) : d0;
+        const uint32_t ss = sh ? ((d1 >> 16) | (tail << 16)) : d1;
+        // decode: magnitudes from the grid, sign bit i of group g is bit i of
+        // (idx | parity(idx) << 7), idx the 7-bit field g of ss; magnitudes are
+        // >= 8, so (x ^ 0xff) + 1 negates a byte without a carry
+        uint32_t v[8];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint2 mag = *reinterpret_cast<const uint2 *>(grid + ((gidx >> (8 * g)) & 0xffu) * 8);
+            const uint32_t idx = (ss >> (7 * g)) & 0x7fu;
+            const uint32_t sgn = idx | ((__builtin_popcount(idx) & 1u) << 7);
+            const uint32_t s0 = ((sgn & 0xfu) * 0x00204081u) & 0x01010101u;
+            const uint32_t s1 = (((sgn >> 4) & 0xfu) * 0x00204081u) & 0x01010101u;
+            v[2 * g] = (mag.x ^ (s0 * 0xffu)) + s0;
+            v[2 * g + 1] = (mag.y ^ (s1 * 0xffu)) + s1;
+        }
+        const int scale = 2 * (int)(ss >> 28) + 1;
+        const float t0 = 0.125f * fp16_to_f32(dh);
+#pragma unroll
+        for (int mi = 0; mi < M; ++mi) {
+            // exact integer sum of the super-block over its eight lanes
+            const int is = group_sum<8>(scale * dot8(v, x[mi]));
+            if (j == 0 && valid) acc[mi] += (t0 * ad[mi]) * (float)is;
+        }
+    }
+#pragma unroll
+    for (int mi = 0; mi < M; ++mi) acc[mi] = group_sumf<64>(acc[mi]);
+    if (row < n && lane < M) {
+        float v = acc[0];
+#pragma unroll
+        for (int mi = 1; mi < M; ++mi) v = lane == mi ? acc[mi] : v;
+        c[(size_t)lane * n + row] = v;
+    }
+}
+
+template <int M>
+hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int64_t n, int64_t k,
+                          hipStream_t stream) {
+    const dim3 grid((unsigned)((n + kThreads / 64 - 1) / (kThreads / 64)));
+    const auto *wp = static_cast<const uint8_t *>(w);
+    const auto *ap = static_cast<const uint8_t *>(a);
+    if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K)
+        hipLaunchKernelGGL(gemv_q4_K_kernel<M>, grid, dim3(kThreads), 0, stream, wp, ap, c, (int)n, (int)(k / 256));
+    else
+        hipLaunchKernelGGL(gemv_iq2_xxs_kernel<M>, grid, dim3(kThreads), 0, stream, wp, ap, c, (int)n,
+                           (int)(k / 256));
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
+                              hipStream_t stream) {
+    if (type != PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K && type != PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K)
+        return hipErrorInvalidValue;
+    switch (m) {
+    case 1: return launch_kq_gemv<1>(type, w, a, c, n, k, stream);
+    case 2: return launch_kq_gemv<2>(type, w, a, c, n, k, stream);
+    case 3: return launch_kq_gemv<3>(type, w, a, c, n, k, stream);
+    case 4: return launch_kq_gemv<4>(type, w, a, c, n, k, stream);
+    case 5: return launch_kq_gemv<5>(type, w, a, c, n, k, stream);
+    case 6: return launch_kq_gemv<6>(type, w, a, c, n, k, stream);
+    case 7: return launch_kq_gemv<7>(type, w, a, c, n, k, stream);
+    case 8: return launch_kq_gemv<8>(type, w, a, c, n, k, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace pfng

@@ -15,10 +15,12 @@ hipError_t launch_quantize_q8_K(const float *x, void *y, int64_t rows, int64_t k
 hipError_t launch_naive_mul_mat(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                                 hipStream_t stream);
 
-// gemv.hip — m <= 8
+// gemv.hip (q4_0) and gemv_kquant.hip (q4_K, iq2_xxs) — m <= 8
 bool gemv_supported(int type, int64_t m, int64_t k);
 hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                        hipStream_t stream);
+hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
+                              hipStream_t stream);
 
 // Launch plan of the MFMA GEMMs: the tile configuration for the shape.
 struct MfmaPlan {

@@ -173,7 +173,8 @@ ValidationResult validate(const BenchmarkRequest &r) {
     if (!v.supported) return v;
     if constexpr (Path == PFNG_PATH_GEMV) {
         if (r.m > 8) return {false, "the GEMV path takes M <= 8"};
-        if (r.m == 1 ? r.k % 64 : r.k % 256) return {false, "the GEMV path needs K % 64 == 0 (M = 1) or K % 256 == 0"};
+        if (T == QuantizationType::WeightQ4_0ActivationQ8_0 && (r.m == 1 ? r.k % 64 : r.k % 256))
+            return {false, "the q4_0 GEMV path needs K % 64 == 0 (M = 1) or K % 256 == 0"};
     }
     if constexpr (Path == PFNG_PATH_MFMA && T == QuantizationType::WeightQ4_0ActivationQ8_0) {
         if (r.k % 128) return {false, "the q4_0 MFMA path needs K % 128 == 0"};
@@ -206,14 +207,14 @@ void register_q4_0_hip_mi355x() {
 }
 
 void register_q4_K_hip_mi355x() {
-    add<QT::WeightQ4_KActivationQ8_K, PFNG_PATH_AUTO>("q4_K-q8_K-HIP-mi355x", "Q4_K/Q8_K HIP gfx950 int8 MFMA GEMM");
+    add<QT::WeightQ4_KActivationQ8_K, PFNG_PATH_AUTO>("q4_K-q8_K-HIP-mi355x", "Q4_K/Q8_K HIP gfx950 (GEMV for M<=8, int8 MFMA otherwise)");
     add<QT::WeightQ4_KActivationQ8_K, PFNG_PATH_NAIVE>("q4_K-q8_K-HIP-naive",
                                                        "Q4_K/Q8_K HIP thread-per-output, reference fp32 order");
 }
 
 void register_iq2_xxs_hip_mi355x() {
     add<QT::WeightIQ2_XXSActivationQ8_K, PFNG_PATH_AUTO>("iq2_xxs-q8_K-HIP-mi355x",
-                                                         "IQ2_XXS/Q8_K HIP gfx950 int8 MFMA GEMM");
+                                                         "IQ2_XXS/Q8_K HIP gfx950 (GEMV for M<=8, int8 MFMA otherwise)");
     add<QT::WeightIQ2_XXSActivationQ8_K, PFNG_PATH_NAIVE>("iq2_xxs-q8_K-HIP-naive",
                                                           "IQ2_XXS/Q8_K HIP thread-per-output, reference fp32 order");
 }

@@ -351,3 +351,32 @@ def test_mfma_in_graph_replays(hip, torch_gpu, oracle):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+# ------------------------------------------------------- q4_K / iq2_xxs GEMV ----
+
+@pytest.mark.parametrize("qtype", [1, 2])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (257, 1536), (64, 256), (33, 8192)])
+def test_gemv_kquant(hip, torch_gpu, oracle, qtype, m, n, k):
+    torch = torch_gpu
+    say(f"gemv type={qtype} m={m} n={n} k={k}")
+    act, w = oracle.create_input(qtype, m, n, k, seed=m * 31 + n + qtype)
+    aq = oracle.quantize_q8_K(act)
+    got = run_mul_mat(hip, torch, qtype, w, aq, m, n, k, hip.PATH_GEMV)
+    check_close(oracle, qtype, got, w, aq, m, n, k, label=f"gemv type={qtype} m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("qtype", [1, 2])
+def test_gemv_kquant_random_bytes_and_extremes(hip, torch_gpu, oracle, qtype):
+    torch = torch_gpu
+    m, n, k = 4, 130, 2304
+    say(f"gemv random bytes type={qtype}")
+    w = random_weight_blocks(oracle, qtype, n, k, seed=41 + qtype)
+    for aq in (oracle.quantize_q8_K(oracle.create_input(qtype, m, 1, k, seed=2)[0]),
+               extreme_activation(oracle, m, k, seed=5)):
+        got = run_mul_mat(hip, torch, qtype, w, aq, m, n, k, hip.PATH_GEMV)
+        check_close(oracle, qtype, got, w, aq, m, n, k, label=f"gemv random bytes type={qtype}")
+        # the automatic path takes the GEMV for m <= 8
+        auto = run_mul_mat(hip, torch, qtype, w, aq, m, n, k, hip.PATH_AUTO)
+        assert np.array_equal(auto, got)
