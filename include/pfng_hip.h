@@ -94,6 +94,17 @@ int pfng_hip_mul_mat_iq2_xxs_q8_K(const void *weight, const void *act_q8_K, floa
 int pfng_hip_mul_mat(int type, const void *weight, const void *act_q, float *out, int64_t m, int64_t n, int64_t k,
                      int path, void *stream);
 
+/* ---- weight quantizers (setup; the reference runs them on the host) ------ */
+
+/* Replaces quantize_row_q4_0 (llama_reference.cpp:13-36) per row: x is
+ * rows x k fp32 (row-major, 16-byte aligned), y receives rows * k/32
+ * block_q4_0 (2-byte aligned), byte-identical to the reference. */
+int pfng_hip_quantize_q4_0(const float *x, void *y, int64_t rows, int64_t k, void *stream);
+
+/* Replaces quantize_row_q4_K (llama_reference.cpp:72-111, with its
+ * non-upstream scale packing :97-101) per row; y 16-byte aligned. */
+int pfng_hip_quantize_q4_K(const float *x, void *y, int64_t rows, int64_t k, void *stream);
+
 /* ---- end to end: llama_reference::compute on the GPU -------------------- */
 
 /* Bytes of device workspace pfng_hip_compute needs for the quantized activations. */

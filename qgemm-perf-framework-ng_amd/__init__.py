@@ -56,7 +56,8 @@ def lib() -> ctypes.CDLL:
         L.pfng_hip_last_error.restype = ctypes.c_char_p
         L.pfng_hip_version.restype = ctypes.c_char_p
         L.pfng_hip_device_check.argtypes = [ctypes.c_char_p, sz, ctypes.POINTER(ctypes.c_int)]
-        for name in ("pfng_hip_quantize_q8_0", "pfng_hip_quantize_q8_K"):
+        for name in ("pfng_hip_quantize_q8_0", "pfng_hip_quantize_q8_K", "pfng_hip_quantize_q4_0",
+                     "pfng_hip_quantize_q4_K"):
             getattr(L, name).argtypes = [vp, vp, i64, i64, vp]
         for name in ("pfng_hip_mul_mat_q4_0_q8_0", "pfng_hip_mul_mat_q4_K_q8_K", "pfng_hip_mul_mat_iq2_xxs_q8_K"):
             getattr(L, name).argtypes = [vp, vp, vp, i64, i64, i64, ci, vp]
@@ -80,7 +81,7 @@ def lib() -> ctypes.CDLL:
 # C-ABI symbols declared in include/pfng_hip.h
 EXPORTED_SYMBOLS = (
     "pfng_hip_last_error", "pfng_hip_version", "pfng_hip_device_check",
-    "pfng_hip_quantize_q8_0", "pfng_hip_quantize_q8_K",
+    "pfng_hip_quantize_q8_0", "pfng_hip_quantize_q8_K", "pfng_hip_quantize_q4_0", "pfng_hip_quantize_q4_K",
     "pfng_hip_mul_mat_q4_0_q8_0", "pfng_hip_mul_mat_q4_K_q8_K", "pfng_hip_mul_mat_iq2_xxs_q8_K",
     "pfng_hip_mul_mat", "pfng_hip_compute_workspace_size", "pfng_hip_compute", "pfng_hip_block_isums",
 )
@@ -174,6 +175,18 @@ def quantize_q8_0(x, out=None, stream=None):
     if out is None:
         out = torch.empty((rows, (k // 32) * 34), dtype=torch.uint8, device=x.device)
     check(lib().pfng_hip_quantize_q8_0(_p(x), _p(out), rows, k, _stream(stream)))
+    return out
+
+
+def quantize_weights_gpu(qtype: int, x, out=None, stream=None):
+    """Reference weight quantizer on the device: x (rows, k) float32 CUDA tensor
+    -> (rows, k/QK * block_bytes) uint8 block bytes (q4_0 or q4_K)."""
+    torch = _torch()
+    rows, k = x.shape
+    if out is None:
+        out = torch.empty((rows, (k // QK[qtype]) * WEIGHT_BLOCK_BYTES[qtype]), dtype=torch.uint8, device=x.device)
+    fn = {Q4_0: lib().pfng_hip_quantize_q4_0, Q4_K: lib().pfng_hip_quantize_q4_K}[qtype]
+    check(fn(_p(x), _p(out), rows, k, _stream(stream)))
     return out
 
 

@@ -121,6 +121,22 @@ int pfng_hip_quantize_q8_K(const float *x, void *y, int64_t rows, int64_t k, voi
     return hip_status(pfng::launch_quantize_q8_K(x, y, rows, k, static_cast<hipStream_t>(stream)), "quantize_q8_K launch");
 }
 
+int pfng_hip_quantize_q4_0(const float *x, void *y, int64_t rows, int64_t k, void *stream) {
+    if (rows < 0 || k <= 0 || k % 32) return fail(PFNG_ERR_INVALID_ARGUMENT, "quantize_q4_0: rows=%lld k=%lld (k must be a positive multiple of 32)", (long long)rows, (long long)k);
+    if (rows == 0) return PFNG_OK;
+    if (!x || !y) return fail(PFNG_ERR_INVALID_ARGUMENT, "quantize_q4_0: null pointer");
+    if (!aligned(x, 16) || !aligned(y, 2)) return fail(PFNG_ERR_INVALID_ARGUMENT, "quantize_q4_0: x must be 16-byte and y 2-byte aligned");
+    return hip_status(pfng::launch_quantize_q4_0(x, y, rows, k, static_cast<hipStream_t>(stream)), "quantize_q4_0 launch");
+}
+
+int pfng_hip_quantize_q4_K(const float *x, void *y, int64_t rows, int64_t k, void *stream) {
+    if (rows < 0 || k <= 0 || k % 256) return fail(PFNG_ERR_INVALID_ARGUMENT, "quantize_q4_K: rows=%lld k=%lld (k must be a positive multiple of 256)", (long long)rows, (long long)k);
+    if (rows == 0) return PFNG_OK;
+    if (!x || !y) return fail(PFNG_ERR_INVALID_ARGUMENT, "quantize_q4_K: null pointer");
+    if (!aligned(x, 16) || !aligned(y, 16)) return fail(PFNG_ERR_INVALID_ARGUMENT, "quantize_q4_K: x and y must be 16-byte aligned");
+    return hip_status(pfng::launch_quantize_q4_K(x, y, rows, k, static_cast<hipStream_t>(stream)), "quantize_q4_K launch");
+}
+
 int pfng_hip_mul_mat(int type, const void *weight, const void *act_q, float *out, int64_t m, int64_t n, int64_t k,
                      int path, void *stream) {
     int rc = check_shape(type, m, n, k);

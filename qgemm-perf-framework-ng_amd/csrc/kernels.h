@@ -11,6 +11,10 @@ namespace pfng {
 hipError_t launch_quantize_q8_0(const float *x, void *y, int64_t rows, int64_t k, hipStream_t stream);
 hipError_t launch_quantize_q8_K(const float *x, void *y, int64_t rows, int64_t k, hipStream_t stream);
 
+// quantize_weights.hip — host quantizers of the reference, on the device
+hipError_t launch_quantize_q4_0(const float *x, void *y, int64_t rows, int64_t k, hipStream_t stream);
+hipError_t launch_quantize_q4_K(const float *x, void *y, int64_t rows, int64_t k, hipStream_t stream);
+
 // naive.hip — one thread per output in the reference's exact fp32 order
 hipError_t launch_naive_mul_mat(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                                 hipStream_t stream);

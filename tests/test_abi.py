@@ -47,6 +47,10 @@ def test_version_string(pkg):
     (lambda L: L.pfng_hip_quantize_q8_0(None, None, -1, 32, None), 1),
     (lambda L: L.pfng_hip_quantize_q8_0(None, None, 0, 32, None), 0),
     (lambda L: L.pfng_hip_quantize_q8_K(None, None, 2, 128, None), 1),
+    (lambda L: L.pfng_hip_quantize_q4_0(None, None, 2, 48, None), 1),
+    (lambda L: L.pfng_hip_quantize_q4_0(None, None, 0, 64, None), 0),
+    (lambda L: L.pfng_hip_quantize_q4_K(ctypes.c_void_p(16), ctypes.c_void_p(8), 2, 256, None), 1),
+    (lambda L: L.pfng_hip_quantize_q4_K(None, None, 1, 384, None), 1),
     (lambda L: L.pfng_hip_quantize_q8_K(ctypes.c_void_p(16), ctypes.c_void_p(3), 2, 256, None), 1),
     (lambda L: L.pfng_hip_mul_mat(7, None, None, None, 1, 1, 32, 0, None), 1),
     (lambda L: L.pfng_hip_mul_mat(0, None, None, None, 1, 1, 48, 0, None), 1),

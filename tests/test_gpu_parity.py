@@ -380,3 +380,46 @@ def test_gemv_kquant_random_bytes_and_extremes(hip, torch_gpu, oracle, qtype):
         # the automatic path takes the GEMV for m <= 8
         auto = run_mul_mat(hip, torch, qtype, w, aq, m, n, k, hip.PATH_AUTO)
         assert np.array_equal(auto, got)
+
+
+# ------------------------------------------------------ weight quantizers ----
+
+def weight_test_matrix(rows, k, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, k)) * rng.uniform(1e-4, 30, (rows, 1))).astype(np.float32)
+    x[0] = 0.0                                   # all-zero blocks (d = -0.0 for q4_0)
+    x[1, :64] = 7.0                              # constant blocks / sub-blocks
+    x[2, :256] = np.linspace(-1, 1, 256)         # ties at the rounding points
+    x[3, ::2] = -x[3, 1::2]                      # equal magnitudes of both signs (first one wins)
+    x[4, :256] = np.abs(x[4, :256]) + 1.0        # all positive: negative mins
+    x[5, :256] = -np.abs(x[5, :256]) - 1.0       # all negative
+    x[6, 32:64] = np.float32(3.0) + np.float32(1e-6) * np.arange(32, dtype=np.float32)  # tiny range
+    return x
+
+
+@pytest.mark.parametrize("qtype", [0, 1])
+@pytest.mark.parametrize("rows,k", [(37, 1024), (1, 256), (300, 4096)])
+def test_weight_quantizer_bit_exact(hip, torch_gpu, oracle, qtype, rows, k):
+    torch = torch_gpu
+    say(f"weight quantizer type={qtype} rows={rows} k={k}")
+    x = weight_test_matrix(max(rows, 8), k, seed=qtype + k)[:rows] if rows >= 8 else \
+        np.random.default_rng(1).uniform(-1, 1, (rows, k)).astype(np.float32)
+    got = hip.quantize_weights_gpu(qtype, dev(torch, x))
+    torch.cuda.synchronize()
+    expect = oracle.quantize_q4_0(x) if qtype == 0 else oracle.quantize_q4_K(x)
+    assert np.array_equal(got.cpu().numpy().reshape(-1), expect.view(np.uint8).reshape(-1))
+
+
+def test_weight_quantizer_matches_reference_generator(hip, torch_gpu, oracle):
+    """The device quantizers reproduce the reference harness's weights for
+    seed 1 (draws from the product's host generator, quantized on the GPU)."""
+    torch = torch_gpu
+    say("weight quantizer vs create_input")
+    for qtype, (m, n, k) in ((0, (2, 64, 1536)), (1, (2, 64, 1536))):
+        import numpy as _np
+        rng_act, w_ref = oracle.create_input(qtype, m, n, k, seed=1, variant=0)
+        # the weights' fp32 draws follow the activations' in the same mt19937 stream
+        draws = oracle.uniform_real_draws(1, -1.0, 1.0, m * k + n * k)[m * k:].reshape(n, k)
+        got = hip.quantize_weights_gpu(qtype, dev(torch, _np.ascontiguousarray(draws, dtype=_np.float32)))
+        torch.cuda.synchronize()
+        assert _np.array_equal(got.cpu().numpy().reshape(-1), _np.ascontiguousarray(w_ref).view(_np.uint8).reshape(-1))
