@@ -194,6 +194,13 @@ int pfng_hip_compute(int type, const float *activation, const void *weight, floa
     if (workspace_bytes < pfng_hip_compute_workspace_size(type, m, k))
         return fail(PFNG_ERR_INVALID_ARGUMENT, "compute: workspace of %zu bytes is smaller than the %zu needed",
                     workspace_bytes, pfng_hip_compute_workspace_size(type, m, k));
+    // GEMV-sized problems quantize inside the product kernel (one launch, no
+    // round trip of the q8 rows through HBM); the workspace is then unused
+    if ((path == PFNG_PATH_AUTO || path == PFNG_PATH_GEMV) && activation && weight && out &&
+        aligned(activation, 16) && aligned(weight, 16) && aligned(out, 4) && pfng::fused_gemv_supported(type, m, k))
+        return hip_status(pfng::launch_fused_gemv(type, weight, activation, out, m, n, k,
+                                                  static_cast<hipStream_t>(stream)),
+                          "fused gemv launch");
     rc = type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0 ? pfng_hip_quantize_q8_0(activation, workspace, m, k, stream)
                                                   : pfng_hip_quantize_q8_K(activation, workspace, m, k, stream);
     if (rc) return rc;

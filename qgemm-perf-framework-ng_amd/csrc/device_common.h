@@ -63,6 +63,17 @@ __device__ __forceinline__ uint32_t f32_to_fp16_bits(float value) {
     return (sign >> 16) | (shl1_w > 0xFF000000u ? 0x7E00u : nonsign);
 }
 
+// Four values of a q8_0 / q8_K block: (int8)round(x * id) packed little-endian
+// (llama_reference.cpp:49, :63; x * id separately rounded, roundf = std::round).
+__device__ __forceinline__ uint32_t q8_quantize4(float4 v, float id) {
+    const int q0 = (int)roundf(mul_rn(v.x, id));
+    const int q1 = (int)roundf(mul_rn(v.y, id));
+    const int q2 = (int)roundf(mul_rn(v.z, id));
+    const int q3 = (int)roundf(mul_rn(v.w, id));
+    return (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+           ((uint32_t)(q3 & 0xff) << 24);
+}
+
 // Butterfly reductions inside groups of W lanes (W a power of two <= 64).
 template <int W>
 __device__ __forceinline__ float group_max(float v) {

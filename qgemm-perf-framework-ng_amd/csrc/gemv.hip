@@ -229,6 +229,82 @@ __global__ __launch_bounds__(kThreads) void gemv_q4_0_m1_kernel(const uint8_t *_
     if (row < n && lane == 0) c[row] = acc * 0.0625f;
 }
 
+// Fused activation quantization + GEMV (m <= 8): each workgroup quantizes the
+// m fp32 activation rows into q8_0 blocks in LDS (the same arithmetic as
+// quantize_q8_0_kernel, so the bytes equal the standalone quantizer's), then
+// its 16 waves each take one weight row as gemv_q4_0_m1_kernel does, reading
+// the activation pairs from LDS. This saves the quantizer's launch and its
+// round trip through HBM; the quantization is repeated per workgroup but costs
+// m * k / 1024 elements per thread.
+constexpr int kFusedThreads = 1024;
+
+template <int M>
+__global__ __launch_bounds__(kFusedThreads) void gemv_q4_0_fused_kernel(const uint8_t *__restrict__ w,
+                                                                       const float *__restrict__ x,
+                                                                       float *__restrict__ c, int n, int nb) {
+    extern __shared__ __align__(16) uint8_t aq[];  // M rows of nb q8_0 blocks, HBM layout
+    const int tid = threadIdx.x, sub = tid & 7;
+    for (int blk = tid >> 3; blk < M * nb; blk += kFusedThreads / 8) {
+        const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)blk * 32 + sub * 4);
+        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        amax = group_max<8>(amax);
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const uint32_t q = q8_quantize4(v, id);
+        uint16_t *ob = reinterpret_cast<uint16_t *>(aq + blk * 34);
+        ob[1 + 2 * sub] = (uint16_t)(q & 0xffffu);
+        ob[2 + 2 * sub] = (uint16_t)(q >> 16);
+        if (sub == 0) ob[0] = (uint16_t)f32_to_fp16_bits(d);
+    }
+    __syncthreads();
+    const int lane = tid & 63;
+    const int row = blockIdx.x * (kFusedThreads / 64) + (tid >> 6);
+    const int lrow = row < n ? row : n - 1;
+    float acc[M];
+#pragma unroll
+    for (int mi = 0; mi < M; ++mi) acc[mi] = 0.0f;
+    for (int p = lane; p < nb / 2; p += 64) {
+        const uint32_t *ws = reinterpret_cast<const uint32_t *>(w + ((size_t)lrow * nb + 2 * p) * 18);
+        uint32_t u[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) u[i] = ws[i];
+        const uint32_t q0[4] = {shift2(u[0], u[1]), shift2(u[1], u[2]), shift2(u[2], u[3]), shift2(u[3], u[4])};
+        const uint32_t q1[4] = {u[5], u[6], u[7], u[8]};
+#pragma unroll
+        for (int mi = 0; mi < M; ++mi) {
+            const uint32_t *as = reinterpret_cast<const uint32_t *>(aq + (mi * nb + 2 * p) * 34);
+            uint32_t v[17];
+#pragma unroll
+            for (int i = 0; i < 17; ++i) v[i] = as[i];
+            uint32_t x0[8], x1[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                x0[i] = shift2(v[i], v[i + 1]);
+                x1[i] = v[9 + i];
+            }
+            acc[mi] += q4_0_block_dot16(q0, u[0] & 0xffffu, x0, v[0] & 0xffffu);
+            acc[mi] += q4_0_block_dot16(q1, u[4] >> 16, x1, v[8] >> 16);
+        }
+    }
+#pragma unroll
+    for (int mi = 0; mi < M; ++mi) acc[mi] = group_sumf<64>(acc[mi]);
+    if (row < n && lane < M) {
+        float v = acc[0];
+#pragma unroll
+        for (int mi = 1; mi < M; ++mi) v = lane == mi ? acc[mi] : v;
+        c[(size_t)lane * n + row] = v * 0.0625f;
+    }
+}
+
+template <int M>
+hipError_t launch_fused_m(const void *w, const float *x, float *c, int64_t n, int64_t k, hipStream_t stream) {
+    const int nb = (int)(k / 32);
+    const dim3 grid((unsigned)((n + kFusedThreads / 64 - 1) / (kFusedThreads / 64)));
+    hipLaunchKernelGGL(gemv_q4_0_fused_kernel<M>, grid, dim3(kFusedThreads), (size_t)M * nb * 34, stream,
+                       static_cast<const uint8_t *>(w), x, c, (int)n, nb);
+    return hipGetLastError();
+}
+
 template <int M>
 hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n, int64_t k, hipStream_t stream) {
     const int nb = (int)(k / 32);
@@ -245,6 +321,27 @@ hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n,
 }
 
 }  // namespace
+
+bool fused_gemv_supported(int type, int64_t m, int64_t k) {
+    return type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0 && m >= 1 && m <= 8 && k % 64 == 0 &&
+           m * (k / 32) * 34 <= 65536;
+}
+
+hipError_t launch_fused_gemv(int type, const void *w, const float *x, float *c, int64_t m, int64_t n, int64_t k,
+                             hipStream_t stream) {
+    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return hipErrorInvalidValue;
+    switch (m) {
+    case 1: return launch_fused_m<1>(w, x, c, n, k, stream);
+    case 2: return launch_fused_m<2>(w, x, c, n, k, stream);
+    case 3: return launch_fused_m<3>(w, x, c, n, k, stream);
+    case 4: return launch_fused_m<4>(w, x, c, n, k, stream);
+    case 5: return launch_fused_m<5>(w, x, c, n, k, stream);
+    case 6: return launch_fused_m<6>(w, x, c, n, k, stream);
+    case 7: return launch_fused_m<7>(w, x, c, n, k, stream);
+    case 8: return launch_fused_m<8>(w, x, c, n, k, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
 
 bool gemv_supported(int type, int64_t m, int64_t k) {
     if (m < 1 || m > 8) return false;

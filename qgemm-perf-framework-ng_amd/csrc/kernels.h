@@ -23,6 +23,10 @@ hipError_t launch_naive_mul_mat(int type, const void *w, const void *a, float *c
 bool gemv_supported(int type, int64_t m, int64_t k);
 hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                        hipStream_t stream);
+// fused activation quantization + GEMV (q4_0, m <= 8, the m q8_0 rows fit 64 KB of LDS)
+bool fused_gemv_supported(int type, int64_t m, int64_t k);
+hipError_t launch_fused_gemv(int type, const void *w, const float *x, float *c, int64_t m, int64_t n, int64_t k,
+                             hipStream_t stream);
 hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                               hipStream_t stream);
 

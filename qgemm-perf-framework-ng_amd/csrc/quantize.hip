@@ -21,15 +21,6 @@ namespace {
 constexpr int kQ8_0BlocksPerGroup = 32;  // 256 threads, 8 lanes per block
 constexpr int kQ8_0GroupBytes = kQ8_0BlocksPerGroup * 34;
 
-__device__ __forceinline__ uint32_t quantize4(float4 v, float id) {
-    const int q0 = (int)roundf(mul_rn(v.x, id));
-    const int q1 = (int)roundf(mul_rn(v.y, id));
-    const int q2 = (int)roundf(mul_rn(v.z, id));
-    const int q3 = (int)roundf(mul_rn(v.w, id));
-    return (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
-           ((uint32_t)(q3 & 0xff) << 24);
-}
-
 template <bool kAligned4>
 __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x, uint8_t *__restrict__ y,
                                                            int64_t nblocks) {
@@ -46,7 +37,7 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
     amax = group_max<8>(amax);
     const float d = amax / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    const uint32_t q = quantize4(v, id);
+    const uint32_t q = q8_quantize4(v, id);
 
     // block layout in LDS: short 0 = d, shorts 1..16 = qs
     uint16_t *blk = stage + local_block * 17;
@@ -83,7 +74,7 @@ __global__ __launch_bounds__(256) void quantize_q8_K_kernel(const float *__restr
     amax = group_max<64>(amax);
     const float d = amax / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    const uint32_t q = quantize4(v, id);
+    const uint32_t q = q8_quantize4(v, id);
     int s = (int)(int8_t)(q & 0xff) + (int)(int8_t)((q >> 8) & 0xff) + (int)(int8_t)((q >> 16) & 0xff) +
             (int)(int8_t)(q >> 24);
     s = group_sum<4>(s);
