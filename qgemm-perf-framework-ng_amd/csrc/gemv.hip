@@ -190,22 +190,37 @@ __global__ __launch_bounds__(kThreads) void gemv_q4_0_kernel(const uint8_t *__re
     }
 }
 
-// m == 1: no LDS staging and no barrier. Each lane owns one q4_0 block pair of
-// its row (36 bytes, nine dword loads) and the matching q8_0 block pair of the
-// activation row (68 bytes, seventeen dword loads); both are 4-byte aligned when
-// k % 64 == 0. All 26 loads are issued before any arithmetic, so each lane pays
-// one memory round trip. One wavefront covers 64 block pairs of one row (a
-// whole row at k = 4096); 4096 rows give 4096 waves, four per SIMD.
-__global__ __launch_bounds__(kThreads) void gemv_q4_0_m1_kernel(const uint8_t *__restrict__ w,
-                                                               const uint8_t *__restrict__ a, float *__restrict__ c,
-                                                               int n, int nb) {
+// m == 1. Each lane owns one q4_0 block pair of its row (36 bytes, nine dword
+// loads, 4-byte aligned when k % 64 == 0) and reads the matching q8_0 block
+// pair of the activation row (68 bytes, seventeen dwords). All of a lane's
+// loads are issued before any arithmetic, so each lane pays one memory round
+// trip. One wavefront covers 64 block pairs of one row (a whole row at
+// k = 4096). kLdsAct: workgroups of 16 rows copy the activation row into LDS
+// once (the 16 waves then read it from there instead of each fetching it from
+// L2); measured 5 % faster at 4096 x 4096. Without it (activation rows above
+// 64 KB), 4-row workgroups read the activation directly.
+template <bool kLdsAct>
+__global__ __launch_bounds__(kLdsAct ? 1024 : kThreads) void gemv_q4_0_m1_kernel(const uint8_t *__restrict__ w,
+                                                                               const uint8_t *__restrict__ a,
+                                                                               float *__restrict__ c, int n, int nb) {
+    constexpr int kBlockThreads = kLdsAct ? 1024 : kThreads;
+    extern __shared__ __align__(16) uint8_t sact[];
+    const uint8_t *act = a;
+    if constexpr (kLdsAct) {
+        // nb is even (k % 64 == 0), so the row is a whole number of dwords
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(a);
+        uint32_t *dst = reinterpret_cast<uint32_t *>(sact);
+        for (int i = threadIdx.x; i < nb * 34 / 4; i += kBlockThreads) dst[i] = src[i];
+        __syncthreads();
+        act = sact;
+    }
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int row = blockIdx.x * (kBlockThreads / 64) + (threadIdx.x >> 6);
     const int lrow = row < n ? row : n - 1;  // clamped: loads stay unconditional, the store is guarded
     float acc = 0.0f;
     for (int p = lane; p < nb / 2; p += 64) {
         const uint32_t *ws = reinterpret_cast<const uint32_t *>(w + ((size_t)lrow * nb + 2 * p) * 18);
-        const uint32_t *as = reinterpret_cast<const uint32_t *>(a + (size_t)(2 * p) * 34);
+        const uint32_t *as = reinterpret_cast<const uint32_t *>(act + (size_t)(2 * p) * 34);
         uint32_t u[9], v[17];
 #pragma unroll
         for (int i = 0; i < 9; ++i) u[i] = ws[i];
@@ -355,9 +370,17 @@ hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t
     if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return launch_kquant_gemv(type, w, a, c, m, n, k, stream);
     switch (m) {
     case 1: {
-        const int grid = (int)((n + kThreads / 64 - 1) / (kThreads / 64));
-        hipLaunchKernelGGL(gemv_q4_0_m1_kernel, dim3(grid), dim3(kThreads), 0, stream, static_cast<const uint8_t *>(w),
-                           static_cast<const uint8_t *>(a), c, (int)n, (int)(k / 32));
+        const int nb = (int)(k / 32);
+        const size_t act_bytes = (size_t)nb * 34;
+        if (act_bytes <= 65536) {
+            const int grid = (int)((n + 15) / 16);
+            hipLaunchKernelGGL(gemv_q4_0_m1_kernel<true>, dim3(grid), dim3(1024), act_bytes, stream,
+                               static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(a), c, (int)n, nb);
+        } else {
+            const int grid = (int)((n + kThreads / 64 - 1) / (kThreads / 64));
+            hipLaunchKernelGGL(gemv_q4_0_m1_kernel<false>, dim3(grid), dim3(kThreads), 0, stream,
+                               static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(a), c, (int)n, nb);
+        }
         return hipGetLastError();
     }
     case 2: return launch_gemv_q4_0_m<2>(w, a, c, n, k, stream);
