@@ -171,9 +171,65 @@ def summarize(args):
     print(json.dumps(report))
 
 
+def bench_stats(args):
+    """Per-kernel table of a `rocprofv3 --kernel-trace --stats -- python3 bench.py`
+    run, with the bench line's own HIP-event kernel times beside the kernels
+    they name (the average of every matching dispatch)."""
+    stats = read_csvs(args.trace, "kernel_stats.csv")
+    if not stats:
+        raise SystemExit(f"no kernel_stats.csv under {args.trace}")
+    line = {}
+    if args.bench_json:
+        with open(args.bench_json) as f:
+            text = [t for t in f.read().splitlines() if t.startswith("{")]
+        line = json.loads(text[-1]) if text else {}
+    items = [("c1 headline", line.get("roofline"))]
+    for key in ("gemm", "q4_K", "iq2_xxs", "prefill", "gemv_q4_K", "gemv_iq2_xxs"):
+        if isinstance(line.get(key), dict):
+            items.append((key, line[key].get("roofline")))
+
+    def short(name):
+        name = name.replace("(anonymous namespace)::", "").replace("pfng::", "")
+        name = name[5:] if name.startswith("void ") else name
+        return name.split("(int")[0].split("(unsigned")[0].split("(float")[0].split("(__")[0][:110]
+
+    rows = sorted(stats, key=lambda r: -float(r["TotalDurationNs"]))
+    out = ["# bench.py kernel statistics (rocprofv3 --kernel-trace --stats)", "",
+           "Command (repository root on the GPU box), then the summary:", "```"]
+    out += list(args.command or [])
+    out += ["```", "", "| kernel | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
+    for r in rows:
+        out.append(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.3f} | "
+                   f"{float(r['MinNs']) / 1e3:.3f} | {float(r['MaxNs']) / 1e3:.3f} |")
+    out += ["", "Bench items (HIP events over graph replays, same run) against the profiler's average",
+            "for the kernel family each item names:", "",
+            "| item | kernel | bench kernel_us | profiler avg us (matching dispatches) |", "|---|---|---|---|"]
+    for label, roof in items:
+        if not roof:
+            continue
+        kname = roof["kernel"]
+        base, _, tag = kname.partition("<")
+        tag = {"q4_K": "(Kq)0", "iq2_xxs": "(Kq)1"}.get(tag.rstrip(">"), "")
+        match = [r for r in stats if base in r["Name"] and tag in short(r["Name"])]
+        # one line per instantiation: the plan picks the tile configuration by shape
+        for r in match or [None]:
+            prof = (f"{float(r['AverageNs']) / 1e3:.3f} (`{short(r['Name'])}`, {r['Calls']} dispatches)"
+                    if r else "not profiled")
+            out.append(f"| {label} | `{kname}` | {roof['kernel_us']} | {prof} |")
+    out.append("")
+    with open(args.md, "w") as f:
+        f.write("\n".join(out) + "\n")
+    print("\n".join(out))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     sub = ap.add_subparsers(dest="cmd", required=True)
+    b = sub.add_parser("bench-stats")
+    b.add_argument("--trace", required=True, help="output directory of the profiled bench.py run")
+    b.add_argument("--bench-json", help="file holding the bench.py JSON line of that run")
+    b.add_argument("--md", required=True)
+    b.add_argument("--command", action="append", help="profiler command line to record in the summary")
     w = sub.add_parser("workload")
     w.add_argument("--config", choices=sorted(CONFIGS), required=True)
     w.add_argument("--iters", type=int, default=100)
@@ -188,6 +244,8 @@ def main():
     args = ap.parse_args()
     if args.cmd == "workload":
         run_workload(args.config, args.iters)
+    elif args.cmd == "bench-stats":
+        bench_stats(args)
     else:
         summarize(args)
 
