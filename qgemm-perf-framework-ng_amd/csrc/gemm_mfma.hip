@@ -370,7 +370,11 @@ using Q40Small4 = Q40Config<64, 64, 1, 2, 4>;
 // loads three stages ahead
 using Q40Tiny = Q40Config<32, 32, 1, 1, 8, 2, 3>;
 
-enum { kCfgBig = 0, kCfgSmall = 1, kCfgSmall4 = 2, kCfgTiny = 3 };
+// decode batches (at most one 32x32 tile per CU): 32x32 tiles, 8 waves each
+// taking 4 of the stage's 32 blocks, loads two stages ahead
+using Q40Mid = Q40Config<32, 32, 1, 1, 32, 8, 2>;
+
+enum { kCfgBig = 0, kCfgSmall = 1, kCfgSmall4 = 2, kCfgTiny = 3, kCfgMid = 4 };
 
 int64_t tiles_of(int64_t m, int64_t n, int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); }
 
@@ -383,18 +387,22 @@ bool mfma_supported(int type, int64_t m, int64_t k) {
     return (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K || type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K) && k % 256 == 0;
 }
 
-// Tile choice: the largest tile that still gives at least two workgroups per
-// CU (to hide latency, each CU needs several resident waves), else the 32x32
-// tile whose two K-waves double the waves per output.
+// Tile choice (measured on MI355X, 256 CUs): when the 32x32 tiles number at
+// most one per CU (decode batches: m <= 64 at n = 4096), the 8-K-wave 32x32
+// tile; else 128x128 tiles when there are at least two per CU, 64x64 tiles
+// from 1.25 per CU (at 1.0 per CU the 32x32 tile was still faster), and the
+// 2-K-wave 32x32 tile below that.
 MfmaPlan plan_mfma(int type, int64_t m, int64_t n, int64_t k, int cus) {
     if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return plan_kquant(type, m, n, k, cus);
     MfmaPlan p;
     const int64_t enough = 2 * (int64_t)cus;
-    if (tiles_of(m, n, 128, 128) >= enough) {
+    if (k % (32 * Q40Mid::kKB) == 0 && tiles_of(m, n, 32, 32) <= cus) {
+        p.config = kCfgMid;
+    } else if (tiles_of(m, n, 128, 128) >= enough) {
         p.config = kCfgBig;
     } else if (k % (32 * Q40Small::kKB) != 0) {
         p.config = kCfgSmall4;
-    } else if (tiles_of(m, n, 64, 64) >= enough) {
+    } else if (4 * tiles_of(m, n, 64, 64) >= 5 * (int64_t)cus) {
         p.config = kCfgSmall;
     } else {
         p.config = kCfgTiny;
@@ -409,6 +417,7 @@ hipError_t launch_mfma_mul_mat(int type, const void *w, const void *a, float *c,
     case kCfgBig: return launch_q4_0<Q40Big, false>(w, a, c, nullptr, m, n, k, stream);
     case kCfgSmall: return launch_q4_0<Q40Small, false>(w, a, c, nullptr, m, n, k, stream);
     case kCfgTiny: return launch_q4_0<Q40Tiny, false>(w, a, c, nullptr, m, n, k, stream);
+    case kCfgMid: return launch_q4_0<Q40Mid, false>(w, a, c, nullptr, m, n, k, stream);
     default: return launch_q4_0<Q40Small4, false>(w, a, c, nullptr, m, n, k, stream);
     }
 }
@@ -416,6 +425,7 @@ hipError_t launch_mfma_mul_mat(int type, const void *w, const void *a, float *c,
 hipError_t launch_mfma_block_isums(int type, const void *w, const void *a, int32_t *out, int64_t m, int64_t n,
                                    int64_t k, hipStream_t stream) {
     if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return launch_kquant_block_isums(type, w, a, out, m, n, k, stream);
+    if (k % (32 * Q40Mid::kKB) == 0 && m <= 64) return launch_q4_0<Q40Mid, true>(w, a, nullptr, out, m, n, k, stream);
     if (k % (32 * Q40Tiny::kKB) == 0) return launch_q4_0<Q40Tiny, true>(w, a, nullptr, out, m, n, k, stream);
     return launch_q4_0<Q40Small4, true>(w, a, nullptr, out, m, n, k, stream);
 }

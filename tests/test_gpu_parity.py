@@ -147,7 +147,8 @@ def test_gemv_q4_0(hip, torch_gpu, oracle, m, n, k):
 
 # ------------------------------------------------------------------- MFMA ----
 
-@pytest.mark.parametrize("m,n,k", [(32, 32, 128), (100, 77, 256), (480, 1536, 1536), (9, 300, 640), (2048, 4096, 256)])
+@pytest.mark.parametrize("m,n,k", [(32, 32, 128), (100, 77, 256), (480, 1536, 1536), (9, 300, 640), (2048, 4096, 256),
+                                   (1, 50, 128), (16, 4096, 4096), (33, 1000, 512), (64, 100, 2048), (65, 70, 256)])
 def test_mfma_q4_0(hip, torch_gpu, oracle, m, n, k):
     torch = torch_gpu
     say(f"mfma q4_0 {m}x{n}x{k}")
@@ -158,7 +159,10 @@ def test_mfma_q4_0(hip, torch_gpu, oracle, m, n, k):
     check_close(oracle, 0, got, w, aq, m, n, k, rows=rows, label=f"mfma {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("m,n,k", [(32, 32, 128), (70, 45, 384), (64, 64, 1536)])
+# tile configurations: 64x64 with 2 waves (k % 256 != 0), 32x32 with 2 K-waves,
+# 32x32 with 8 K-waves (m <= 64, k % 1024 == 0)
+@pytest.mark.parametrize("m,n,k", [(32, 32, 128), (70, 45, 384), (64, 64, 1536), (9, 40, 256), (50, 33, 640),
+                                   (96, 40, 512), (20, 50, 2048), (64, 33, 1024)])
 def test_block_isums_q4_0_bit_exact(hip, torch_gpu, oracle, m, n, k):
     torch = torch_gpu
     say(f"block isums q4_0 {m}x{n}x{k}")
@@ -306,12 +310,14 @@ def test_config3_iq2_xxs_full_size_sampled(hip, torch_gpu, oracle):
 # ------------------------------------------------- small-shape configs ----
 
 @pytest.mark.parametrize("qtype,m,n,k", [(0, 480, 1536, 1536), (0, 9, 300, 640), (0, 200, 130, 1024),
-                                         (0, 33, 65, 256), (1, 480, 1536, 1536), (1, 100, 77, 512),
+                                         (0, 33, 65, 256), (0, 16, 4096, 4096), (0, 40, 200, 2048),
+                                         (1, 480, 1536, 1536), (1, 100, 77, 512),
                                          (2, 130, 200, 2048), (2, 31, 33, 256)])
 def test_small_shapes_deterministic_and_correct(hip, torch_gpu, oracle, qtype, m, n, k):
-    """Shapes that take the 32x32-tile configurations (two waves share each
-    stage's blocks and add their partials through LDS): within tolerance, and
-    bit-identical across repeated launches and after a launch of another shape."""
+    """Shapes that take the 32x32-tile configurations (two or, for q4_0 decode
+    batches, eight waves share each stage's blocks and add their partials
+    through LDS): within tolerance, and bit-identical across repeated launches
+    and after a launch of another shape."""
     torch = torch_gpu
     say(f"small shape type={qtype} {m}x{n}x{k}")
     act, w = oracle.create_input(qtype, m, n, k, seed=m + n + k + qtype)
