@@ -43,14 +43,16 @@ __constant__ uint16_t kIq2GridCodes[256] = PFNG_IQ2XXS_GRID_CODES_INIT;
 enum class Kq { Q4K, IQ2 };
 
 // BM x BN workgroup tile, WM x WN waves over it, the 4 sub-blocks of each
-// stage divided among WK waves (WK > 1: partial accumulators added through LDS
-// at the end, in wave order).
-template <Kq T, int BM, int BN, int WM, int WN, int WK = 1>
+// stage divided among WK waves, and WS slices of such waves that take every
+// WS-th super-block each (each slice stages its own super-blocks in its own
+// LDS buffers). WK * WS > 1: the partial accumulators are added through LDS
+// at the end, in a fixed order.
+template <Kq T, int BM, int BN, int WM, int WN, int WK = 1, int WS = 1>
 struct KqConfig {
     static constexpr Kq kType = T;
     static constexpr bool kQ4K = T == Kq::Q4K;
-    static constexpr int kBM = BM, kBN = BN, kWM = WM, kWN = WN, kWK = WK;
-    static constexpr int kThreads = 64 * WM * WN * WK;
+    static constexpr int kBM = BM, kBN = BN, kWM = WM, kWN = WN, kWK = WK, kWS = WS;
+    static constexpr int kThreads = 64 * WM * WN * WK;  // threads of one slice
     static constexpr int TM = BM / WM / 32;  // 32x32 tiles per wave along m
     static constexpr int TN = BN / WN / 32;  // along n
     static constexpr int kSub = 4;                    // sub-blocks per stage
@@ -66,8 +68,10 @@ struct KqConfig {
     static constexpr int kWdm = kWd + BN * 4;                       // q4_K: fp32 [BN] dmin
     static constexpr int kWmin = kWdm + (kQ4K ? BN * 4 : 0);        // q4_K: fp16 [BN][8] mins, each twice
     static constexpr int kBufBytes = kWmin + (kQ4K ? BN * 16 : 0);
-    static constexpr int kGrid = 2 * kBufBytes;                      // iq2: 256 x 8-byte grid magnitudes
+    static constexpr int kSliceBytes = 2 * kBufBytes;                // a slice's two stage buffers
+    static constexpr int kGrid = WS * kSliceBytes;                   // iq2: 256 x 8-byte grid magnitudes
     static constexpr int kLdsBytes = kGrid + (kQ4K ? 0 : 256 * 8);
+    static constexpr int kAllThreads = kThreads * WS;
     // global -> register tasks per stage: each activation row in kActE parts
     // (2 or 4) of its 128 int8 and 8 bsums, each weight row per sub-block
     static constexpr int kActE = BM * 2 >= kThreads ? 2 : kThreads / BM;
@@ -83,7 +87,8 @@ struct KqConfig {
                       kWdm % 16 == 0 && kWmin % 16 == 0 && kBufBytes % 16 == 0,
                   "LDS regions 16-byte aligned");
     static_assert(kWaveSub * WK == kSub, "the stage's sub-blocks split evenly over the K-waves");
-    static_assert((WK - 1) * WM * WN * TM * TN * 16 * 64 * 4 <= 2 * kBufBytes, "K-wave reduction fits in LDS");
+    static_assert((WK * WS - 1) * WM * WN * TM * TN * 16 * 64 * 4 <= WS * kSliceBytes, "K-wave reduction fits in LDS");
+    static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
 };
 
 template <class C>
@@ -103,10 +108,10 @@ constexpr int kQ8KBytes = 292, kQ4KBytes = 144, kIq2Bytes = 66;
 // edge so that every load is unconditional and in bounds.
 template <class C>
 __device__ __forceinline__ void kq_load(const uint8_t *__restrict__ a, const uint8_t *__restrict__ w, int m, int n,
-                                        int nb, int m0, int n0, int b, int h, KqRegs<C> &r) {
+                                        int nb, int m0, int n0, int b, int h, int tid, KqRegs<C> &r) {
 #pragma unroll
     for (int it = 0; it < C::kActPT; ++it) {
-        const int task = threadIdx.x + it * C::kThreads;
+        const int task = tid + it * C::kThreads;
         const int row = m0 + task / C::kActE, e = task % C::kActE;
         const int lrow = row < m ? row : m - 1;
         const uint8_t *blk = a + ((size_t)lrow * nb + b) * kQ8KBytes;
@@ -122,7 +127,7 @@ __device__ __forceinline__ void kq_load(const uint8_t *__restrict__ a, const uin
     }
 #pragma unroll
     for (int it = 0; it < C::kWPT; ++it) {
-        const int task = threadIdx.x + it * C::kThreads;
+        const int task = tid + it * C::kThreads;
         const int row = n0 + task / C::kSub, e = task % C::kSub;
         const int lrow = row < n ? row : n - 1;
         if constexpr (C::kQ4K) {
@@ -164,10 +169,10 @@ __device__ __forceinline__ void q4_K_scale_min(const uint32_t hd[4], int j, uint
 }
 
 template <class C>
-__device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int h, const KqRegs<C> &r) {
+__device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int h, int tid, const KqRegs<C> &r) {
 #pragma unroll
     for (int it = 0; it < C::kActPT; ++it) {
-        const int task = threadIdx.x + it * C::kThreads;
+        const int task = tid + it * C::kThreads;
         const int row = task / C::kActE, e = task % C::kActE;
         const uint32_t *v = r.aq[it];
         uint4 *dst = reinterpret_cast<uint4 *>(lds + C::kAq + row * C::kRowStride + 4 * C::kQsDw * e);
@@ -189,7 +194,7 @@ __device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int 
     }
 #pragma unroll
     for (int it = 0; it < C::kWPT; ++it) {
-        const int task = threadIdx.x + it * C::kThreads;
+        const int task = tid + it * C::kThreads;
         const int row = task / C::kSub, e = task % C::kSub;
         uint8_t *wrow = lds + C::kWq + row * C::kRowStride;
         if constexpr (C::kQ4K) {
@@ -396,12 +401,15 @@ __device__ __forceinline__ void kq_epilogue(const uint8_t *buf, KqAcc<C> &A, int
 }
 
 template <class C, bool kIsums>
-__global__ __launch_bounds__(C::kThreads, 2) void gemm_kq_kernel(const uint8_t *__restrict__ w,
-                                                                 const uint8_t *__restrict__ a, float *__restrict__ c,
-                                                                 int32_t *__restrict__ isums, int m, int n, int nb) {
+__global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_t *__restrict__ w,
+                                                                    const uint8_t *__restrict__ a,
+                                                                    float *__restrict__ c, int32_t *__restrict__ isums,
+                                                                    int m, int n, int nb) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int slice = threadIdx.x / C::kThreads;  // takes super-blocks slice, slice + WS, ...
+    const int tid = threadIdx.x % C::kThreads;    // thread index within the slice
+    const int wave = tid >> 6;
     const int wk = wave / (C::kWM * C::kWN);   // which share of each stage's sub-blocks
     const int wmn = wave % (C::kWM * C::kWN);  // which TM x TN sub-tile
     const int wave_m = wmn / C::kWN;
@@ -410,10 +418,12 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_kq_kernel(const uint8_t *
     const TileOrigin to = xcd_tile(blockIdx.x, (m + C::kBM - 1) / C::kBM, (n + C::kBN - 1) / C::kBN);
     const int m0 = to.mi * C::kBM, n0 = to.ni * C::kBN;
     uint8_t *grid = lds + C::kGrid;
+    uint8_t *buf0 = lds + slice * C::kSliceBytes;
+    uint8_t *buf1 = buf0 + C::kBufBytes;
     if constexpr (!C::kQ4K) {
         // grid magnitudes (kernels/iq2_xxs-q8_K-RVV-common/ggml_min.h:69-134):
         // two bits per byte select 8, 25 or 43
-        for (int e = threadIdx.x; e < 256; e += C::kThreads) {
+        for (int e = threadIdx.x; e < 256; e += C::kAllThreads) {
             const uint32_t code = kIq2GridCodes[e];
             uint32_t v[2] = {0, 0};
 #pragma unroll
@@ -436,40 +446,50 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_kq_kernel(const uint8_t *
     // Double-buffered LDS with one barrier per stage. Stage 2b+h is computed
     // from buffer h while the registers of the next stage are stored into the
     // other buffer and the loads of the stage after it are issued. Stores and
-    // loads are unconditional (the stage index is clamped at the end).
+    // loads are unconditional (the super-block index is clamped at the end);
+    // every slice runs the same number of iterations, and one whose
+    // super-block is past the end skips only the arithmetic.
     KqRegs<C> regs;
-    kq_load<C>(a, w, m, n, nb, m0, n0, 0, 0, regs);
-    kq_store<C>(lds, grid, 0, regs);
-    kq_load<C>(a, w, m, n, nb, m0, n0, 0, 1, regs);
+    const int last = nb - 1;
+    kq_load<C>(a, w, m, n, nb, m0, n0, slice < nb ? slice : last, 0, tid, regs);
+    kq_store<C>(buf0, grid, 0, tid, regs);
+    kq_load<C>(a, w, m, n, nb, m0, n0, slice < nb ? slice : last, 1, tid, regs);
     __syncthreads();
-    for (int b = 0; b < nb; ++b) {
-        const int bn = b + 1 < nb ? b + 1 : nb - 1;
+    const int iters = (nb + C::kWS - 1) / C::kWS;
+    for (int it = 0; it < iters; ++it) {
+        const int b = it * C::kWS + slice;
+        const bool mine = b < nb;  // uniform across the slice's waves
+        const int bn = b + C::kWS < nb ? b + C::kWS : last;
         __builtin_amdgcn_sched_barrier(0);
-        kq_compute<C, 0>(lds, A, tb, lane, wave_m, wave_n);
+        if (mine) kq_compute<C, 0>(buf0, A, tb, lane, wave_m, wave_n);
         __builtin_amdgcn_sched_barrier(0);
-        kq_store<C>(lds + C::kBufBytes, grid, 1, regs);
+        kq_store<C>(buf1, grid, 1, tid, regs);
         __builtin_amdgcn_sched_barrier(0);
-        kq_load<C>(a, w, m, n, nb, m0, n0, bn, 0, regs);
+        kq_load<C>(a, w, m, n, nb, m0, n0, bn, 0, tid, regs);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
-        kq_compute<C, 1>(lds + C::kBufBytes, A, tb, lane, wave_m, wave_n);
-        kq_epilogue<C, kIsums>(lds + C::kBufBytes, A, isums, m, n, nb, m0, n0, b, lane, wave_m, wave_n);
+        if (mine) {
+            kq_compute<C, 1>(buf1, A, tb, lane, wave_m, wave_n);
+            kq_epilogue<C, kIsums>(buf1, A, isums, m, n, nb, m0, n0, b, lane, wave_m, wave_n);
+        }
         __builtin_amdgcn_sched_barrier(0);
-        kq_store<C>(lds, grid, 0, regs);
+        kq_store<C>(buf0, grid, 0, tid, regs);
         __builtin_amdgcn_sched_barrier(0);
-        kq_load<C>(a, w, m, n, nb, m0, n0, bn, 1, regs);
+        kq_load<C>(a, w, m, n, nb, m0, n0, bn, 1, tid, regs);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
     }
 
     if constexpr (!kIsums) {
-        if constexpr (C::kWK > 1) {
-            // add the other K-waves' partials to wave wk == 0's, in wave order;
-            // the stage buffers are free after the loop's last barrier
+        constexpr int kGroups = C::kWK * C::kWS;  // partial accumulators per output tile
+        if constexpr (kGroups > 1) {
+            // add the other groups' partials to group 0's (slice 0, wk 0), in
+            // group order; the stage buffers are free after the last barrier
             constexpr int kRegs = C::TM * C::TN * 16;
+            const int grp = slice * C::kWK + wk;
             float *red = reinterpret_cast<float *>(lds);
-            if (wk > 0) {
-                float *dst = red + ((wk - 1) * C::kWM * C::kWN + wmn) * kRegs * 64 + lane;
+            if (grp > 0) {
+                float *dst = red + ((grp - 1) * C::kWM * C::kWN + wmn) * kRegs * 64 + lane;
 #pragma unroll
                 for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
@@ -478,10 +498,10 @@ __global__ __launch_bounds__(C::kThreads, 2) void gemm_kq_kernel(const uint8_t *
                         for (int r = 0; r < 16; ++r) dst[((tm * C::TN + tn) * 16 + r) * 64] = A.acc[tm][tn][r];
             }
             __syncthreads();
-            if (wk > 0) return;
+            if (grp > 0) return;
 #pragma unroll
-            for (int w2 = 1; w2 < C::kWK; ++w2) {
-                const float *src = red + ((w2 - 1) * C::kWM * C::kWN + wmn) * kRegs * 64 + lane;
+            for (int g2 = 1; g2 < kGroups; ++g2) {
+                const float *src = red + ((g2 - 1) * C::kWM * C::kWN + wmn) * kRegs * 64 + lane;
 #pragma unroll
                 for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
@@ -511,7 +531,7 @@ template <class C, bool kIsums>
 hipError_t launch_kq(const void *w, const void *a, float *c, int32_t *isums, int64_t m, int64_t n, int64_t k,
                      hipStream_t stream) {
     const dim3 grid((unsigned)(((n + C::kBN - 1) / C::kBN) * ((m + C::kBM - 1) / C::kBM)));
-    hipLaunchKernelGGL((gemm_kq_kernel<C, kIsums>), grid, dim3(C::kThreads), C::kLdsBytes, stream,
+    hipLaunchKernelGGL((gemm_kq_kernel<C, kIsums>), grid, dim3(C::kAllThreads), C::kLdsBytes, stream,
                        static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(a), c, isums, (int)m, (int)n,
                        (int)(k / 256));
     return hipGetLastError();
@@ -530,8 +550,16 @@ using KqSmall = KqConfig<T, 64, 64, 2, 2>;
 // partial sums that nearly cancel would be rounded against a small total.
 template <Kq T>
 using KqTiny = KqConfig<T, 32, 32, 1, 1, T == Kq::Q4K ? 2 : 1>;
+// decode batches: the Tiny tile with 4 or 2 slices of whole super-blocks, so
+// that a few hundred output tiles still keep several waves on every CU (the
+// slices split the K range at super-block boundaries, which the iq2_xxs bound
+// allows)
+template <Kq T>
+using KqMid = KqConfig<T, 32, 32, 1, 1, T == Kq::Q4K ? 2 : 1, 4>;
+template <Kq T>
+using KqMid2 = KqConfig<T, 32, 32, 1, 1, T == Kq::Q4K ? 2 : 1, 2>;
 
-enum { kCfgBig = 0, kCfgSmall = 1, kCfgTiny = 2 };
+enum { kCfgBig = 0, kCfgSmall = 1, kCfgTiny = 2, kCfgMid = 3, kCfgMid2 = 4 };
 
 int64_t tiles_of(int64_t m, int64_t n, int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); }
 
@@ -541,23 +569,32 @@ hipError_t dispatch(const void *w, const void *a, float *c, const MfmaPlan &plan
     switch (plan.config) {
     case kCfgBig: return launch_kq<KqBig<T>, false>(w, a, c, nullptr, m, n, k, stream);
     case kCfgSmall: return launch_kq<KqSmall<T>, false>(w, a, c, nullptr, m, n, k, stream);
+    case kCfgMid: return launch_kq<KqMid<T>, false>(w, a, c, nullptr, m, n, k, stream);
+    case kCfgMid2: return launch_kq<KqMid2<T>, false>(w, a, c, nullptr, m, n, k, stream);
     default: return launch_kq<KqTiny<T>, false>(w, a, c, nullptr, m, n, k, stream);
     }
 }
 
 }  // namespace
 
-// The largest tile that still gives at least two workgroups per CU, else the
-// 32 x 32 tile with two K-waves.
+// Tile choice (measured on MI355X, 256 CUs): 128 x 64 tiles at two or more
+// per CU, 64 x 64 tiles at one or more per CU; below that the 32 x 32 tile
+// with the most super-block slices (4, 2, 1) that keeps the waves at or under
+// 8 per CU (more slices only added barrier and staging work).
 MfmaPlan plan_kquant(int type, int64_t m, int64_t n, int64_t k, int cus) {
-    (void)type;
     (void)k;
     MfmaPlan p;
-    const int64_t enough = 2 * (int64_t)cus;
-    if (tiles_of(m, n, 128, 64) >= enough)
+    const int64_t c = cus;
+    const int64_t wk = type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K ? 2 : 1;  // KqTiny's K-waves
+    const int64_t t32 = tiles_of(m, n, 32, 32);
+    if (tiles_of(m, n, 128, 64) >= 2 * c)
         p.config = kCfgBig;
-    else if (tiles_of(m, n, 64, 64) >= enough)
+    else if (tiles_of(m, n, 64, 64) >= c)
         p.config = kCfgSmall;
+    else if (t32 * 4 * wk <= 8 * c)
+        p.config = kCfgMid;
+    else if (t32 * 2 * wk <= 8 * c)
+        p.config = kCfgMid2;
     else
         p.config = kCfgTiny;
     return p;

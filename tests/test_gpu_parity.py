@@ -311,13 +311,15 @@ def test_config3_iq2_xxs_full_size_sampled(hip, torch_gpu, oracle):
 
 @pytest.mark.parametrize("qtype,m,n,k", [(0, 480, 1536, 1536), (0, 9, 300, 640), (0, 200, 130, 1024),
                                          (0, 33, 65, 256), (0, 16, 4096, 4096), (0, 40, 200, 2048),
-                                         (1, 480, 1536, 1536), (1, 100, 77, 512),
-                                         (2, 130, 200, 2048), (2, 31, 33, 256)])
+                                         (1, 480, 1536, 1536), (1, 100, 77, 512), (1, 16, 4096, 4096),
+                                         (1, 32, 11008, 2048), (2, 130, 200, 2048), (2, 31, 33, 256),
+                                         (2, 9, 300, 1024), (2, 480, 1536, 1536), (2, 64, 4096, 4096)])
 def test_small_shapes_deterministic_and_correct(hip, torch_gpu, oracle, qtype, m, n, k):
     """Shapes that take the 32x32-tile configurations (two or, for q4_0 decode
-    batches, eight waves share each stage's blocks and add their partials
-    through LDS): within tolerance, and bit-identical across repeated launches
-    and after a launch of another shape."""
+    batches, eight waves share each stage's blocks; for the K-quants, 2 or 4
+    slices take alternate super-blocks, idle ones included when nb < 4; all add
+    their partials through LDS): within tolerance, and bit-identical across
+    repeated launches and after a launch of another shape."""
     torch = torch_gpu
     say(f"small shape type={qtype} {m}x{n}x{k}")
     act, w = oracle.create_input(qtype, m, n, k, seed=m + n + k + qtype)
