@@ -367,8 +367,8 @@ using Q40Small = Q40Config<64, 64, 2, 2, 8>;
 // medium problems with k % 256 != 0: 64x64 tiles, 2 waves of 64x32, 4 blocks per stage
 using Q40Small4 = Q40Config<64, 64, 1, 2, 4>;
 // small problems: 32x32 tiles, 2 waves each taking 4 of the stage's 8 blocks,
-// loads three stages ahead
-using Q40Tiny = Q40Config<32, 32, 1, 1, 8, 2, 3>;
+// loads two stages ahead (three was 5-10 % slower: fewer waves fit)
+using Q40Tiny = Q40Config<32, 32, 1, 1, 8, 2, 2>;
 
 // decode batches (at most one 32x32 tile per CU): 32x32 tiles, 8 waves each
 // taking 4 of the stage's 32 blocks, loads two stages ahead
