@@ -458,7 +458,7 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
     const int iters = (nb + C::kWS - 1) / C::kWS;
     for (int it = 0; it < iters; ++it) {
         const int b = it * C::kWS + slice;
-        const bool mine = b < nb;  // uniform across the slice's waves
+        const bool mine = C::kWS == 1 || b < nb;  // uniform across the slice's waves
         const int bn = b + C::kWS < nb ? b + C::kWS : last;
         __builtin_amdgcn_sched_barrier(0);
         if (mine) kq_compute<C, 0>(buf0, A, tb, lane, wave_m, wave_n);

@@ -288,15 +288,19 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWavesPerEU) void gemm_q4_0_kern
 #pragma unroll
     for (int r = 0; r < C::kDepth; ++r) load_stage<C>(a, w, m, n, nb, m0, n0, clampst(1 + r) * C::kKB, regs[r]);
     __syncthreads();
+    // The loop runs a whole number of kDepth-stage rounds; stages past the end
+    // (stages % kDepth != 0) skip only the arithmetic. Leaving the round with
+    // a break instead made the compiler wait for freshly issued loads before
+    // every barrier, which undid the prefetch.
     for (int s0 = 0; s0 < stages; s0 += C::kDepth) {
 #pragma unroll
         for (int r = 0; r < C::kDepth; ++r) {
             const int s = s0 + r;
-            if (C::kDepth > 1 && s >= stages) break;  // uniform across the workgroup
             const int buf = s & 1;
             __builtin_amdgcn_sched_barrier(0);
-            compute_stage<C, kIsums>(lds + buf * C::kBufBytes, acc, isums, m, n, nb, m0, n0, s, wk * C::kWaveBlocks,
-                                     lane, wave_m, wave_n);
+            if (C::kDepth == 1 || s < stages)  // uniform across the workgroup
+                compute_stage<C, kIsums>(lds + buf * C::kBufBytes, acc, isums, m, n, nb, m0, n0, s,
+                                         wk * C::kWaveBlocks, lane, wave_m, wave_n);
             __builtin_amdgcn_sched_barrier(0);
             store_stage<C>(lds + (buf ^ 1) * C::kBufBytes, regs[r]);
             __builtin_amdgcn_sched_barrier(0);
