@@ -27,8 +27,11 @@ criterion (benchmark.cpp:144-156) against the device naive path, which
 reproduces llama_reference::compute bit for bit.
 
 cpu_baseline: the reference's own llama_reference::compute (oracle/_ref, built
-from /root/reference sources) timed on this host, one thread, on a bounded
-sample; if oracle/_ref is absent the C restatement (oracle/) is timed instead.
+from /root/reference sources) timed on this host on a bounded sample (c1 and
+c0, about 16 s in all): on up to 16 threads (the box's CPU share; output
+columns split, bit-identical result) as `value`/`cores`, and on one thread as
+`value_1core`. If oracle/_ref is absent the C restatement (oracle/) is timed
+instead.
 """
 from __future__ import annotations
 
@@ -125,36 +128,42 @@ def capture(torch, fn, count):
 
 
 def cpu_baseline(budget_s):
-    """Time the reference's compute() on the host: c1 (GEMV) in GB/s, c0 (GEMM) in TOPS."""
+    """Time the reference's compute() on the host: c1 (GEMV) in GB/s, c0 (GEMM)
+    in TOPS, on all usable cores (output columns split over threads, bitwise the
+    same result) and on one core."""
     import numpy as np
     import oracle as O
     O.lib()
     use_ref = O.ref_available()
-    m, n, k = 1, 4096, 4096
-    act, w = O.create_input(0, m, n, k, seed=1, variant=0)
-    out = np.zeros((m, n), np.float32)
-    if use_ref:
-        R = O.ref()
-        run = lambda a, ww, o, mm, nn, kk: R.ref_compute(0, O._ptr(a), O._ptr(ww), O._ptr(o), mm, nn, kk)  # noqa: E731
-    else:
-        run = lambda a, ww, o, mm, nn, kk: O.lib().pfo_compute(0, O._ptr(a), O._ptr(ww), O._ptr(o), mm, nn, kk, 1)  # noqa: E731
-    iters = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < budget_s * 0.5:
-        run(act, w, out, m, n, k)
-        iters += 1
-    t_gemv = time.perf_counter() - t0
-    gbs = gemv_bytes(m, n, k) * iters / t_gemv / 1e9
-    m2, n2, k2 = 480, 1536, 1536
-    act2, w2 = O.create_input(0, m2, n2, k2, seed=1, variant=0)
-    out2 = np.zeros((m2, n2), np.float32)
-    reps = 0
-    t0 = time.perf_counter()
-    while reps == 0 or time.perf_counter() - t0 < budget_s * 0.5:
-        run(act2, w2, out2, m2, n2, k2)
-        reps += 1
-    t_gemm = time.perf_counter() - t0
-    tops = 2.0 * m2 * n2 * k2 * reps / t_gemm / 1e12
+    # the GPU box's CPU share is 16 cores per GPU
+    threads = max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()))
+
+    def runner(t):
+        if use_ref:
+            R = O.ref()
+            if t == 1:
+                return lambda a, ww, o, mm, nn, kk: R.ref_compute(0, O._ptr(a), O._ptr(ww), O._ptr(o), mm, nn, kk)
+            return lambda a, ww, o, mm, nn, kk: R.ref_compute_threads(0, O._ptr(a), O._ptr(ww), O._ptr(o), mm, nn, kk, t)
+        return lambda a, ww, o, mm, nn, kk: O.lib().pfo_compute(0, O._ptr(a), O._ptr(ww), O._ptr(o), mm, nn, kk, t)
+
+    def timed(run, shape, seconds):
+        m, n, k = shape
+        act, w = O.create_input(0, m, n, k, seed=1, variant=0)
+        out = np.zeros((m, n), np.float32)
+        reps = 0
+        t0 = time.perf_counter()
+        while reps == 0 or time.perf_counter() - t0 < seconds:
+            run(act, w, out, m, n, k)
+            reps += 1
+        return reps, time.perf_counter() - t0
+
+    c1, c0 = (1, 4096, 4096), (480, 1536, 1536)
+    res = {}
+    for t in (threads, 1):
+        run = runner(t)
+        r1, s1 = timed(run, c1, budget_s * 0.25)
+        r0, s0 = timed(run, c0, budget_s * 0.25)
+        res[t] = (gemv_bytes(*c1) * r1 / s1 / 1e9, 2.0 * 480 * 1536 * 1536 * r0 / s0 / 1e12, r1, s1, r0, s0)
     cpu = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -163,12 +172,16 @@ def cpu_baseline(budget_s):
                 break
     except OSError:
         pass
+    allc, one = res[threads], res[1]
+    what = "llama_reference::compute (oracle/_ref)" if use_ref else "oracle/pfng_oracle.c compute"
     return {
-        "value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "reference" if use_ref else "port",
-        "sample": (f"{'llama_reference::compute (oracle/_ref)' if use_ref else 'oracle/pfng_oracle.c compute'}, "
-                   f"1 thread on {cpu}: c1 1x4096x4096 x{iters} calls in {t_gemv:.1f}s (incl. activation quantize); "
-                   f"c0 480x1536x1536 x{reps} in {t_gemm:.1f}s"),
-        "gemm_tops": round(tops, 5),
+        "value": round(allc[0], 3), "unit": "GB/s", "cores": threads, "kind": "reference" if use_ref else "port",
+        "sample": (f"{what} on {cpu}, activation quantize included; {threads} threads (output columns split): "
+                   f"c1 1x4096x4096 x{allc[2]} calls in {allc[3]:.1f}s, c0 480x1536x1536 x{allc[4]} in {allc[5]:.1f}s; "
+                   f"1 thread: c1 x{one[2]} in {one[3]:.1f}s, c0 x{one[4]} in {one[5]:.1f}s"),
+        "gemm_tops": round(allc[1], 5),
+        "value_1core": round(one[0], 3),
+        "gemm_tops_1core": round(one[1], 5),
     }
 
 
@@ -259,7 +272,7 @@ def main():
     ap.add_argument("--gemm-steps", type=int, default=2048, help="timed steps of the c0/c2 GEMMs")
     ap.add_argument("--iq2-steps", type=int, default=512, help="timed c3 GEMM steps (0 = skip)")
     ap.add_argument("--prefill-steps", type=int, default=64, help="timed c4 GEMM steps (0 = skip)")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline budget (0 = skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=16.0, help="bounded CPU-baseline budget (0 = skip)")
     args = ap.parse_args()
 
     if args.gpus != 1:

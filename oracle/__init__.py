@@ -125,6 +125,8 @@ def ref() -> ctypes.CDLL:
         R.ref_create_input.argtypes = [ctypes.c_int, ctypes.c_uint64, _sz, _sz, _sz, _vp, _vp]
         R.ref_compute.restype = ctypes.c_int
         R.ref_compute.argtypes = [ctypes.c_int, _vp, _vp, _vp, _sz, _sz, _sz]
+        R.ref_compute_threads.restype = ctypes.c_int
+        R.ref_compute_threads.argtypes = [ctypes.c_int, _vp, _vp, _vp, _sz, _sz, _sz, ctypes.c_int]
         _ref = R
     return _ref
 

@@ -13,7 +13,9 @@
 // grid, so ref_dot_iq2_xxs_q8_K/ref_compute are valid only for grid indices < 32
 // (the reference generator's range, benchmark.cpp:78).
 #include <cstring>
+#include <thread>
 #include <variant>
+#include <vector>
 
 #include "benchmark.h"
 #include "llama_reference.h"
@@ -88,5 +90,48 @@ REF_API int ref_compute(int type, const float *activation, const void *weight, f
     }
     const auto result = llama_reference::compute(to_type(type), input);
     std::memcpy(out, result.data(), result.size() * sizeof(float));
+    return 0;
+}
+
+// The loops of llama_reference.cpp:164-205 (compute_q4_0 / q4_K / iq2_xxs),
+// with the output columns n split over `threads` std::threads: every output
+// element is the same reference dot in the same block order, so the result
+// equals ref_compute's bit for bit. This is the all-core CPU baseline.
+REF_API int ref_compute_threads(int type, const float *activation, const void *weight, float *out, size_t m, size_t n,
+                                size_t k, int threads) {
+    if (type < 0 || type > 2 || threads < 1) return -2;
+    const size_t qk = type == 0 ? QK4_0 : QK_K;
+    const size_t blocks = k / qk;
+    std::vector<block_q8_0> a0;
+    std::vector<block_q8_K> aK;
+    if (type == 0) {
+        a0.resize(m * blocks);
+        for (size_t i = 0; i < m; ++i) llama_reference::quantize_row_q8_0(activation + i * k, a0.data() + i * blocks, k);
+    } else {
+        aK.resize(m * blocks);
+        for (size_t i = 0; i < m; ++i) llama_reference::quantize_row_q8_K(activation + i * k, aK.data() + i * blocks, k);
+    }
+    auto work = [&](size_t n0, size_t n1) {
+        for (size_t i = 0; i < m; ++i)
+            for (size_t j = n0; j < n1; ++j) {
+                if (type == 0) {
+                    const auto *w = static_cast<const block_q4_0 *>(weight);
+                    out[i * n + j] = llama_reference::dot_q4_0_q8_0(std::span<const block_q4_0>(w + j * blocks, blocks),
+                                                                    std::span<const block_q8_0>(a0.data() + i * blocks, blocks));
+                } else {
+                    float s = 0.0f;
+                    for (size_t b = 0; b < blocks; ++b)
+                        s += type == 1 ? llama_reference::dot_q4_K_q8_K(static_cast<const block_q4_K *>(weight)[j * blocks + b],
+                                                                        aK[i * blocks + b])
+                                       : llama_reference::dot_iq2_xxs_q8_K(
+                                             static_cast<const block_iq2_xxs *>(weight)[j * blocks + b], aK[i * blocks + b]);
+                    out[i * n + j] = s;
+                }
+            }
+    };
+    std::vector<std::thread> pool;
+    const size_t t = static_cast<size_t>(threads) < n ? static_cast<size_t>(threads) : (n ? n : 1);
+    for (size_t p = 0; p < t; ++p) pool.emplace_back(work, n * p / t, n * (p + 1) / t);
+    for (auto &th : pool) th.join();
     return 0;
 }

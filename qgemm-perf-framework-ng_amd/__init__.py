@@ -168,12 +168,31 @@ def _p(t) -> ctypes.c_void_p:
     return ctypes.c_void_p(t.data_ptr())
 
 
+def _need(t, nbytes: int, name: str) -> None:
+    """The C-ABI takes bare device pointers: check here that a tensor is a
+    contiguous device tensor holding at least `nbytes` bytes."""
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    have = t.numel() * t.element_size()
+    if have < nbytes:
+        raise ValueError(f"{name} holds {have} bytes, {nbytes} needed")
+
+
+def _blocks(qtype: int, rows: int, k: int, weight: bool) -> int:
+    per = WEIGHT_BLOCK_BYTES[qtype] if weight else ACT_BLOCK_BYTES[qtype]
+    return rows * (k // QK[qtype]) * per
+
+
 def quantize_q8_0(x, out=None, stream=None):
     """x: (rows, k) float32 CUDA tensor -> (rows, k/32*34) uint8 block_q8_0 bytes."""
     torch = _torch()
     rows, k = x.shape
     if out is None:
         out = torch.empty((rows, (k // 32) * 34), dtype=torch.uint8, device=x.device)
+    _need(x, rows * k * 4, "x")
+    _need(out, _blocks(Q4_0, rows, k, False), "out")
     check(lib().pfng_hip_quantize_q8_0(_p(x), _p(out), rows, k, _stream(stream)))
     return out
 
@@ -186,6 +205,8 @@ def quantize_weights_gpu(qtype: int, x, out=None, stream=None):
     if out is None:
         out = torch.empty((rows, (k // QK[qtype]) * WEIGHT_BLOCK_BYTES[qtype]), dtype=torch.uint8, device=x.device)
     fn = {Q4_0: lib().pfng_hip_quantize_q4_0, Q4_K: lib().pfng_hip_quantize_q4_K}[qtype]
+    _need(x, rows * k * 4, "x")
+    _need(out, _blocks(qtype, rows, k, True), "out")
     check(fn(_p(x), _p(out), rows, k, _stream(stream)))
     return out
 
@@ -196,6 +217,8 @@ def quantize_q8_K(x, out=None, stream=None):
     rows, k = x.shape
     if out is None:
         out = torch.empty((rows, (k // 256) * 292), dtype=torch.uint8, device=x.device)
+    _need(x, rows * k * 4, "x")
+    _need(out, _blocks(Q4_K, rows, k, False), "out")
     check(lib().pfng_hip_quantize_q8_K(_p(x), _p(out), rows, k, _stream(stream)))
     return out
 
@@ -209,6 +232,10 @@ def mul_mat(qtype: int, weight, act_q, m: int, n: int, k: int, path: int = PATH_
     torch = _torch()
     if out is None:
         out = torch.empty((m, n), dtype=torch.float32, device=weight.device)
+    if qtype in QK and m > 0 and n > 0 and k > 0 and k % QK[qtype] == 0:  # other shapes: the library reports the error
+        _need(weight, _blocks(qtype, n, k, True), "weight")
+        _need(act_q, _blocks(qtype, m, k, False), "act_q")
+        _need(out, m * n * 4, "out")
     check(lib().pfng_hip_mul_mat(qtype, _p(weight), _p(act_q), _p(out), m, n, k, path, _stream(stream)))
     return out
 
@@ -222,6 +249,11 @@ def compute(qtype: int, activation, weight, n: int, path: int = PATH_AUTO, out=N
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=activation.device)
     if out is None:
         out = torch.empty((m, n), dtype=torch.float32, device=activation.device)
+    if qtype in QK and m > 0 and n > 0 and k > 0 and k % QK[qtype] == 0:
+        _need(activation, m * k * 4, "activation")
+        _need(weight, _blocks(qtype, n, k, True), "weight")
+        _need(out, m * n * 4, "out")
+        _need(workspace, need, "workspace")
     check(lib().pfng_hip_compute(qtype, _p(activation), _p(weight), _p(out), m, n, k, _p(workspace),
                                  workspace.numel(), path, _stream(stream)))
     return out
@@ -233,5 +265,8 @@ def block_isums(qtype: int, weight, act_q, m: int, n: int, k: int, stream=None):
     nb = k // QK[qtype]
     shape = (m, n, nb, 2) if qtype == Q4_K else (m, n, nb)
     out = torch.empty(shape, dtype=torch.int32, device=weight.device)
+    if qtype in QK and m > 0 and n > 0 and k > 0 and k % QK[qtype] == 0:
+        _need(weight, _blocks(qtype, n, k, True), "weight")
+        _need(act_q, _blocks(qtype, m, k, False), "act_q")
     check(lib().pfng_hip_block_isums(qtype, _p(weight), _p(act_q), _p(out), m, n, k, _stream(stream)))
     return out

@@ -455,3 +455,27 @@ def test_compute_fused_gemv(hip, torch_gpu, oracle, m, n, k):
         unfused = hip.mul_mat(0, wt, hip.quantize_q8_0(at), m, n, k, path=hip.PATH_GEMV)
         torch.cuda.synchronize()
         assert torch.equal(fused, unfused)
+
+
+def test_wrappers_reject_short_or_strided_buffers(hip, torch_gpu):
+    """The C-ABI takes bare pointers; the Python wrappers check sizes, layout
+    and device first and raise before anything is launched."""
+    torch = torch_gpu
+    say("wrapper argument checks")
+    m, n, k = 4, 64, 256
+    w = torch.zeros((n, (k // 32) * 18), dtype=torch.uint8, device="cuda")
+    a = torch.zeros((m, (k // 32) * 34), dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError, match="weight holds"):
+        hip.mul_mat(0, w[: n - 1], a, m, n, k)
+    with pytest.raises(ValueError, match="act_q holds"):
+        hip.mul_mat(0, w, a[: m - 1], m, n, k)
+    with pytest.raises(ValueError, match="out holds"):
+        hip.mul_mat(0, w, a, m, n, k, out=torch.empty((m, n - 1), dtype=torch.float32, device="cuda"))
+    with pytest.raises(ValueError, match="contiguous"):
+        hip.mul_mat(0, torch.zeros((n, 2 * (k // 32) * 18), dtype=torch.uint8, device="cuda")[:, ::2], a, m, n, k)
+    with pytest.raises(ValueError, match="device tensor"):
+        hip.quantize_q8_0(torch.zeros((m, k), dtype=torch.float32))
+    x = torch.zeros((m, k), dtype=torch.float32, device="cuda")
+    with pytest.raises(ValueError, match="workspace holds"):
+        hip.compute(0, x, w, n, workspace=torch.empty(8, dtype=torch.uint8, device="cuda"))
+    torch.cuda.synchronize()

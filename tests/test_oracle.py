@@ -201,6 +201,22 @@ def test_oracle_matches_reference_build_other_shapes(oracle, t, m, n, k):
     assert np.array_equal(out.view(np.uint32), rout.view(np.uint32))
 
 
+@pytest.mark.skipif(not os.path.exists(os.path.join(os.path.dirname(GOLDEN), "..", "oracle", "_ref", "libpfng_ref.so")),
+                    reason="oracle/_ref not built (reference tree absent)")
+@pytest.mark.parametrize("t,m,n,k,threads", [(0, 1, 37, 512, 4), (0, 6, 9, 256, 16), (1, 3, 11, 512, 3),
+                                             (2, 2, 13, 512, 5)])
+def test_threaded_reference_compute_equals_reference_compute(oracle, t, m, n, k, threads):
+    """The all-core CPU baseline splits llama_reference::compute's output columns
+    over threads; every element must stay bit-identical."""
+    R = oracle.ref()
+    act, w = oracle.create_input(t, m, n, k, seed=9, variant=0)
+    a = np.zeros((m, n), np.float32)
+    b = np.zeros((m, n), np.float32)
+    assert R.ref_compute(t, oracle._ptr(act), oracle._ptr(w), oracle._ptr(a), m, n, k) == 0
+    assert R.ref_compute_threads(t, oracle._ptr(act), oracle._ptr(w), oracle._ptr(b), m, n, k, threads) == 0
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 # ---------------------------------------------------------- iq2 tables ----
 
 def test_iq2xxs_grid_and_signs_match_reference_tables(oracle):
