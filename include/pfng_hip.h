@@ -41,7 +41,8 @@ typedef enum {
     PFNG_ERR_DEVICE = 4            /* current device is not a gfx950 */
 } pfng_status;
 
-/* Matrix-product implementations; PFNG_PATH_AUTO picks per shape. */
+/* Matrix-product implementations; PFNG_PATH_AUTO picks per shape (the GEMV for
+ * m <= 8 where it applies, except q4_K from m = 7 on, then the MFMA tiles). */
 typedef enum {
     PFNG_PATH_AUTO = 0,
     PFNG_PATH_GEMV = 1,  /* wavefront-per-row GEMV, no MFMA, m <= 8: q4_0 with
