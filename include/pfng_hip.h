@@ -121,8 +121,9 @@ int pfng_hip_compute(int type, const float *activation, const void *weight, floa
 
 /* ---- diagnostics ---------------------------------------------------------- */
 
-/* Exact integer parts of every block dot, computed with the same operand
- * decode and int8 MFMA tile path as PFNG_PATH_MFMA:
+/* Exact integer parts of every block dot, computed by the same kernel
+ * configuration (operand decode, tile, K split) that PFNG_PATH_MFMA runs for
+ * this shape on the current device:
  *   q4_0   : out[(m*n + n)*(k/32) + b]     = sum (q_w - 8) * q_a over block b
  *   q4_K   : out[((m*n+n)*(k/256) + b)*2]  = sum_j sc_j*S_j, [..+1] = sum_j min_j*(bsum_2j+bsum_2j+1)
  *   iq2_xxs: out[(m*n + n)*(k/256) + b]    = sum_j (2 s_j + 1) * S_j

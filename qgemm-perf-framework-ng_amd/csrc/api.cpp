@@ -220,8 +220,12 @@ int pfng_hip_block_isums(int type, const void *weight, const void *act_q, int32_
     if (!aligned(weight, 16) || !aligned(act_q, 16) || !aligned(out, 4) || !pfng::mfma_supported(type, m, k))
         return fail(PFNG_ERR_UNSUPPORTED, "block_isums: %s MFMA tile path not available for k=%lld", type_name(type),
                     (long long)k);
-    return hip_status(pfng::launch_mfma_block_isums(type, weight, act_q, out, m, n, k, static_cast<hipStream_t>(stream)),
-                      "block_isums launch");
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(PFNG_ERR_HIP, "hipGetDevice failed");
+    const pfng::MfmaPlan plan = pfng::plan_mfma(type, m, n, k, device_cus(dev));
+    return hip_status(
+        pfng::launch_mfma_block_isums(type, weight, act_q, out, m, n, k, plan, static_cast<hipStream_t>(stream)),
+        "block_isums launch");
 }
 
 }  // extern "C"

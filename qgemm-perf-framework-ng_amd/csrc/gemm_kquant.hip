@@ -540,9 +540,6 @@ hipError_t launch_kq(const void *w, const void *a, float *c, int32_t *isums, int
 // large problems: 128 x 64 tiles, 4 waves of 64 x 32
 template <Kq T>
 using KqBig = KqConfig<T, 128, 64, 2, 2>;
-// medium problems: 64 x 64 tiles, 4 waves of 32 x 32
-template <Kq T>
-using KqSmall = KqConfig<T, 64, 64, 2, 2>;
 // small problems: 32 x 32 tiles. q4_K: 2 waves each taking 2 of the stage's 4
 // sub-blocks (its accuracy bound is per element, so partial super-block sums
 // may be scaled separately). iq2_xxs: one wave, since its bound is per
@@ -559,7 +556,14 @@ using KqMid = KqConfig<T, 32, 32, 1, 1, T == Kq::Q4K ? 2 : 1, 4>;
 template <Kq T>
 using KqMid2 = KqConfig<T, 32, 32, 1, 1, T == Kq::Q4K ? 2 : 1, 2>;
 
-enum { kCfgBig = 0, kCfgSmall = 1, kCfgTiny = 2, kCfgMid = 3, kCfgMid2 = 4 };
+// the 128 x 64 and 64 x 64 tiles with 2 slices: 8 waves per workgroup where
+// the tiles alone give about one workgroup per CU
+template <Kq T>
+using KqBigS2 = KqConfig<T, 128, 64, 2, 2, 1, 2>;
+template <Kq T>
+using KqSmallS2 = KqConfig<T, 64, 64, 2, 2, 1, 2>;
+
+enum { kCfgBig = 0, kCfgTiny = 2, kCfgMid = 3, kCfgMid2 = 4, kCfgBigS2 = 5, kCfgSmallS2 = 6 };
 
 int64_t tiles_of(int64_t m, int64_t n, int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); }
 
@@ -568,29 +572,35 @@ hipError_t dispatch(const void *w, const void *a, float *c, const MfmaPlan &plan
                     hipStream_t stream) {
     switch (plan.config) {
     case kCfgBig: return launch_kq<KqBig<T>, false>(w, a, c, nullptr, m, n, k, stream);
-    case kCfgSmall: return launch_kq<KqSmall<T>, false>(w, a, c, nullptr, m, n, k, stream);
     case kCfgMid: return launch_kq<KqMid<T>, false>(w, a, c, nullptr, m, n, k, stream);
     case kCfgMid2: return launch_kq<KqMid2<T>, false>(w, a, c, nullptr, m, n, k, stream);
+    case kCfgBigS2: return launch_kq<KqBigS2<T>, false>(w, a, c, nullptr, m, n, k, stream);
+    case kCfgSmallS2: return launch_kq<KqSmallS2<T>, false>(w, a, c, nullptr, m, n, k, stream);
     default: return launch_kq<KqTiny<T>, false>(w, a, c, nullptr, m, n, k, stream);
     }
 }
 
 }  // namespace
 
-// Tile choice (measured on MI355X, 256 CUs): 128 x 64 tiles at two or more
-// per CU, 64 x 64 tiles at one or more per CU; below that the 32 x 32 tile
-// with the most super-block slices (4, 2, 1) that keeps the waves at or under
-// 8 per CU (more slices only added barrier and staging work).
+// Tile choice (measured on MI355X, 256 CUs, n = 4096 and the baseline
+// shapes): 128 x 64 tiles at two or more per CU; with 2 super-block slices at
+// one or more per CU (c3); 64 x 64 tiles with 2 slices from half a tile per CU
+// (q4_K) or three quarters (iq2_xxs) (c2: 9.1 instead of 11.3 us); below that
+// the 32 x 32 tile with the most slices (4, 2, 1) that keeps the waves at or
+// under 8 per CU (more slices only added barrier and staging work).
 MfmaPlan plan_kquant(int type, int64_t m, int64_t n, int64_t k, int cus) {
     (void)k;
     MfmaPlan p;
     const int64_t c = cus;
-    const int64_t wk = type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K ? 2 : 1;  // KqTiny's K-waves
-    const int64_t t32 = tiles_of(m, n, 32, 32);
-    if (tiles_of(m, n, 128, 64) >= 2 * c)
+    const bool q4k = type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K;
+    const int64_t wk = q4k ? 2 : 1;  // KqTiny's K-waves
+    const int64_t t32 = tiles_of(m, n, 32, 32), t64 = tiles_of(m, n, 64, 64), t128 = tiles_of(m, n, 128, 64);
+    if (t128 >= 2 * c)
         p.config = kCfgBig;
-    else if (tiles_of(m, n, 64, 64) >= c)
-        p.config = kCfgSmall;
+    else if (t128 >= c)
+        p.config = kCfgBigS2;
+    else if (4 * t64 >= (q4k ? 2 : 3) * c)
+        p.config = kCfgSmallS2;
     else if (t32 * 4 * wk <= 8 * c)
         p.config = kCfgMid;
     else if (t32 * 2 * wk <= 8 * c)
@@ -607,12 +617,30 @@ hipError_t launch_kquant_mul_mat(int type, const void *w, const void *a, float *
     return hipErrorInvalidValue;
 }
 
+// The block-sum diagnostic of a configuration. K-waves (WK > 1, q4_K's
+// 32 x 32 tiles) split each super-block's sub-blocks and only meet in the fp32
+// reduction, so their integer sums are reported by the same tile and slices
+// with one K-wave; every other configuration reports its own sums.
+template <class C>
+using KqIsums = KqConfig<C::kType, C::kBM, C::kBN, C::kWM, C::kWN, 1, C::kWS>;
+
+template <Kq T>
+hipError_t dispatch_isums(const void *w, const void *a, int32_t *out, const MfmaPlan &plan, int64_t m, int64_t n,
+                          int64_t k, hipStream_t stream) {
+    switch (plan.config) {
+    case kCfgBig: return launch_kq<KqIsums<KqBig<T>>, true>(w, a, nullptr, out, m, n, k, stream);
+    case kCfgBigS2: return launch_kq<KqIsums<KqBigS2<T>>, true>(w, a, nullptr, out, m, n, k, stream);
+    case kCfgSmallS2: return launch_kq<KqIsums<KqSmallS2<T>>, true>(w, a, nullptr, out, m, n, k, stream);
+    case kCfgMid: return launch_kq<KqIsums<KqMid<T>>, true>(w, a, nullptr, out, m, n, k, stream);
+    case kCfgMid2: return launch_kq<KqIsums<KqMid2<T>>, true>(w, a, nullptr, out, m, n, k, stream);
+    default: return launch_kq<KqIsums<KqTiny<T>>, true>(w, a, nullptr, out, m, n, k, stream);
+    }
+}
+
 hipError_t launch_kquant_block_isums(int type, const void *w, const void *a, int32_t *out, int64_t m, int64_t n,
-                                     int64_t k, hipStream_t stream) {
-    if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K)
-        return launch_kq<KqBig<Kq::Q4K>, true>(w, a, nullptr, out, m, n, k, stream);
-    if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K)
-        return launch_kq<KqBig<Kq::IQ2>, true>(w, a, nullptr, out, m, n, k, stream);
+                                     int64_t k, const MfmaPlan &plan, hipStream_t stream) {
+    if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K) return dispatch_isums<Kq::Q4K>(w, a, out, plan, m, n, k, stream);
+    if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K) return dispatch_isums<Kq::IQ2>(w, a, out, plan, m, n, k, stream);
     return hipErrorInvalidValue;
 }
 

@@ -427,11 +427,16 @@ hipError_t launch_mfma_mul_mat(int type, const void *w, const void *a, float *c,
 }
 
 hipError_t launch_mfma_block_isums(int type, const void *w, const void *a, int32_t *out, int64_t m, int64_t n,
-                                   int64_t k, hipStream_t stream) {
-    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return launch_kquant_block_isums(type, w, a, out, m, n, k, stream);
-    if (k % (32 * Q40Mid::kKB) == 0 && m <= 64) return launch_q4_0<Q40Mid, true>(w, a, nullptr, out, m, n, k, stream);
-    if (k % (32 * Q40Tiny::kKB) == 0) return launch_q4_0<Q40Tiny, true>(w, a, nullptr, out, m, n, k, stream);
-    return launch_q4_0<Q40Small4, true>(w, a, nullptr, out, m, n, k, stream);
+                                   int64_t k, const MfmaPlan &plan, hipStream_t stream) {
+    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0)
+        return launch_kquant_block_isums(type, w, a, out, m, n, k, plan, stream);
+    switch (plan.config) {
+    case kCfgBig: return launch_q4_0<Q40Big, true>(w, a, nullptr, out, m, n, k, stream);
+    case kCfgSmall: return launch_q4_0<Q40Small, true>(w, a, nullptr, out, m, n, k, stream);
+    case kCfgTiny: return launch_q4_0<Q40Tiny, true>(w, a, nullptr, out, m, n, k, stream);
+    case kCfgMid: return launch_q4_0<Q40Mid, true>(w, a, nullptr, out, m, n, k, stream);
+    default: return launch_q4_0<Q40Small4, true>(w, a, nullptr, out, m, n, k, stream);
+    }
 }
 
 }  // namespace pfng

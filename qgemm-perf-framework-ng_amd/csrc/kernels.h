@@ -40,14 +40,15 @@ bool mfma_supported(int type, int64_t m, int64_t k);
 MfmaPlan plan_mfma(int type, int64_t m, int64_t n, int64_t k, int cus);
 hipError_t launch_mfma_mul_mat(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                                const MfmaPlan &plan, hipStream_t stream);
+// the integer block sums of the configuration `plan` selects (diagnostic)
 hipError_t launch_mfma_block_isums(int type, const void *w, const void *a, int32_t *out, int64_t m, int64_t n,
-                                   int64_t k, hipStream_t stream);
+                                   int64_t k, const MfmaPlan &plan, hipStream_t stream);
 
 // gemm_kquant.hip — q4_K and iq2_xxs against q8_K
 MfmaPlan plan_kquant(int type, int64_t m, int64_t n, int64_t k, int cus);
 hipError_t launch_kquant_mul_mat(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                                  const MfmaPlan &plan, hipStream_t stream);
 hipError_t launch_kquant_block_isums(int type, const void *w, const void *a, int32_t *out, int64_t m, int64_t n,
-                                     int64_t k, hipStream_t stream);
+                                     int64_t k, const MfmaPlan &plan, hipStream_t stream);
 
 }  // namespace pfng

@@ -159,10 +159,11 @@ def test_mfma_q4_0(hip, torch_gpu, oracle, m, n, k):
     check_close(oracle, 0, got, w, aq, m, n, k, rows=rows, label=f"mfma {m}x{n}x{k}")
 
 
-# tile configurations: 64x64 with 2 waves (k % 256 != 0), 32x32 with 2 K-waves,
-# 32x32 with 8 K-waves (m <= 64, k % 1024 == 0)
+# block_isums runs the configuration the MFMA plan picks for the shape: 64x64
+# with 2 waves (k % 256 != 0), 32x32 with 2 K-waves, 32x32 with 8 K-waves
+# (decode batches, k % 1024 == 0), 64x64 with 4 waves (640x2048)
 @pytest.mark.parametrize("m,n,k", [(32, 32, 128), (70, 45, 384), (64, 64, 1536), (9, 40, 256), (50, 33, 640),
-                                   (96, 40, 512), (20, 50, 2048), (64, 33, 1024)])
+                                   (96, 40, 512), (20, 50, 2048), (64, 33, 1024), (640, 2048, 256)])
 def test_block_isums_q4_0_bit_exact(hip, torch_gpu, oracle, m, n, k):
     torch = torch_gpu
     say(f"block isums q4_0 {m}x{n}x{k}")
@@ -234,8 +235,12 @@ def extreme_activation(oracle, m, k, seed):
     return oracle.quantize_q8_K(x)
 
 
+# the configuration follows the plan: 32x32 tiles with 4/2/1 super-block
+# slices (small shapes), 64x64 with 2 slices (480x1536), 128x64 with 2 slices
+# (2048x1024) and 128x64 (2048x2048)
 @pytest.mark.parametrize("qtype", [1, 2])
-@pytest.mark.parametrize("m,n,k", [(32, 64, 256), (100, 77, 512), (1, 1, 256), (130, 65, 768), (480, 64, 1536)])
+@pytest.mark.parametrize("m,n,k", [(32, 64, 256), (100, 77, 512), (1, 1, 256), (130, 65, 768), (480, 64, 1536),
+                                   (480, 1536, 256), (2048, 1024, 256), (2048, 2048, 256)])
 def test_block_isums_kquant_bit_exact(hip, torch_gpu, oracle, qtype, m, n, k):
     torch = torch_gpu
     say(f"block isums type={qtype} {m}x{n}x{k}")
