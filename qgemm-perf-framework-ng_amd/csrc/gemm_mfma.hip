@@ -378,7 +378,11 @@ using Q40Tiny = Q40Config<32, 32, 1, 1, 8, 2, 2>;
 // taking 4 of the stage's 32 blocks, loads two stages ahead
 using Q40Mid = Q40Config<32, 32, 1, 1, 32, 8, 2>;
 
-enum { kCfgBig = 0, kCfgSmall = 1, kCfgSmall4 = 2, kCfgTiny = 3, kCfgMid = 4 };
+// between the two: 64x64 tiles, 4 waves of 32x32 twice over (2 K-waves each
+// taking 8 of a 16-block stage), loads two stages ahead
+using Q40SmallK2 = Q40Config<64, 64, 2, 2, 16, 2, 2>;
+
+enum { kCfgBig = 0, kCfgSmall = 1, kCfgSmall4 = 2, kCfgTiny = 3, kCfgMid = 4, kCfgSmallK2 = 5 };
 
 int64_t tiles_of(int64_t m, int64_t n, int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); }
 
@@ -394,8 +398,9 @@ bool mfma_supported(int type, int64_t m, int64_t k) {
 // Tile choice (measured on MI355X, 256 CUs): when the 32x32 tiles number at
 // most one per CU (decode batches: m <= 64 at n = 4096), the 8-K-wave 32x32
 // tile; else 128x128 tiles when there are at least two per CU, 64x64 tiles
-// from 1.25 per CU (at 1.0 per CU the 32x32 tile was still faster), and the
-// 2-K-wave 32x32 tile below that.
+// from 1.25 per CU, the 2-K-wave 64x64 tile from 0.75 per CU when K is long
+// enough for its 16-block stages (256x4096x4096: 22.6 instead of 26.8 us), and
+// the 2-K-wave 32x32 tile below that.
 MfmaPlan plan_mfma(int type, int64_t m, int64_t n, int64_t k, int cus) {
     if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return plan_kquant(type, m, n, k, cus);
     MfmaPlan p;
@@ -408,6 +413,8 @@ MfmaPlan plan_mfma(int type, int64_t m, int64_t n, int64_t k, int cus) {
         p.config = kCfgSmall4;
     } else if (4 * tiles_of(m, n, 64, 64) >= 5 * (int64_t)cus) {
         p.config = kCfgSmall;
+    } else if (k % (32 * Q40SmallK2::kKB) == 0 && k >= 2048 && 4 * tiles_of(m, n, 64, 64) >= 3 * (int64_t)cus) {
+        p.config = kCfgSmallK2;
     } else {
         p.config = kCfgTiny;
     }
@@ -422,6 +429,7 @@ hipError_t launch_mfma_mul_mat(int type, const void *w, const void *a, float *c,
     case kCfgSmall: return launch_q4_0<Q40Small, false>(w, a, c, nullptr, m, n, k, stream);
     case kCfgTiny: return launch_q4_0<Q40Tiny, false>(w, a, c, nullptr, m, n, k, stream);
     case kCfgMid: return launch_q4_0<Q40Mid, false>(w, a, c, nullptr, m, n, k, stream);
+    case kCfgSmallK2: return launch_q4_0<Q40SmallK2, false>(w, a, c, nullptr, m, n, k, stream);
     default: return launch_q4_0<Q40Small4, false>(w, a, c, nullptr, m, n, k, stream);
     }
 }
@@ -435,6 +443,7 @@ hipError_t launch_mfma_block_isums(int type, const void *w, const void *a, int32
     case kCfgSmall: return launch_q4_0<Q40Small, true>(w, a, nullptr, out, m, n, k, stream);
     case kCfgTiny: return launch_q4_0<Q40Tiny, true>(w, a, nullptr, out, m, n, k, stream);
     case kCfgMid: return launch_q4_0<Q40Mid, true>(w, a, nullptr, out, m, n, k, stream);
+    case kCfgSmallK2: return launch_q4_0<Q40SmallK2, true>(w, a, nullptr, out, m, n, k, stream);
     default: return launch_q4_0<Q40Small4, true>(w, a, nullptr, out, m, n, k, stream);
     }
 }
