@@ -255,9 +255,9 @@ def test_block_isums_kquant_bit_exact(hip, torch_gpu, oracle, qtype, m, n, k):
 
 
 @pytest.mark.parametrize("qtype", [1, 2])
-def test_block_isums_kquant_random_bytes_and_extremes(hip, torch_gpu, oracle, qtype):
+@pytest.mark.parametrize("m,n,k", [(96, 130, 1024), (480, 1536, 512)])  # 32x32 with 4 slices; 64x64 with 2
+def test_block_isums_kquant_random_bytes_and_extremes(hip, torch_gpu, oracle, qtype, m, n, k):
     torch = torch_gpu
-    m, n, k = 96, 130, 1024
     say(f"block isums random bytes type={qtype} {m}x{n}x{k}")
     w = random_weight_blocks(oracle, qtype, n, k, seed=17 + qtype)
     for aq in (oracle.quantize_q8_K(oracle.create_input(qtype, m, 1, k, seed=9)[0]),
