@@ -46,7 +46,9 @@ typedef enum {
 typedef enum {
     PFNG_PATH_AUTO = 0,
     PFNG_PATH_GEMV = 1,  /* wavefront-per-row GEMV, no MFMA, m <= 8: q4_0 with
-                            k % 64 == 0 for m == 1, k % 256 == 0 otherwise;
+                            k % 64 == 0 for m == 1; for m = 2..8 k % 256 == 0,
+                            or k % 64 == 0 while m * (k / 64) * 76 + 16 <= 65536
+                            (the LDS-staged activation layout);
                             q4_K and iq2_xxs for every k % 256 == 0 */
     PFNG_PATH_MFMA = 2,  /* int8-MFMA GEMM, LDS-staged tiles: q4_0 with k % 128 == 0,
                             q4_K and iq2_xxs for every k % 256 == 0 */

@@ -244,6 +244,127 @@ __global__ __launch_bounds__(kLdsAct ? 1024 : kThreads) void gemv_q4_0_m1_kernel
     if (row < n && lane == 0) c[row] = acc * 0.0625f;
 }
 
+// m = 2..8 when the m activation rows fit 64 KB of LDS in the layout below.
+// Workgroups of 16 weight rows stage the activations once: each q8_0 block
+// pair of each row becomes 64 realigned int8 bytes (17-dword stride, so lanes
+// reading consecutive pairs hit distinct banks) plus its two scales widened to
+// fp32 in a separate array. Each wavefront then takes one weight row: lane p
+// owns block pair p (nine weight dwords, as gemv_q4_0_m1_kernel), decodes it
+// once and dots it with the m activation pairs read from LDS, so the inner
+// loop is the v_dot4 work and the fp32 scaling only. One wave covers a
+// 4096-wide K stretch per step.
+//
+// Cross-lane reduction: P = the largest power of two <= m rows go through a
+// reduce-scatter butterfly in which every exchange halves the values a lane
+// carries (log2(P) exchanges of P-1 values in all, then a plain butterfly over
+// the lane bits left), the other m - P rows through a plain butterfly each.
+// Lane l's accumulator j (j < P) holds activation row j ^ f(l), f(l) being the
+// lane bits the exchanges run over, so that every lane keeps the lower half
+// and sends the upper half: the lane dependence sits in the LDS read address
+// and accumulators are only ever indexed by constants (a lane-dependent
+// choice between accumulators becomes a scratch-memory array).
+constexpr int kPairsThreads = 1024;
+constexpr int kPairDwords = 17;  // 16 int8 dwords + 1 pad
+
+// int8 part, rounded up to 16 bytes, then the fp32 scale pairs; the size
+// allows for the rounding: m * (nb / 2) * 76 + 16 bytes
+__host__ __device__ constexpr int64_t pairs_scale_offset(int64_t m, int64_t nb) {
+    return (m * (nb / 2) * kPairDwords * 4 + 15) / 16 * 16;
+}
+__host__ __device__ constexpr int64_t pairs_lds_bytes(int64_t m, int64_t nb) {
+    return m * (nb / 2) * (kPairDwords * 4 + 8) + 16;
+}
+
+constexpr int pow2_floor(int v) { return v >= 8 ? 8 : (v >= 4 ? 4 : (v >= 2 ? 2 : 1)); }
+constexpr int log2_exact(int v) { return v == 8 ? 3 : (v == 4 ? 2 : (v == 2 ? 1 : 0)); }
+
+template <int M>
+__global__ __launch_bounds__(kPairsThreads) void gemv_q4_0_pairs_kernel(const uint8_t *__restrict__ w,
+                                                                       const uint8_t *__restrict__ a,
+                                                                       float *__restrict__ c, int n, int nb) {
+    constexpr int P = pow2_floor(M);
+    constexpr int kLaneShift = 6 - log2_exact(P);  // lanes per reduce-scatter result: 1 << kLaneShift
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int np = nb / 2;
+    uint32_t *xq = reinterpret_cast<uint32_t *>(lds);                          // [M][np][17]
+    float2 *xd = reinterpret_cast<float2 *>(lds + pairs_scale_offset(M, nb));  // [M][np]
+    for (int task = threadIdx.x; task < M * np; task += kPairsThreads) {
+        // task = row * np + pair: the pair's 68 bytes, 4-byte aligned (nb even)
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(a + (size_t)task * 68);
+        uint32_t v[17];
+#pragma unroll
+        for (int i = 0; i < 17; ++i) v[i] = src[i];
+        uint32_t *dst = xq + (size_t)task * kPairDwords;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            dst[i] = shift2(v[i], v[i + 1]);
+            dst[8 + i] = v[9 + i];
+        }
+        xd[task] = make_float2(fp16_to_f32(v[0] & 0xffffu), fp16_to_f32(v[8] >> 16));
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (kPairsThreads / 64) + (threadIdx.x >> 6);
+    const int lrow = row < n ? row : n - 1;  // clamped: loads stay unconditional, the store is guarded
+    const int f = lane >> kLaneShift;        // < P
+    int arow[M];                             // activation row of accumulator j
+#pragma unroll
+    for (int j = 0; j < M; ++j) arow[j] = j < P ? j ^ f : j;
+    float acc[M];
+#pragma unroll
+    for (int j = 0; j < M; ++j) acc[j] = 0.0f;
+    for (int p = lane; p < np; p += 64) {
+        const uint32_t *ws = reinterpret_cast<const uint32_t *>(w + ((size_t)lrow * nb + 2 * p) * 18);
+        uint32_t u[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) u[i] = ws[i];
+        __builtin_amdgcn_sched_barrier(0);
+        // block 2p: d at byte 0, qs at 2 (realign by two bytes); block 2p+1: d at 18, qs at 20
+        uint32_t lo0[4], hi0[4], lo1[4], hi1[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q4_0_unpack16(shift2(u[i], u[i + 1]), lo0[i], hi0[i]);
+            q4_0_unpack16(u[5 + i], lo1[i], hi1[i]);
+        }
+        const float dw0 = fp16_to_f32(u[0] & 0xffffu), dw1 = fp16_to_f32(u[4] >> 16);
+#pragma unroll
+        for (int j = 0; j < M; ++j) {
+            const int t = arow[j] * np + p;
+            const uint32_t *x = xq + (size_t)t * kPairDwords;
+            const float2 da = xd[t];
+            int s0 = 0, s1 = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                s0 = __builtin_amdgcn_sdot4((int)lo0[i], (int)x[i], s0, false);
+                s1 = __builtin_amdgcn_sdot4((int)lo1[i], (int)x[8 + i], s1, false);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                s0 = __builtin_amdgcn_sdot4((int)hi0[i], (int)x[4 + i], s0, false);
+                s1 = __builtin_amdgcn_sdot4((int)hi1[i], (int)x[12 + i], s1, false);
+            }
+            acc[j] += (float)s0 * (dw0 * da.x);
+            acc[j] += (float)s1 * (dw1 * da.y);
+        }
+    }
+    // reduce-scatter over accumulators 0..P-1: exchange offsets 32, 16, ...
+#pragma unroll
+    for (int h = P / 2, o = 32; h >= 1; h >>= 1, o >>= 1) {
+#pragma unroll
+        for (int i = 0; i < h; ++i) acc[i] += __shfl_xor(acc[i + h], o, 64);
+    }
+#pragma unroll
+    for (int o = (1 << kLaneShift) / 2; o > 0; o >>= 1) acc[0] += __shfl_xor(acc[0], o, 64);
+#pragma unroll
+    for (int j = P; j < M; ++j) acc[j] = group_sumf<64>(acc[j]);
+    if (row < n) {
+        if ((lane & ((1 << kLaneShift) - 1)) == 0) c[(size_t)f * n + row] = acc[0] * 0.0625f;
+#pragma unroll
+        for (int j = P; j < M; ++j)
+            if (lane == 63 - (j - P)) c[(size_t)j * n + row] = acc[j] * 0.0625f;
+    }
+}
+
 // Fused activation quantization + GEMV (m <= 8): each workgroup quantizes the
 // m fp32 activation rows into q8_0 blocks in LDS (the same arithmetic as
 // quantize_q8_0_kernel, so the bytes equal the standalone quantizer's), then
@@ -323,6 +444,12 @@ hipError_t launch_fused_m(const void *w, const float *x, float *c, int64_t n, in
 template <int M>
 hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n, int64_t k, hipStream_t stream) {
     const int nb = (int)(k / 32);
+    if (k % 64 == 0 && pairs_lds_bytes(M, nb) <= 65536) {
+        const int grid = (int)((n + kPairsThreads / 64 - 1) / (kPairsThreads / 64));
+        hipLaunchKernelGGL(gemv_q4_0_pairs_kernel<M>, dim3(grid), dim3(kPairsThreads), (size_t)pairs_lds_bytes(M, nb),
+                           stream, static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(a), c, (int)n, nb);
+        return hipGetLastError();
+    }
     const int groups = nb / kGroupBlocks;
     const int gcap = groups < kChunkGroups ? groups : kChunkGroups;
     int L = 1;
@@ -360,7 +487,8 @@ hipError_t launch_fused_gemv(int type, const void *w, const float *x, float *c, 
 
 bool gemv_supported(int type, int64_t m, int64_t k) {
     if (m < 1 || m > 8) return false;
-    if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return m == 1 ? k % 64 == 0 : k % 256 == 0;
+    if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0)
+        return m == 1 ? k % 64 == 0 : k % 256 == 0 || (k % 64 == 0 && pairs_lds_bytes(m, k / 32) <= 65536);
     // q4_K and iq2_xxs (gemv_kquant.hip) take every k % 256 == 0
     return (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K || type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K) && k % 256 == 0;
 }

@@ -135,7 +135,8 @@ def test_naive_bit_exact(hip, torch_gpu, oracle, qtype, m, n, k):
 # ------------------------------------------------------------------- GEMV ----
 
 @pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
-@pytest.mark.parametrize("n,k", [(4096, 4096), (257, 1536), (64, 256), (33, 8192), (40, 65536)])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (257, 1536), (64, 256), (33, 8192), (40, 65536), (129, 7680),
+                                 (77, 320), (50, 64)])
 def test_gemv_q4_0(hip, torch_gpu, oracle, m, n, k):
     torch = torch_gpu
     say(f"gemv q4_0 m={m} n={n} k={k}")
