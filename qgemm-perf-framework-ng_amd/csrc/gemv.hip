@@ -1,4 +1,5 @@
-// GEMV path (m <= 8) for gfx950: no MFMA, the weight stream is the roofline.
+// GEMV path (m <= 8; q4_0 up to m = 16) for gfx950: no MFMA, the weight stream
+// is the roofline.
 //
 // Work decomposition. The weight matrix is a stream of 18-byte q4_0 blocks.
 // Eight consecutive blocks (a "group", 144 B) start on a 16-byte boundary
@@ -244,7 +245,7 @@ __global__ __launch_bounds__(kLdsAct ? 1024 : kThreads) void gemv_q4_0_m1_kernel
     if (row < n && lane == 0) c[row] = acc * 0.0625f;
 }
 
-// m = 2..8 when the m activation rows fit 64 KB of LDS in the layout below.
+// m = 2..16 when the m activation rows fit the 160 KB of LDS in the layout below.
 // Workgroups of 16 weight rows stage the activations once: each q8_0 block
 // pair of each row becomes 64 realigned int8 bytes (17-dword stride, so lanes
 // reading consecutive pairs hit distinct banks) plus its two scales widened to
@@ -275,8 +276,10 @@ __host__ __device__ constexpr int64_t pairs_lds_bytes(int64_t m, int64_t nb) {
     return m * (nb / 2) * (kPairDwords * 4 + 8) + 16;
 }
 
-constexpr int pow2_floor(int v) { return v >= 8 ? 8 : (v >= 4 ? 4 : (v >= 2 ? 2 : 1)); }
-constexpr int log2_exact(int v) { return v == 8 ? 3 : (v == 4 ? 2 : (v == 2 ? 1 : 0)); }
+constexpr int kPairsMaxM = 16;
+constexpr int64_t kPairsMaxLds = 160 * 1024;  // one workgroup per CU holds the whole LDS
+constexpr int pow2_floor(int v) { return v >= 16 ? 16 : (v >= 8 ? 8 : (v >= 4 ? 4 : (v >= 2 ? 2 : 1))); }
+constexpr int log2_exact(int v) { return v == 16 ? 4 : (v == 8 ? 3 : (v == 4 ? 2 : (v == 2 ? 1 : 0))); }
 
 template <int M>
 __global__ __launch_bounds__(kPairsThreads) void gemv_q4_0_pairs_kernel(const uint8_t *__restrict__ w,
@@ -444,22 +447,26 @@ hipError_t launch_fused_m(const void *w, const float *x, float *c, int64_t n, in
 template <int M>
 hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n, int64_t k, hipStream_t stream) {
     const int nb = (int)(k / 32);
-    if (k % 64 == 0 && pairs_lds_bytes(M, nb) <= 65536) {
+    if (k % 64 == 0 && pairs_lds_bytes(M, nb) <= kPairsMaxLds) {
         const int grid = (int)((n + kPairsThreads / 64 - 1) / (kPairsThreads / 64));
         hipLaunchKernelGGL(gemv_q4_0_pairs_kernel<M>, dim3(grid), dim3(kPairsThreads), (size_t)pairs_lds_bytes(M, nb),
                            stream, static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(a), c, (int)n, nb);
         return hipGetLastError();
     }
-    const int groups = nb / kGroupBlocks;
-    const int gcap = groups < kChunkGroups ? groups : kChunkGroups;
-    int L = 1;
-    while (L * 2 <= gcap) L *= 2;
-    const int rows_per_block = (kThreads / 64) * (64 / L);
-    const int grid = (int)((n + rows_per_block - 1) / rows_per_block);
-    const size_t lds = (size_t)M * kChunkGroups * kGroupBytesLds;
-    hipLaunchKernelGGL(gemv_q4_0_kernel<M>, dim3(grid), dim3(kThreads), lds, stream,
-                       static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(a), c, (int)n, nb, L);
-    return hipGetLastError();
+    if constexpr (M <= 8) {
+        // longer rows: groups of 8 blocks per lane, activation chunks in LDS (k % 256 == 0)
+        const int groups = nb / kGroupBlocks;
+        const int gcap = groups < kChunkGroups ? groups : kChunkGroups;
+        int L = 1;
+        while (L * 2 <= gcap) L *= 2;
+        const int rows_per_block = (kThreads / 64) * (64 / L);
+        const int grid = (int)((n + rows_per_block - 1) / rows_per_block);
+        const size_t lds = (size_t)M * kChunkGroups * kGroupBytesLds;
+        hipLaunchKernelGGL(gemv_q4_0_kernel<M>, dim3(grid), dim3(kThreads), lds, stream,
+                           static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(a), c, (int)n, nb, L);
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -486,9 +493,14 @@ hipError_t launch_fused_gemv(int type, const void *w, const float *x, float *c, 
 }
 
 bool gemv_supported(int type, int64_t m, int64_t k) {
-    if (m < 1 || m > 8) return false;
-    if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0)
-        return m == 1 ? k % 64 == 0 : k % 256 == 0 || (k % 64 == 0 && pairs_lds_bytes(m, k / 32) <= 65536);
+    if (m < 1) return false;
+    const bool pairs = k % 64 == 0 && pairs_lds_bytes(m, k / 32) <= kPairsMaxLds;
+    if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) {
+        if (m == 1) return k % 64 == 0;
+        if (m <= 8) return k % 256 == 0 || pairs;
+        return m <= kPairsMaxM && pairs;  // m = 9..16 only in the pair-per-lane kernel
+    }
+    if (m > 8) return false;
     // q4_K and iq2_xxs (gemv_kquant.hip) take every k % 256 == 0
     return (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K || type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K) && k % 256 == 0;
 }
@@ -518,6 +530,14 @@ hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t
     case 6: return launch_gemv_q4_0_m<6>(w, a, c, n, k, stream);
     case 7: return launch_gemv_q4_0_m<7>(w, a, c, n, k, stream);
     case 8: return launch_gemv_q4_0_m<8>(w, a, c, n, k, stream);
+    case 9: return launch_gemv_q4_0_m<9>(w, a, c, n, k, stream);
+    case 10: return launch_gemv_q4_0_m<10>(w, a, c, n, k, stream);
+    case 11: return launch_gemv_q4_0_m<11>(w, a, c, n, k, stream);
+    case 12: return launch_gemv_q4_0_m<12>(w, a, c, n, k, stream);
+    case 13: return launch_gemv_q4_0_m<13>(w, a, c, n, k, stream);
+    case 14: return launch_gemv_q4_0_m<14>(w, a, c, n, k, stream);
+    case 15: return launch_gemv_q4_0_m<15>(w, a, c, n, k, stream);
+    case 16: return launch_gemv_q4_0_m<16>(w, a, c, n, k, stream);
     default: return hipErrorInvalidValue;
     }
 }

@@ -134,11 +134,16 @@ def test_naive_bit_exact(hip, torch_gpu, oracle, qtype, m, n, k):
 
 # ------------------------------------------------------------------- GEMV ----
 
-@pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 9, 12, 16])
 @pytest.mark.parametrize("n,k", [(4096, 4096), (257, 1536), (64, 256), (33, 8192), (40, 65536), (129, 7680),
                                  (77, 320), (50, 64)])
 def test_gemv_q4_0(hip, torch_gpu, oracle, m, n, k):
+    """m = 1 (block pair per lane), m = 2..16 with the activations staged in
+    LDS (m * (k / 64) * 76 + 16 <= 160 KB), m = 2..8 beyond that (groups of 8
+    blocks per lane)."""
     torch = torch_gpu
+    if m > 8 and m * (k // 64) * 76 + 16 > 160 * 1024:
+        pytest.skip("m > 8 takes the GEMV only while the staged activations fit in LDS")
     say(f"gemv q4_0 m={m} n={n} k={k}")
     act, w = oracle.create_input(0, m, n, k, seed=m * 31 + n)
     aq = oracle.quantize_q8_0(act)
