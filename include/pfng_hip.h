@@ -42,8 +42,8 @@ typedef enum {
 } pfng_status;
 
 /* Matrix-product implementations; PFNG_PATH_AUTO picks per shape (the GEMV
- * where it applies: q4_0 up to m = 16, iq2_xxs up to m = 8, q4_K up to m = 6;
- * then the MFMA tiles). */
+ * where it applies: q4_0 up to m = 16, q4_K and iq2_xxs up to m = 8; then the
+ * MFMA tiles). */
 typedef enum {
     PFNG_PATH_AUTO = 0,
     PFNG_PATH_GEMV = 1,  /* wavefront-per-row GEMV, no MFMA: q4_0 for m <= 16

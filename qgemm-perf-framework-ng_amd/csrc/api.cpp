@@ -150,11 +150,9 @@ int pfng_hip_mul_mat(int type, const void *weight, const void *act_q, float *out
     const bool mfma_ok = base_aligned && pfng::mfma_supported(type, m, k);
     switch (path) {
     case PFNG_PATH_AUTO:
-        // measured at 4096x4096: the q4_K GEMV's time grows faster with m than
-        // q4_0's and iq2_xxs's, and from m = 7 the 32x32 MFMA tile is faster
-        // (10.6 vs 11.7 us at m = 7); the other two keep the GEMV up to m = 8
-        if (gemv_ok && !(type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K && m >= 7 && mfma_ok))
-            return hip_status(pfng::launch_gemv(type, weight, act_q, out, m, n, k, s), "gemv launch");
+        // measured at 4096x4096: every GEMV that applies (q4_0 up to m = 16,
+        // the K-quants up to m = 8) is faster than the MFMA tiles
+        if (gemv_ok) return hip_status(pfng::launch_gemv(type, weight, act_q, out, m, n, k, s), "gemv launch");
         if (mfma_ok) return launch_mfma(type, weight, act_q, out, m, n, k, s);
         return hip_status(pfng::launch_naive_mul_mat(type, weight, act_q, out, m, n, k, s), "naive launch");
     case PFNG_PATH_GEMV:

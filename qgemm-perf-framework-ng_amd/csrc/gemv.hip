@@ -278,15 +278,13 @@ __host__ __device__ constexpr int64_t pairs_lds_bytes(int64_t m, int64_t nb) {
 
 constexpr int kPairsMaxM = 16;
 constexpr int64_t kPairsMaxLds = 160 * 1024;  // one workgroup per CU holds the whole LDS
-constexpr int pow2_floor(int v) { return v >= 16 ? 16 : (v >= 8 ? 8 : (v >= 4 ? 4 : (v >= 2 ? 2 : 1))); }
-constexpr int log2_exact(int v) { return v == 16 ? 4 : (v == 8 ? 3 : (v == 4 ? 2 : (v == 2 ? 1 : 0))); }
 
 template <int M>
 __global__ __launch_bounds__(kPairsThreads) void gemv_q4_0_pairs_kernel(const uint8_t *__restrict__ w,
                                                                        const uint8_t *__restrict__ a,
                                                                        float *__restrict__ c, int n, int nb) {
-    constexpr int P = pow2_floor(M);
-    constexpr int kLaneShift = 6 - log2_exact(P);  // lanes per reduce-scatter result: 1 << kLaneShift
+    constexpr int P = pow2_floor16(M);
+    constexpr int kLaneShift = 6 - log2_pow2(P);  // lanes per reduce-scatter result: 1 << kLaneShift
     extern __shared__ __align__(16) uint8_t lds[];
     const int np = nb / 2;
     uint32_t *xq = reinterpret_cast<uint32_t *>(lds);                          // [M][np][17]

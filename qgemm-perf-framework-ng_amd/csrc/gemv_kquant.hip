@@ -196,12 +196,255 @@ __global__ __launch_bounds__(kThreads) void gemv_iq2_xxs_kernel(const uint8_t *_
     }
 }
 
+// ---------------------------------------------------------------------------
+// m = 2..8 with the q8_K activation rows staged in LDS once per workgroup of
+// 16 weight rows (one per wavefront): each 292-byte block becomes 256 int8
+// bytes at a 272-byte stride (16-byte aligned for ds_read_b128, staggered
+// over the banks) and a 48-byte side record with the eight per-sub-block bsum
+// pairs bsums[2j] + bsums[2j+1] as int32 and d as fp32. The waves then read
+// activations from LDS instead of issuing 16-19 dword loads per row each.
+// Cross-lane sums use the reduce-scatter of gemv_q4_0_pairs_kernel: P = the
+// largest power of two <= m accumulators hold activation row q ^ f(lane), so
+// every lane keeps the lower half of each exchange and accumulators are only
+// indexed by constants; the other m - P rows take a plain butterfly.
+constexpr int kStagedThreads = 1024;
+constexpr int kQsStride = 272, kSideStride = 48;
+
+__host__ __device__ constexpr int64_t kq_staged_lds_bytes(int64_t m, int64_t nsb) {
+    return m * nsb * (kQsStride + kSideStride) + 256 * 8;  // + the iq2_xxs grid table
+}
+
+// four threads per block: quarter t copies qs[64t, 64t + 64), forms the bsum
+// pairs 2t and 2t + 1, and quarter 0 widens nothing (d is fp32 already)
+template <int M>
+__device__ __forceinline__ void stage_q8_K(const uint8_t *__restrict__ a, uint8_t *qs, uint8_t *side, int nsb) {
+    for (int task = threadIdx.x; task < M * nsb * 4; task += kStagedThreads) {
+        const int blk = task >> 2, t = task & 3;
+        const uint8_t *src = a + (size_t)blk * kQ8KBytes;
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(src + 4 + 64 * t);
+        uint32_t v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = q[i];
+        const uint32_t *bp = reinterpret_cast<const uint32_t *>(src + 260 + 8 * t);
+        const uint32_t b0 = bp[0], b1 = bp[1];
+        const float d = *reinterpret_cast<const float *>(src);
+        uint4 *dq = reinterpret_cast<uint4 *>(qs + (size_t)blk * kQsStride + 64 * t);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dq[i] = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+        uint8_t *sd = side + (size_t)blk * kSideStride;
+        *reinterpret_cast<int2 *>(sd + 8 * t) =
+            make_int2((int)(int16_t)(b0 & 0xffffu) + (int)(int16_t)(b0 >> 16),
+                      (int)(int16_t)(b1 & 0xffffu) + (int)(int16_t)(b1 >> 16));
+        if (t == 0) *reinterpret_cast<float *>(sd + 32) = d;
+    }
+}
+
+// q4_K: four lanes per super-block as gemv_q4_K_kernel, 16 super-blocks per
+// wave and step.
+template <int M>
+__global__ __launch_bounds__(kStagedThreads) void gemv_q4_K_staged_kernel(const uint8_t *__restrict__ w,
+                                                                         const uint8_t *__restrict__ a,
+                                                                         float *__restrict__ c, int n, int nb) {
+    constexpr int P = pow2_floor16(M);
+    constexpr int kLaneShift = 6 - log2_pow2(P);
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint8_t *qs = lds, *side = lds + (size_t)M * nb * kQsStride;
+    stage_q8_K<M>(a, qs, side, nb);
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (kStagedThreads / 64) + (threadIdx.x >> 6);
+    const int lrow = row < n ? row : n - 1;  // clamped: loads stay unconditional, the store is guarded
+    const int slot = lane >> 2, e = lane & 3;
+    const int f = lane >> kLaneShift;
+    float acc[M];
+#pragma unroll
+    for (int q = 0; q < M; ++q) acc[q] = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += 16) {
+        const int b = b0 + slot;
+        const bool valid = b < nb;
+        const int lb = valid ? b : nb - 1;
+        const uint8_t *blk = w + ((size_t)lrow * nb + lb) * kQ4KBytes;
+        const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
+        const uint4 qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * e);
+        const uint4 qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * e);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t qw[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            lo[i] = qw[i] & 0x0f0f0f0fu;
+            hi[i] = (qw[i] >> 4) & 0x0f0f0f0fu;
+        }
+        int sc0, m0, sc1, m1;
+        q4_K_scale_min(hd, 2 * e, sc0, m0);
+        q4_K_scale_min(hd, 2 * e + 1, sc1, m1);
+        const float d = fp16_to_f32(hd.x & 0xffffu), dmin = fp16_to_f32(hd.x >> 16);
+#pragma unroll
+        for (int q = 0; q < M; ++q) {
+            const int r = q < P ? q ^ f : q;
+            const int rec = r * nb + lb;
+            const uint4 *xq = reinterpret_cast<const uint4 *>(qs + (size_t)rec * kQsStride + 64 * e);
+            uint32_t x[16];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint4 t = xq[i];
+                x[4 * i] = t.x;
+                x[4 * i + 1] = t.y;
+                x[4 * i + 2] = t.z;
+                x[4 * i + 3] = t.w;
+            }
+            const uint8_t *sd = side + (size_t)rec * kSideStride;
+            const int2 bsp = *reinterpret_cast<const int2 *>(sd + 8 * e);
+            const float ad = *reinterpret_cast<const float *>(sd + 32);
+            const int is = sc0 * dot8(lo, x) + sc1 * dot8(hi, x + 8);
+            const int im = m0 * bsp.x + m1 * bsp.y;
+            const float part = ad * fmaf(-dmin, (float)im, d * (float)is);
+            acc[q] += valid ? part : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int h = P / 2, o = 32; h >= 1; h >>= 1, o >>= 1) {
+#pragma unroll
+        for (int i = 0; i < h; ++i) acc[i] += __shfl_xor(acc[i + h], o, 64);
+    }
+#pragma unroll
+    for (int o = (1 << kLaneShift) / 2; o > 0; o >>= 1) acc[0] += __shfl_xor(acc[0], o, 64);
+#pragma unroll
+    for (int q = P; q < M; ++q) acc[q] = group_sumf<64>(acc[q]);
+    if (row < n) {
+        if ((lane & ((1 << kLaneShift) - 1)) == 0) c[(size_t)f * n + row] = acc[0];
+#pragma unroll
+        for (int q = P; q < M; ++q)
+            if (lane == 63 - (q - P)) c[(size_t)q * n + row] = acc[q];
+    }
+}
+
+// iq2_xxs: eight lanes per super-block as gemv_iq2_xxs_kernel, eight
+// super-blocks per wave and step. The integer super-block sums are completed
+// across the eight lanes before any scaling (the bound of this format is per
+// super-block): accumulator q < P of lane j holds activation row q ^ (j % P),
+// a reduce-scatter over the low lane bits leaves lane j with the exact sum of
+// row j % P, and lanes j < P scale it once.
+template <int M>
+__global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(const uint8_t *__restrict__ w,
+                                                                            const uint8_t *__restrict__ a,
+                                                                            float *__restrict__ c, int n, int nb) {
+    constexpr int P = pow2_floor16(M);
+    static_assert(P <= 8, "eight lanes per super-block");
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint8_t *qs = lds, *side = lds + (size_t)M * nb * kQsStride;
+    uint8_t *grid = side + (size_t)M * nb * kSideStride;
+    if (threadIdx.x < 256) {
+        // grid magnitudes (kernels/iq2_xxs-q8_K-RVV-common/ggml_min.h:69-134): two
+        // bits per byte select 8, 25 or 43
+        const uint32_t code = kIq2GridCodes[threadIdx.x];
+        uint32_t v[2] = {0, 0};
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const uint32_t c2 = (code >> (2 * jj)) & 3u;
+            v[jj / 4] |= (c2 == 0 ? 8u : (c2 == 1 ? 25u : 43u)) << (8 * (jj % 4));
+        }
+        *reinterpret_cast<uint2 *>(grid + 8 * threadIdx.x) = make_uint2(v[0], v[1]);
+    }
+    stage_q8_K<M>(a, qs, side, nb);
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (kStagedThreads / 64) + (threadIdx.x >> 6);
+    const int lrow = row < n ? row : n - 1;
+    const int slot = lane >> 3, j = lane & 7;
+    const int f = j & (P - 1);
+    float accp = 0.0f;       // row f, in lanes j < P
+    float accx[M - P + 1];   // rows P..M-1, in lanes j == 0
+#pragma unroll
+    for (int q = 0; q <= M - P; ++q) accx[q] = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += 8) {
+        const int b = b0 + slot;
+        const bool valid = b < nb;
+        const int lb = valid ? b : nb - 1;
+        // 66-byte blocks are 2-byte aligned: the covering dwords plus a
+        // trailing half-word, never past the sub-block's last byte
+        const size_t base = ((size_t)lrow * nb + lb) * kIq2Bytes;
+        const size_t o = base + 2 + 8 * j;
+        const uint32_t *p4 = reinterpret_cast<const uint32_t *>(w + (o & ~(size_t)3));
+        const uint32_t d0 = p4[0], d1 = p4[1];
+        const uint32_t tail = *reinterpret_cast<const uint16_t *>(w + o + 6);
+        const uint32_t dh = *reinterpret_cast<const uint16_t *>(w + base);
+        __builtin_amdgcn_sched_barrier(0);
+        const bool sh = (o & 3) != 0;
+        const uint32_t gidx = sh ? __builtin_amdgcn_alignbyte(d1, d0, 2) : d0;
+        const uint32_t ss = sh ? ((d1 >> 16) | (tail << 16)) : d1;
+        uint32_t v[8];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint2 mag = *reinterpret_cast<const uint2 *>(grid + ((gidx >> (8 * g)) & 0xffu) * 8);
+            const uint32_t idx = (ss >> (7 * g)) & 0x7fu;
+            const uint32_t sgn = idx | ((__builtin_popcount(idx) & 1u) << 7);
+            const uint32_t s0 = ((sgn & 0xfu) * 0x00204081u) & 0x01010101u;
+            const uint32_t s1 = (((sgn >> 4) & 0xfu) * 0x00204081u) & 0x01010101u;
+            v[2 * g] = (mag.x ^ (s0 * 0xffu)) + s0;
+            v[2 * g + 1] = (mag.y ^ (s1 * 0xffu)) + s1;
+        }
+        const int scale = 2 * (int)(ss >> 28) + 1;
+        const float t0 = valid ? 0.125f * fp16_to_f32(dh) : 0.0f;
+        int is[M];
+#pragma unroll
+        for (int q = 0; q < M; ++q) {
+            const int r = q < P ? q ^ f : q;
+            const uint4 *xq = reinterpret_cast<const uint4 *>(qs + (size_t)(r * nb + lb) * kQsStride + 32 * j);
+            const uint4 x0 = xq[0], x1 = xq[1];
+            const uint32_t x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            is[q] = scale * dot8(v, x);
+        }
+        // exact integer sums over the eight lanes of the super-block
+#pragma unroll
+        for (int h = P / 2; h >= 1; h >>= 1) {
+#pragma unroll
+            for (int i = 0; i < h; ++i) is[i] += __shfl_xor(is[i + h], h, 64);
+        }
+#pragma unroll
+        for (int off = P; off < 8; off <<= 1) is[0] += __shfl_xor(is[0], off, 64);
+        const float adp = *reinterpret_cast<const float *>(side + (size_t)(f * nb + lb) * kSideStride + 32);
+        if (j < P) accp += (t0 * adp) * (float)is[0];
+#pragma unroll
+        for (int q = P; q < M; ++q) {
+            const int tot = group_sum<8>(is[q]);
+            const float adq = *reinterpret_cast<const float *>(side + (size_t)(q * nb + lb) * kSideStride + 32);
+            if (j == 0) accx[q - P] += (t0 * adq) * (float)tot;
+        }
+    }
+    // across the eight super-block slots
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) accp += __shfl_xor(accp, off, 64);
+#pragma unroll
+    for (int q = P; q < M; ++q) accx[q - P] = group_sumf<64>(accx[q - P]);
+    if (row < n) {
+        if (lane < P) c[(size_t)lane * n + row] = accp;
+#pragma unroll
+        for (int q = P; q < M; ++q)
+            if (lane == 63 - (q - P)) c[(size_t)q * n + row] = accx[q - P];
+    }
+}
+
 template <int M>
 hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int64_t n, int64_t k,
                           hipStream_t stream) {
-    const dim3 grid((unsigned)((n + kThreads / 64 - 1) / (kThreads / 64)));
     const auto *wp = static_cast<const uint8_t *>(w);
     const auto *ap = static_cast<const uint8_t *>(a);
+    const int64_t nsb = k / 256;
+    if constexpr (M >= 2) {
+        if (kq_staged_lds_bytes(M, nsb) <= 160 * 1024) {
+            const dim3 sgrid((unsigned)((n + kStagedThreads / 64 - 1) / (kStagedThreads / 64)));
+            const size_t lds = (size_t)kq_staged_lds_bytes(M, nsb);
+            if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K)
+                hipLaunchKernelGGL(gemv_q4_K_staged_kernel<M>, sgrid, dim3(kStagedThreads), lds, stream, wp, ap, c,
+                                   (int)n, (int)nsb);
+            else
+                hipLaunchKernelGGL(gemv_iq2_xxs_staged_kernel<M>, sgrid, dim3(kStagedThreads), lds, stream, wp, ap, c,
+                                   (int)n, (int)nsb);
+            return hipGetLastError();
+        }
+    }
+    const dim3 grid((unsigned)((n + kThreads / 64 - 1) / (kThreads / 64)));
     if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K)
         hipLaunchKernelGGL(gemv_q4_K_kernel<M>, grid, dim3(kThreads), 0, stream, wp, ap, c, (int)n, (int)(k / 256));
     else

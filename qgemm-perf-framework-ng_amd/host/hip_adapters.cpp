@@ -199,7 +199,7 @@ using QT = QuantizationType;
 
 void register_q4_0_hip_mi355x() {
     add<QT::WeightQ4_0ActivationQ8_0, PFNG_PATH_AUTO>("q4_0-q8_0-HIP-mi355x",
-                                                      "Q4_0/Q8_0 HIP gfx950 (GEMV for M<=8, int8 MFMA otherwise)");
+                                                      "Q4_0/Q8_0 HIP gfx950 (GEMV for M<=16, int8 MFMA otherwise)");
     add<QT::WeightQ4_0ActivationQ8_0, PFNG_PATH_GEMV>("q4_0-q8_0-HIP-gemv", "Q4_0/Q8_0 HIP gfx950 wave-per-row GEMV");
     add<QT::WeightQ4_0ActivationQ8_0, PFNG_PATH_MFMA>("q4_0-q8_0-HIP-mfma", "Q4_0/Q8_0 HIP gfx950 int8 MFMA GEMM");
     add<QT::WeightQ4_0ActivationQ8_0, PFNG_PATH_NAIVE>("q4_0-q8_0-HIP-naive",
@@ -207,7 +207,7 @@ void register_q4_0_hip_mi355x() {
 }
 
 void register_q4_K_hip_mi355x() {
-    add<QT::WeightQ4_KActivationQ8_K, PFNG_PATH_AUTO>("q4_K-q8_K-HIP-mi355x", "Q4_K/Q8_K HIP gfx950 (GEMV for M<=6, int8 MFMA otherwise)");
+    add<QT::WeightQ4_KActivationQ8_K, PFNG_PATH_AUTO>("q4_K-q8_K-HIP-mi355x", "Q4_K/Q8_K HIP gfx950 (GEMV for M<=8, int8 MFMA otherwise)");
     add<QT::WeightQ4_KActivationQ8_K, PFNG_PATH_NAIVE>("q4_K-q8_K-HIP-naive",
                                                        "Q4_K/Q8_K HIP thread-per-output, reference fp32 order");
 }
