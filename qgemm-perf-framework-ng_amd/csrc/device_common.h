@@ -85,6 +85,7 @@ __device__ __forceinline__ float group_max(float v) {
 // largest power of two <= v for v in 1..16, and the log2 of a power of two
 constexpr int pow2_floor16(int v) { return v >= 16 ? 16 : (v >= 8 ? 8 : (v >= 4 ? 4 : (v >= 2 ? 2 : 1))); }
 constexpr int log2_pow2(int v) { return v == 16 ? 4 : (v == 8 ? 3 : (v == 4 ? 2 : (v == 2 ? 1 : 0))); }
+constexpr int pow2_ceil16(int v) { return v <= 1 ? 1 : (v <= 2 ? 2 : (v <= 4 ? 4 : (v <= 8 ? 8 : 16))); }
 
 template <int W>
 __device__ __forceinline__ int group_sum(int v) {

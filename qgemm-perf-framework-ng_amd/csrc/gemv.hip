@@ -283,7 +283,11 @@ template <int M>
 __global__ __launch_bounds__(kPairsThreads) void gemv_q4_0_pairs_kernel(const uint8_t *__restrict__ w,
                                                                        const uint8_t *__restrict__ a,
                                                                        float *__restrict__ c, int n, int nb) {
-    constexpr int P = pow2_floor16(M);
+    // reduce-scatter width: rows beyond the largest power of two <= M cost a
+    // plain butterfly each; at M = 7 and M >= 13 padding to the next power of
+    // two (dummy rows, never stored) measured faster
+    constexpr int P = M == 7 || M >= 13 ? pow2_ceil16(M) : pow2_floor16(M);
+    constexpr int NA = P > M ? P : M;              // accumulators per lane
     constexpr int kLaneShift = 6 - log2_pow2(P);  // lanes per reduce-scatter result: 1 << kLaneShift
     extern __shared__ __align__(16) uint8_t lds[];
     const int np = nb / 2;
@@ -308,12 +312,15 @@ __global__ __launch_bounds__(kPairsThreads) void gemv_q4_0_pairs_kernel(const ui
     const int row = blockIdx.x * (kPairsThreads / 64) + (threadIdx.x >> 6);
     const int lrow = row < n ? row : n - 1;  // clamped: loads stay unconditional, the store is guarded
     const int f = lane >> kLaneShift;        // < P
-    int arow[M];                             // activation row of accumulator j
+    int arow[NA];                            // activation row read for accumulator j (clamped)
 #pragma unroll
-    for (int j = 0; j < M; ++j) arow[j] = j < P ? j ^ f : j;
-    float acc[M];
+    for (int j = 0; j < NA; ++j) {
+        const int r = j < P ? j ^ f : j;
+        arow[j] = r < M ? r : M - 1;
+    }
+    float acc[NA];
 #pragma unroll
-    for (int j = 0; j < M; ++j) acc[j] = 0.0f;
+    for (int j = 0; j < NA; ++j) acc[j] = 0.0f;
     for (int p = lane; p < np; p += 64) {
         const uint32_t *ws = reinterpret_cast<const uint32_t *>(w + ((size_t)lrow * nb + 2 * p) * 18);
         uint32_t u[9];
@@ -329,7 +336,7 @@ __global__ __launch_bounds__(kPairsThreads) void gemv_q4_0_pairs_kernel(const ui
         }
         const float dw0 = fp16_to_f32(u[0] & 0xffffu), dw1 = fp16_to_f32(u[4] >> 16);
 #pragma unroll
-        for (int j = 0; j < M; ++j) {
+        for (int j = 0; j < NA; ++j) {
             const int t = arow[j] * np + p;
             const uint32_t *x = xq + (size_t)t * kPairDwords;
             const float2 da = xd[t];
@@ -359,7 +366,7 @@ __global__ __launch_bounds__(kPairsThreads) void gemv_q4_0_pairs_kernel(const ui
 #pragma unroll
     for (int j = P; j < M; ++j) acc[j] = group_sumf<64>(acc[j]);
     if (row < n) {
-        if ((lane & ((1 << kLaneShift) - 1)) == 0) c[(size_t)f * n + row] = acc[0] * 0.0625f;
+        if ((lane & ((1 << kLaneShift) - 1)) == 0 && f < M) c[(size_t)f * n + row] = acc[0] * 0.0625f;
 #pragma unroll
         for (int j = P; j < M; ++j)
             if (lane == 63 - (j - P)) c[(size_t)j * n + row] = acc[j] * 0.0625f;

@@ -203,10 +203,12 @@ __global__ __launch_bounds__(kThreads) void gemv_iq2_xxs_kernel(const uint8_t *_
 // over the banks) and a 48-byte side record with the eight per-sub-block bsum
 // pairs bsums[2j] + bsums[2j+1] as int32 and d as fp32. The waves then read
 // activations from LDS instead of issuing 16-19 dword loads per row each.
-// Cross-lane sums use the reduce-scatter of gemv_q4_0_pairs_kernel: P = the
-// largest power of two <= m accumulators hold activation row q ^ f(lane), so
-// every lane keeps the lower half of each exchange and accumulators are only
-// indexed by constants; the other m - P rows take a plain butterfly.
+// Cross-lane sums use the reduce-scatter of gemv_q4_0_pairs_kernel: P
+// accumulators hold activation row q ^ f(lane), so every lane keeps the lower
+// half of each exchange and accumulators are only indexed by constants. P is
+// the largest power of two <= m (the other m - P rows take a plain butterfly)
+// or, where that measured faster, the next power of two (accumulators of rows
+// >= m read a clamped row, combine only with each other, are never stored).
 constexpr int kStagedThreads = 1024;
 constexpr int kQsStride = 272, kSideStride = 48;
 
@@ -245,7 +247,9 @@ template <int M>
 __global__ __launch_bounds__(kStagedThreads) void gemv_q4_K_staged_kernel(const uint8_t *__restrict__ w,
                                                                          const uint8_t *__restrict__ a,
                                                                          float *__restrict__ c, int n, int nb) {
-    constexpr int P = pow2_floor16(M);
+    // reduce-scatter width: padded to 8 at M = 7 (dummy row, never stored), measured faster
+    constexpr int P = M == 7 ? 8 : pow2_floor16(M);
+    constexpr int NA = P > M ? P : M;  // accumulators per lane
     constexpr int kLaneShift = 6 - log2_pow2(P);
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t *qs = lds, *side = lds + (size_t)M * nb * kQsStride;
@@ -256,9 +260,9 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_q4_K_staged_kernel(const 
     const int lrow = row < n ? row : n - 1;  // clamped: loads stay unconditional, the store is guarded
     const int slot = lane >> 2, e = lane & 3;
     const int f = lane >> kLaneShift;
-    float acc[M];
+    float acc[NA];
 #pragma unroll
-    for (int q = 0; q < M; ++q) acc[q] = 0.0f;
+    for (int q = 0; q < NA; ++q) acc[q] = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += 16) {
         const int b = b0 + slot;
         const bool valid = b < nb;
@@ -280,9 +284,9 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_q4_K_staged_kernel(const 
         q4_K_scale_min(hd, 2 * e + 1, sc1, m1);
         const float d = fp16_to_f32(hd.x & 0xffffu), dmin = fp16_to_f32(hd.x >> 16);
 #pragma unroll
-        for (int q = 0; q < M; ++q) {
-            const int r = q < P ? q ^ f : q;
-            const int rec = r * nb + lb;
+        for (int q = 0; q < NA; ++q) {
+            const int r0 = q < P ? q ^ f : q;
+            const int rec = (r0 < M ? r0 : M - 1) * nb + lb;
             const uint4 *xq = reinterpret_cast<const uint4 *>(qs + (size_t)rec * kQsStride + 64 * e);
             uint32_t x[16];
 #pragma unroll
@@ -312,7 +316,7 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_q4_K_staged_kernel(const 
 #pragma unroll
     for (int q = P; q < M; ++q) acc[q] = group_sumf<64>(acc[q]);
     if (row < n) {
-        if ((lane & ((1 << kLaneShift) - 1)) == 0) c[(size_t)f * n + row] = acc[0];
+        if ((lane & ((1 << kLaneShift) - 1)) == 0 && f < M) c[(size_t)f * n + row] = acc[0];
 #pragma unroll
         for (int q = P; q < M; ++q)
             if (lane == 63 - (q - P)) c[(size_t)q * n + row] = acc[q];
@@ -329,8 +333,10 @@ template <int M>
 __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(const uint8_t *__restrict__ w,
                                                                             const uint8_t *__restrict__ a,
                                                                             float *__restrict__ c, int n, int nb) {
-    constexpr int P = pow2_floor16(M);
-    static_assert(P <= 8, "eight lanes per super-block");
+    // reduce-scatter width: padded to 8 from M = 6 on (dummy rows, never
+    // stored), where it measured faster than per-step butterflies of the rest
+    constexpr int P = M >= 6 ? 8 : pow2_floor16(M);
+    constexpr int NA = P > M ? P : M;
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t *qs = lds, *side = lds + (size_t)M * nb * kQsStride;
     uint8_t *grid = side + (size_t)M * nb * kSideStride;
@@ -354,9 +360,10 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(con
     const int slot = lane >> 3, j = lane & 7;
     const int f = j & (P - 1);
     float accp = 0.0f;       // row f, in lanes j < P
-    float accx[M - P + 1];   // rows P..M-1, in lanes j == 0
+    constexpr int NX = M > P ? M - P : 1;
+    float accx[NX];          // rows P..M-1, in lanes j == 0
 #pragma unroll
-    for (int q = 0; q <= M - P; ++q) accx[q] = 0.0f;
+    for (int q = 0; q < NX; ++q) accx[q] = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += 8) {
         const int b = b0 + slot;
         const bool valid = b < nb;
@@ -386,10 +393,11 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(con
         }
         const int scale = 2 * (int)(ss >> 28) + 1;
         const float t0 = valid ? 0.125f * fp16_to_f32(dh) : 0.0f;
-        int is[M];
+        int is[NA];
 #pragma unroll
-        for (int q = 0; q < M; ++q) {
-            const int r = q < P ? q ^ f : q;
+        for (int q = 0; q < NA; ++q) {
+            const int r0 = q < P ? q ^ f : q;
+            const int r = r0 < M ? r0 : M - 1;
             const uint4 *xq = reinterpret_cast<const uint4 *>(qs + (size_t)(r * nb + lb) * kQsStride + 32 * j);
             const uint4 x0 = xq[0], x1 = xq[1];
             const uint32_t x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
@@ -403,7 +411,8 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(con
         }
 #pragma unroll
         for (int off = P; off < 8; off <<= 1) is[0] += __shfl_xor(is[0], off, 64);
-        const float adp = *reinterpret_cast<const float *>(side + (size_t)(f * nb + lb) * kSideStride + 32);
+        const float adp =
+            *reinterpret_cast<const float *>(side + (size_t)((f < M ? f : M - 1) * nb + lb) * kSideStride + 32);
         if (j < P) accp += (t0 * adp) * (float)is[0];
 #pragma unroll
         for (int q = P; q < M; ++q) {
@@ -418,7 +427,7 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(con
 #pragma unroll
     for (int q = P; q < M; ++q) accx[q - P] = group_sumf<64>(accx[q - P]);
     if (row < n) {
-        if (lane < P) c[(size_t)lane * n + row] = accp;
+        if (lane < P && lane < M) c[(size_t)lane * n + row] = accp;
 #pragma unroll
         for (int q = P; q < M; ++q)
             if (lane == 63 - (q - P)) c[(size_t)q * n + row] = accx[q - P];

@@ -134,7 +134,7 @@ def test_naive_bit_exact(hip, torch_gpu, oracle, qtype, m, n, k):
 
 # ------------------------------------------------------------------- GEMV ----
 
-@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 9, 12, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 7, 8, 9, 12, 13, 15, 16])
 @pytest.mark.parametrize("n,k", [(4096, 4096), (257, 1536), (64, 256), (33, 8192), (40, 65536), (129, 7680),
                                  (77, 320), (50, 64)])
 def test_gemv_q4_0(hip, torch_gpu, oracle, m, n, k):
@@ -378,7 +378,7 @@ def test_mfma_in_graph_replays(hip, torch_gpu, oracle):
 # ------------------------------------------------------- q4_K / iq2_xxs GEMV ----
 
 @pytest.mark.parametrize("qtype", [1, 2])
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 7, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("n,k", [(4096, 4096), (257, 1536), (64, 256), (33, 8192), (20, 20480)])
 def test_gemv_kquant(hip, torch_gpu, oracle, qtype, m, n, k):
     """m = 1 reads the activations from global memory; m = 2..8 stage them in
