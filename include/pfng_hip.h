@@ -118,8 +118,10 @@ size_t pfng_hip_compute_workspace_size(int type, int64_t m, int64_t k);
 /* Replaces llama_reference::compute (llama_reference.h:18, .cpp:165-215):
  * quantizes the fp32 activations into workspace, then runs the product.
  * workspace must hold pfng_hip_compute_workspace_size() bytes. For q4_0 with
- * m <= 8 and PFNG_PATH_AUTO or PFNG_PATH_GEMV the quantization is fused into
- * the GEMV kernel (same q8_0 bytes, kept in LDS) and workspace is not written. */
+ * m <= 2, k % 64 == 0, m * (k / 32) * 34 <= 65536 and PFNG_PATH_AUTO or
+ * PFNG_PATH_GEMV the quantization is fused into the GEMV kernel (same q8_0
+ * bytes, kept in LDS) and workspace is not written; from m = 3 on the separate
+ * quantize launch is cheaper than quantizing again in every workgroup. */
 int pfng_hip_compute(int type, const float *activation, const void *weight, float *out, int64_t m, int64_t n,
                      int64_t k, void *workspace, size_t workspace_bytes, int path, void *stream);
 
