@@ -42,16 +42,16 @@ typedef enum {
 } pfng_status;
 
 /* Matrix-product implementations; PFNG_PATH_AUTO picks per shape (the GEMV
- * where it applies: q4_0 up to m = 16, q4_K and iq2_xxs up to m = 8; then the
- * MFMA tiles). */
+ * where it applies, up to m = 16; then the MFMA tiles). */
 typedef enum {
     PFNG_PATH_AUTO = 0,
     PFNG_PATH_GEMV = 1,  /* wavefront-per-row GEMV, no MFMA: q4_0 for m <= 16
                             with k % 64 == 0 for m == 1; for m = 2..16 when the
                             LDS-staged activations fit, k % 64 == 0 and
                             m * (k / 64) * 76 + 16 <= 163840, and for m = 2..8
-                            also every k % 256 == 0; q4_K and iq2_xxs for
-                            m <= 8 and every k % 256 == 0 */
+                            also every k % 256 == 0; q4_K and iq2_xxs with
+                            k % 256 == 0 for m <= 8, and for m = 9..16 while
+                            m * (k / 256) * 320 + 2048 <= 163840 */
     PFNG_PATH_MFMA = 2,  /* int8-MFMA GEMM, LDS-staged tiles: q4_0 with k % 128 == 0,
                             q4_K and iq2_xxs for every k % 256 == 0 */
     PFNG_PATH_NAIVE = 3  /* one thread per output, the reference's exact fp32 order */

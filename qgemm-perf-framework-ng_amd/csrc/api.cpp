@@ -150,13 +150,13 @@ int pfng_hip_mul_mat(int type, const void *weight, const void *act_q, float *out
     const bool mfma_ok = base_aligned && pfng::mfma_supported(type, m, k);
     switch (path) {
     case PFNG_PATH_AUTO:
-        // measured at 4096x4096: every GEMV that applies (q4_0 up to m = 16,
-        // the K-quants up to m = 8) is faster than the MFMA tiles
+        // measured at 4096x4096: every GEMV that applies (up to m = 16) is
+        // faster than the MFMA tiles
         if (gemv_ok) return hip_status(pfng::launch_gemv(type, weight, act_q, out, m, n, k, s), "gemv launch");
         if (mfma_ok) return launch_mfma(type, weight, act_q, out, m, n, k, s);
         return hip_status(pfng::launch_naive_mul_mat(type, weight, act_q, out, m, n, k, s), "naive launch");
     case PFNG_PATH_GEMV:
-        if (!gemv_ok) return fail(PFNG_ERR_UNSUPPORTED, "%s GEMV path needs m<=8 (q4_0: m<=16; k%%64==0 for m==1; else k%%64==0 with m*(k/64)*76+16<=163840, or k%%256==0 for m<=8) and 16-byte aligned operands (m=%lld k=%lld)", type_name(type), (long long)m, (long long)k);
+        if (!gemv_ok) return fail(PFNG_ERR_UNSUPPORTED, "%s GEMV path needs m<=16 (q4_0: k%%64==0 for m==1, else k%%64==0 with m*(k/64)*76+16<=163840, or k%%256==0 for m<=8; q4_K/iq2_xxs: k%%256==0, for m>8 also m*(k/256)*320+2048<=163840) and 16-byte aligned operands (m=%lld k=%lld)", type_name(type), (long long)m, (long long)k);
         return hip_status(pfng::launch_gemv(type, weight, act_q, out, m, n, k, s), "gemv launch");
     case PFNG_PATH_MFMA:
         if (!mfma_ok) return fail(PFNG_ERR_UNSUPPORTED, "%s MFMA path not available for m=%lld k=%lld", type_name(type), (long long)m, (long long)k);

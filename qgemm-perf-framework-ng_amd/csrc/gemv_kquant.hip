@@ -247,8 +247,9 @@ template <int M>
 __global__ __launch_bounds__(kStagedThreads) void gemv_q4_K_staged_kernel(const uint8_t *__restrict__ w,
                                                                          const uint8_t *__restrict__ a,
                                                                          float *__restrict__ c, int n, int nb) {
-    // reduce-scatter width: padded to 8 at M = 7 (dummy row, never stored), measured faster
-    constexpr int P = M == 7 ? 8 : pow2_floor16(M);
+    // reduce-scatter width: padded to the next power of two at M = 7 and
+    // M >= 13 (dummy rows, never stored), where that measured faster
+    constexpr int P = M == 7 || M >= 13 ? pow2_ceil16(M) : pow2_floor16(M);
     constexpr int NA = P > M ? P : M;  // accumulators per lane
     constexpr int kLaneShift = 6 - log2_pow2(P);
     extern __shared__ __align__(16) uint8_t lds[];
@@ -326,17 +327,22 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_q4_K_staged_kernel(const 
 // iq2_xxs: eight lanes per super-block as gemv_iq2_xxs_kernel, eight
 // super-blocks per wave and step. The integer super-block sums are completed
 // across the eight lanes before any scaling (the bound of this format is per
-// super-block): accumulator q < P of lane j holds activation row q ^ (j % P),
-// a reduce-scatter over the low lane bits leaves lane j with the exact sum of
-// row j % P, and lanes j < P scale it once.
+// super-block). Rows go in NG groups of P: accumulator q < NG * P of lane j
+// holds activation row P * (q / P) + ((q % P) ^ (j % P)), a reduce-scatter
+// over the low lane bits leaves lane j with the exact sum of row
+// P * g + j % P of each group g, and lanes j < P scale it once. With one group
+// the rows past P (if any) take a plain butterfly each.
 template <int M>
 __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(const uint8_t *__restrict__ w,
                                                                             const uint8_t *__restrict__ a,
                                                                             float *__restrict__ c, int n, int nb) {
-    // reduce-scatter width: padded to 8 from M = 6 on (dummy rows, never
-    // stored), where it measured faster than per-step butterflies of the rest
-    constexpr int P = M >= 6 ? 8 : pow2_floor16(M);
-    constexpr int NA = P > M ? P : M;
+    // groups of 8 rows above M = 8; up to 8, one group padded to 8 from M = 6
+    // on (dummy rows, never stored), where that measured faster than
+    // per-step butterflies of the rows past the largest power of two
+    constexpr int NG = (M + 7) / 8;
+    constexpr int P = NG > 1 || M >= 6 ? 8 : pow2_floor16(M);
+    constexpr int NX = NG * P < M ? M - NG * P : 0;  // rows past the groups (one group only)
+    constexpr int NA = NG * P + NX;
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t *qs = lds, *side = lds + (size_t)M * nb * kQsStride;
     uint8_t *grid = side + (size_t)M * nb * kSideStride;
@@ -359,11 +365,12 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(con
     const int lrow = row < n ? row : n - 1;
     const int slot = lane >> 3, j = lane & 7;
     const int f = j & (P - 1);
-    float accp = 0.0f;       // row f, in lanes j < P
-    constexpr int NX = M > P ? M - P : 1;
-    float accx[NX];          // rows P..M-1, in lanes j == 0
+    float accp[NG];                          // row P * g + f, in lanes j < P
+    float accx[NX > 0 ? NX : 1];             // rows NG * P.., in lanes j == 0
 #pragma unroll
-    for (int q = 0; q < NX; ++q) accx[q] = 0.0f;
+    for (int g = 0; g < NG; ++g) accp[g] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < (NX > 0 ? NX : 1); ++q) accx[q] = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += 8) {
         const int b = b0 + slot;
         const bool valid = b < nb;
@@ -396,41 +403,50 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(con
         int is[NA];
 #pragma unroll
         for (int q = 0; q < NA; ++q) {
-            const int r0 = q < P ? q ^ f : q;
+            const int r0 = q < NG * P ? P * (q / P) + ((q % P) ^ f) : q;
             const int r = r0 < M ? r0 : M - 1;
             const uint4 *xq = reinterpret_cast<const uint4 *>(qs + (size_t)(r * nb + lb) * kQsStride + 32 * j);
             const uint4 x0 = xq[0], x1 = xq[1];
             const uint32_t x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
             is[q] = scale * dot8(v, x);
         }
-        // exact integer sums over the eight lanes of the super-block
 #pragma unroll
-        for (int h = P / 2; h >= 1; h >>= 1) {
+        for (int g = 0; g < NG; ++g) {
+            // exact integer sums over the eight lanes of the super-block
 #pragma unroll
-            for (int i = 0; i < h; ++i) is[i] += __shfl_xor(is[i + h], h, 64);
+            for (int h = P / 2; h >= 1; h >>= 1) {
+#pragma unroll
+                for (int i = 0; i < h; ++i) is[P * g + i] += __shfl_xor(is[P * g + i + h], h, 64);
+            }
+#pragma unroll
+            for (int off = P; off < 8; off <<= 1) is[P * g] += __shfl_xor(is[P * g], off, 64);
+            const int rp = P * g + f;
+            const float adp = *reinterpret_cast<const float *>(
+                side + (size_t)((rp < M ? rp : M - 1) * nb + lb) * kSideStride + 32);
+            if (j < P) accp[g] += (t0 * adp) * (float)is[P * g];
         }
 #pragma unroll
-        for (int off = P; off < 8; off <<= 1) is[0] += __shfl_xor(is[0], off, 64);
-        const float adp =
-            *reinterpret_cast<const float *>(side + (size_t)((f < M ? f : M - 1) * nb + lb) * kSideStride + 32);
-        if (j < P) accp += (t0 * adp) * (float)is[0];
-#pragma unroll
-        for (int q = P; q < M; ++q) {
+        for (int q = NG * P; q < NA; ++q) {
             const int tot = group_sum<8>(is[q]);
             const float adq = *reinterpret_cast<const float *>(side + (size_t)(q * nb + lb) * kSideStride + 32);
-            if (j == 0) accx[q - P] += (t0 * adq) * (float)tot;
+            if (j == 0) accx[q - NG * P] += (t0 * adq) * (float)tot;
         }
     }
     // across the eight super-block slots
 #pragma unroll
-    for (int off = 8; off < 64; off <<= 1) accp += __shfl_xor(accp, off, 64);
+    for (int g = 0; g < NG; ++g) {
 #pragma unroll
-    for (int q = P; q < M; ++q) accx[q - P] = group_sumf<64>(accx[q - P]);
+        for (int off = 8; off < 64; off <<= 1) accp[g] += __shfl_xor(accp[g], off, 64);
+    }
+#pragma unroll
+    for (int q = 0; q < NX; ++q) accx[q] = group_sumf<64>(accx[q]);
     if (row < n) {
-        if (lane < P && lane < M) c[(size_t)lane * n + row] = accp;
 #pragma unroll
-        for (int q = P; q < M; ++q)
-            if (lane == 63 - (q - P)) c[(size_t)q * n + row] = accx[q - P];
+        for (int g = 0; g < NG; ++g)
+            if (lane < P && P * g + lane < M) c[(size_t)(P * g + lane) * n + row] = accp[g];
+#pragma unroll
+        for (int q = 0; q < NX; ++q)
+            if (lane == 63 - q) c[(size_t)(NG * P + q) * n + row] = accx[q];
     }
 }
 
@@ -453,16 +469,25 @@ hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int6
             return hipGetLastError();
         }
     }
-    const dim3 grid((unsigned)((n + kThreads / 64 - 1) / (kThreads / 64)));
-    if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K)
-        hipLaunchKernelGGL(gemv_q4_K_kernel<M>, grid, dim3(kThreads), 0, stream, wp, ap, c, (int)n, (int)(k / 256));
-    else
-        hipLaunchKernelGGL(gemv_iq2_xxs_kernel<M>, grid, dim3(kThreads), 0, stream, wp, ap, c, (int)n,
-                           (int)(k / 256));
-    return hipGetLastError();
+    if constexpr (M <= 8) {
+        // activations read from global memory (m == 1, or rows too long to stage)
+        const dim3 grid((unsigned)((n + kThreads / 64 - 1) / (kThreads / 64)));
+        if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K)
+            hipLaunchKernelGGL(gemv_q4_K_kernel<M>, grid, dim3(kThreads), 0, stream, wp, ap, c, (int)n,
+                               (int)(k / 256));
+        else
+            hipLaunchKernelGGL(gemv_iq2_xxs_kernel<M>, grid, dim3(kThreads), 0, stream, wp, ap, c, (int)n,
+                               (int)(k / 256));
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
+
+bool kquant_gemv_staged_fits(int64_t m, int64_t k) {
+    return m >= 2 && m <= 16 && k % 256 == 0 && kq_staged_lds_bytes(m, k / 256) <= 160 * 1024;
+}
 
 hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                               hipStream_t stream) {
@@ -477,6 +502,14 @@ hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, 
     case 6: return launch_kq_gemv<6>(type, w, a, c, n, k, stream);
     case 7: return launch_kq_gemv<7>(type, w, a, c, n, k, stream);
     case 8: return launch_kq_gemv<8>(type, w, a, c, n, k, stream);
+    case 9: return launch_kq_gemv<9>(type, w, a, c, n, k, stream);
+    case 10: return launch_kq_gemv<10>(type, w, a, c, n, k, stream);
+    case 11: return launch_kq_gemv<11>(type, w, a, c, n, k, stream);
+    case 12: return launch_kq_gemv<12>(type, w, a, c, n, k, stream);
+    case 13: return launch_kq_gemv<13>(type, w, a, c, n, k, stream);
+    case 14: return launch_kq_gemv<14>(type, w, a, c, n, k, stream);
+    case 15: return launch_kq_gemv<15>(type, w, a, c, n, k, stream);
+    case 16: return launch_kq_gemv<16>(type, w, a, c, n, k, stream);
     default: return hipErrorInvalidValue;
     }
 }

@@ -207,14 +207,14 @@ void register_q4_0_hip_mi355x() {
 }
 
 void register_q4_K_hip_mi355x() {
-    add<QT::WeightQ4_KActivationQ8_K, PFNG_PATH_AUTO>("q4_K-q8_K-HIP-mi355x", "Q4_K/Q8_K HIP gfx950 (GEMV for M<=8, int8 MFMA otherwise)");
+    add<QT::WeightQ4_KActivationQ8_K, PFNG_PATH_AUTO>("q4_K-q8_K-HIP-mi355x", "Q4_K/Q8_K HIP gfx950 (GEMV for M<=16, int8 MFMA otherwise)");
     add<QT::WeightQ4_KActivationQ8_K, PFNG_PATH_NAIVE>("q4_K-q8_K-HIP-naive",
                                                        "Q4_K/Q8_K HIP thread-per-output, reference fp32 order");
 }
 
 void register_iq2_xxs_hip_mi355x() {
     add<QT::WeightIQ2_XXSActivationQ8_K, PFNG_PATH_AUTO>("iq2_xxs-q8_K-HIP-mi355x",
-                                                         "IQ2_XXS/Q8_K HIP gfx950 (GEMV for M<=8, int8 MFMA otherwise)");
+                                                         "IQ2_XXS/Q8_K HIP gfx950 (GEMV for M<=16, int8 MFMA otherwise)");
     add<QT::WeightIQ2_XXSActivationQ8_K, PFNG_PATH_NAIVE>("iq2_xxs-q8_K-HIP-naive",
                                                           "IQ2_XXS/Q8_K HIP thread-per-output, reference fp32 order");
 }

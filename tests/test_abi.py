@@ -59,9 +59,10 @@ def test_version_string(pkg):
     (lambda L: L.pfng_hip_mul_mat(0, None, None, None, 4, 4, 64, 0, None), 1),
     (lambda L: L.pfng_hip_mul_mat(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 4, 4, 64, 9, None), 1),
     (lambda L: L.pfng_hip_mul_mat(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 64, 4, 96, 2, None), 2),
-    # the GEMV takes q4_0 up to m = 16 and the K-quants up to m = 8
+    # the GEMV takes up to m = 16 (m > 8 only while the activations fit in LDS)
     (lambda L: L.pfng_hip_mul_mat(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 17, 4, 256, 1, None), 2),
-    (lambda L: L.pfng_hip_mul_mat(1, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 9, 4, 256, 1, None), 2),
+    (lambda L: L.pfng_hip_mul_mat(1, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 17, 4, 256, 1, None), 2),
+    (lambda L: L.pfng_hip_mul_mat(2, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 9, 4, 20480, 1, None), 2),
     (lambda L: L.pfng_hip_compute(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 4, 4, 64, None, 10, 0, None), 1),
     (lambda L: L.pfng_hip_block_isums(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 4, 4, 96, None), 2),
 ])
