@@ -13,6 +13,11 @@ Two sub-commands, so that the profiler itself is started from the command line
              configuration's kernel: average duration, algorithmic bytes and
              ops, HBM bytes per launch (counter KiB x the copy calibration
              factor), and the fractions of the 8 TB/s and 5.0 POPS peaks.
+             Optional --sq runs (SQ_ counters, at most 8 per run) add the
+             per-dispatch counters and, for the GEMMs, the VALU / MFMA / LDS
+             wave-instructions per item (one 32x32x32 int8 MFMA tile, 65536
+             ops): the VALU work an item needs against the 32 cycles of its
+             int8 MFMA, and the cycles per item the run achieved per SIMD.
 
 Example (the three profiler passes, then the summary):
   python3 qgemm-perf-framework-ng_amd/evidence.py workload --config c1 --iters 200   # under rocprofv3
@@ -32,6 +37,11 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 COPY_BYTES = 256 << 20
+SIMDS = 256 * 4            # MI355X: 256 CUs of 4 SIMDs
+PEAK_CLOCK_GHZ = 2.4       # the clock the published peaks assume
+ITEM_OPS = 2 * 32 * 32 * 32
+VALU_CYCLES_PER_INST = 4   # a wave64 VALU instruction on a 16-lane SIMD (no packed fp32)
+MFMA_CYCLES_PER_ITEM = 32  # v_mfma_i32_32x32x32_i8 at the 5.0 POPS peak
 
 # name, qtype, m, n, k, input variant, kernel-name substring, bound
 CONFIGS = {
@@ -147,6 +157,29 @@ def summarize(args):
                            "copy_write_kib": round(w_c, 1), "calibration_fetch": round(ff, 4),
                            "calibration_write": round(fw, 4), "hbm_bytes_per_launch": int(round(hbm)),
                            "hbm_over_algorithmic": round(hbm / alg["bytes"], 3)})
+    if args.sq:
+        sq = {}
+        for root in args.sq:
+            for r in read_csvs(root, "counter_collection.csv"):
+                if kname in r["Kernel_Name"] and r.get("Counter_Name", "").startswith(("SQ_", "GRBM_")):
+                    sq.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+        for name in sorted(sq):
+            report[f"{name}_per_dispatch"] = round(sum(sq[name]) / len(sq[name]), 1)
+        if bound == "mfma" and "SQ_INSTS_VALU" in sq:
+            items = alg["ops"] / ITEM_OPS
+            per = {name: sum(v) / len(v) / items for name, v in sq.items()}
+            report["items_per_launch"] = int(items)
+            report["valu_insts_per_item"] = round(per["SQ_INSTS_VALU"], 2)
+            if "SQ_INSTS_MFMA" in per:
+                report["mfma_insts_per_item"] = round(per["SQ_INSTS_MFMA"], 2)
+                valu_only = per["SQ_INSTS_VALU"] - per["SQ_INSTS_MFMA"]
+                report["non_mfma_valu_insts_per_item"] = round(valu_only, 2)
+                report["valu_cycles_per_item"] = round(valu_only * VALU_CYCLES_PER_INST, 1)
+            if "SQ_INSTS_LDS" in per:
+                report["lds_insts_per_item"] = round(per["SQ_INSTS_LDS"], 2)
+            report["mfma_cycles_per_item_at_peak"] = MFMA_CYCLES_PER_ITEM
+            report["achieved_cycles_per_item_per_simd"] = round(
+                avg_ns * 1e-9 * PEAK_CLOCK_GHZ * 1e9 * SIMDS / items, 1)
     lines = [f"# {kname} — {args.config}: {label}", "",
              "Produced by `qgemm-perf-framework-ng_amd/evidence.py summarize` from rocprofv3 runs of",
              f"`evidence.py workload --config {args.config}`.", "", "Commands:", "```"]
@@ -238,6 +271,7 @@ def main():
     s.add_argument("--trace", required=True, help="output directory of the --kernel-trace --stats run")
     s.add_argument("--fetch", help="output directory of the --pmc FETCH_SIZE run")
     s.add_argument("--write", help="output directory of the --pmc WRITE_SIZE run")
+    s.add_argument("--sq", action="append", help="output directory of an --pmc run of SQ_ counters (repeatable)")
     s.add_argument("--md", help="Markdown summary to write")
     s.add_argument("--json", help="traffic table to update")
     s.add_argument("--command", action="append", help="profiler command line to record in the summary")
