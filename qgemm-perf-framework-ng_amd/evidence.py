@@ -52,6 +52,13 @@ CONFIGS = {
     "c3": ("iq2_xxs x q8_K GEMM M=512 N=4096 K=4096 (baseline weight generator)", 2, 512, 4096, 4096, 1,
            "gemm_kq_kernel", "mfma"),
     "c4": ("q4_0 x q8_0 GEMM M=2048 N=11008 K=4096", 0, 2048, 11008, 4096, 0, "gemm_q4_0_kernel", "mfma"),
+    # decode batches: the M = 2..16 GEMV kernels, not baseline configurations
+    "m8_q4_0": ("q4_0 x q8_0 GEMV M=8 N=4096 K=4096, 32 rotating weight copies", 0, 8, 4096, 4096, 0,
+                "gemv_q4_0_pairs_kernel", "hbm"),
+    "m8_q4_K": ("q4_K x q8_K GEMV M=8 N=4096 K=4096, 32 rotating weight copies", 1, 8, 4096, 4096, 0,
+                "gemv_q4_K_staged_kernel", "hbm"),
+    "m8_iq2_xxs": ("iq2_xxs x q8_K GEMV M=8 N=4096 K=4096, 32 rotating weight copies", 2, 8, 4096, 4096, 1,
+                   "gemv_iq2_xxs_staged_kernel", "hbm"),
 }
 WB = {0: 18, 1: 144, 2: 66}
 AB = {0: 34, 1: 292, 2: 292}
@@ -83,7 +90,7 @@ def run_workload(cfg, iters):
     label, qt, m, n, k, variant, _, _ = CONFIGS[cfg]
     print(f"[evidence] {cfg}: {label}, {iters} launches", flush=True)
     act, w = pkg.create_input(qt, m, n, k, seed=1, variant=variant)
-    copies = 32 if cfg == "c1" else 1
+    copies = 32 if CONFIGS[cfg][7] == "hbm" else 1  # GEMVs: more weight bytes than the 256 MB MALL holds
     base = torch.from_numpy(w).cuda()
     weights = [base] + [base.clone() for _ in range(copies - 1)]
     aq = pkg.quantize_activation(qt, torch.from_numpy(act).cuda())
