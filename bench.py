@@ -12,6 +12,8 @@ One step = one pass of the hot path over one batch of synthetic input:
   * q4_K, iq2_xxs, prefill: configs 2, 3 and 4 in the same form.
   * gemv_q4_K, gemv_iq2_xxs: the M=1 GEMV of the super-block formats at
     N=K=4096 (not baseline configs; reported beside the headline).
+  * decode: the M=8 and M=16 GEMVs (decode batches) of all three formats at
+    N=K=4096, 32 rotating weight copies (not baseline configs).
 Inputs come from the product's own generator (pfng_host_create_input, the
 reference harness's mt19937 draws and host quantizers). Activations are
 quantized once before the timed region (the reference quantizes in prepare(),
@@ -273,6 +275,8 @@ def main():
     ap.add_argument("--iq2-steps", type=int, default=512, help="timed c3 GEMM steps (0 = skip)")
     ap.add_argument("--prefill-steps", type=int, default=64, help="timed c4 GEMM steps (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=16.0, help="bounded CPU-baseline budget (0 = skip)")
+    ap.add_argument("--decode-steps", type=int, default=None,
+                    help="timed steps of each M=8/M=16 decode GEMV (default steps/8, 0 = skip)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -337,11 +341,23 @@ def main():
                          4096, args.steps // 4, args.warmup // 4, variant, f"gemv_{name}_kernel<1>")
                for qt, name, variant in ((1, "q4_K", pkg.INPUT_REFERENCE), (2, "iq2_xxs", pkg.INPUT_BASELINE))]
 
+    decode_steps = args.steps // 8 if args.decode_steps is None else args.decode_steps
+    decode = []
+    if decode_steps > 0:
+        for qt, name, variant, kern in ((0, "q4_0", pkg.INPUT_REFERENCE, "gemv_q4_0_pairs_kernel"),
+                                        (1, "q4_K", pkg.INPUT_REFERENCE, "gemv_q4_K_staged_kernel"),
+                                        (2, "iq2_xxs", pkg.INPUT_BASELINE, "gemv_iq2_xxs_staged_kernel")):
+            act_t = "q8_0" if qt == 0 else "q8_K"
+            for dm in (8, 16):
+                decode.append(gemv_item(torch, pkg, f"m{dm}_{name}: {name} x {act_t} GEMV M={dm} N=4096 K=4096, "
+                                        "32 rotating weight copies", qt, dm, 4096, 4096, decode_steps,
+                                        max(decode_steps // 10, 32), variant, f"{kern}<{dm}>"))
+
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
     if cpu:
         log(f"[bench] cpu baseline: {cpu}")
 
-    items = [x for x in (gemm, q4k, iq2, prefill, *gemv_kq) if x is not None]
+    items = [x for x in (gemm, q4k, iq2, prefill, *gemv_kq, *decode) if x is not None]
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -369,6 +385,7 @@ def main():
         "prefill": prefill,
         "gemv_q4_K": gemv_kq[0],
         "gemv_iq2_xxs": gemv_kq[1],
+        "decode": decode,
         "verified": bool(ver1["passed"] and all(x["verify"]["passed"] for x in items)),
         "cpu_baseline": cpu,
     }

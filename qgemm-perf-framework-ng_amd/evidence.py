@@ -227,6 +227,8 @@ def bench_stats(args):
     for key in ("gemm", "q4_K", "iq2_xxs", "prefill", "gemv_q4_K", "gemv_iq2_xxs"):
         if isinstance(line.get(key), dict):
             items.append((key, line[key].get("roofline")))
+    for it in line.get("decode") or []:
+        items.append((it["workload"].split(":")[0], it.get("roofline")))
 
     def short(name):
         name = name.replace("(anonymous namespace)::", "").replace("pfng::", "")
@@ -249,7 +251,9 @@ def bench_stats(args):
             continue
         kname = roof["kernel"]
         base, _, tag = kname.partition("<")
-        tag = {"q4_K": "(Kq)0", "iq2_xxs": "(Kq)1"}.get(tag.rstrip(">"), "")
+        tag = tag.rstrip(">")
+        # K-quant tiles are tagged by type; GEMV instantiations by their row count
+        tag = {"q4_K": "(Kq)0", "iq2_xxs": "(Kq)1"}.get(tag, f"<{tag}>" if tag.isdigit() else "")
         match = [r for r in stats if base in r["Name"] and tag in short(r["Name"])]
         # one line per instantiation: the plan picks the tile configuration by shape
         for r in match or [None]:
