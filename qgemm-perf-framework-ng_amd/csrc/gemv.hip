@@ -1,18 +1,24 @@
-// GEMV path (m <= 8; q4_0 up to m = 16) for gfx950: no MFMA, the weight stream
-// is the roofline.
+// q4_0 x q8_0 GEMV path (m <= 16) for gfx950: no MFMA, the weight stream is
+// the roofline. Four kernels, picked in launch_gemv / launch_fused_gemv:
 //
-// Work decomposition. The weight matrix is a stream of 18-byte q4_0 blocks.
-// Eight consecutive blocks (a "group", 144 B) start on a 16-byte boundary
-// whenever k % 256 == 0, so every lane loads its group with nine 16-byte loads
-// and decodes the blocks from registers (bytes sit at fixed offsets 18*j).
-// A wavefront is split into 64/L row slots of L lanes; the L lanes of a slot
-// walk the groups of one weight row and are reduced with cross-lane shuffles.
-// All loads of a lane are issued before any arithmetic, so the whole weight
-// stream of the grid is in flight at once.
+//   gemv_q4_0_m1_kernel        m == 1: one wavefront per weight row, one q4_0
+//                              block pair (36 B) per lane, the activation row
+//                              copied into LDS once per 16-row workgroup.
+//   gemv_q4_0_pairs_kernel     m = 2..16 while the staged activations fit LDS:
+//                              the same row/pair mapping, the m activation
+//                              rows staged realigned with fp32 scales, a
+//                              reduce-scatter across the wave at the end.
+//   gemv_q4_0_kernel           m = 2..8 with longer rows (k % 256 == 0): groups
+//                              of eight blocks (144 B, 16-byte aligned) per
+//                              lane, L lanes per row, activations staged in
+//                              LDS chunk by chunk (272 B per group: 8 x 32 int8
+//                              bytes, then the 8 fp16 scales).
+//   gemv_q4_0_fused_kernel     pfng_hip_compute for m <= 2: quantizes the fp32
+//                              activation rows into LDS, then as the m1 kernel.
 //
-// Activations (m <= 8 rows of q8_0) are staged once per workgroup into LDS in
-// a layout that makes the per-lane reads bank-conflict free: for every group,
-// 8 x 32 bytes of int8 followed by the 8 fp16 scales (272 B per group).
+// Every lane issues all the loads of a step before any arithmetic, so the
+// weight stream of the grid is in flight at once; weight rows are clamped so
+// loads stay unconditional and only the stores are guarded.
 //
 // Arithmetic per block (exact integer part, then fp32):
 //   w16 = 16 * (nibble - 8) packed as int8 (q4_0_unpack16), isum16 = sum w16 * a
@@ -263,7 +269,9 @@ __global__ __launch_bounds__(kLdsAct ? 1024 : kThreads) void gemv_q4_0_m1_kernel
 // lane bits the exchanges run over, so that every lane keeps the lower half
 // and sends the upper half: the lane dependence sits in the LDS read address
 // and accumulators are only ever indexed by constants (a lane-dependent
-// choice between accumulators becomes a scratch-memory array).
+// choice between accumulators becomes a scratch-memory array). For some m, P
+// is the next power of two instead: accumulators of rows >= m then read a
+// clamped row, only ever combine with each other, and are never stored.
 constexpr int kPairsThreads = 1024;
 constexpr int kPairDwords = 17;  // 16 int8 dwords + 1 pad
 
@@ -478,8 +486,9 @@ hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n,
 
 // Fusing pays only while the quantization repeated in every workgroup is
 // cheaper than the separate quantize launch: measured at n = k = 4096, fused
-// against quantize + GEMV, m = 1: 4.75 vs 6.43 us, m = 2: 6.02 vs 6.75 us,
-// m = 3: 7.6 vs 7.4 us, m = 8: 13.9 vs 9.4 us.
+// against quantize + GEMV, m = 1: 4.75 vs 6.43 us, m = 2: 6.02 vs 6.75 us; a
+// fused variant of the m = 2..16 kernel took 7.6 vs 7.4 us at m = 3 and 13.9
+// vs 9.4 us at m = 8.
 bool fused_gemv_supported(int type, int64_t m, int64_t k) {
     return type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0 && m >= 1 && m <= 2 && k % 64 == 0 &&
            m * (k / 32) * 34 <= 65536;

@@ -1,9 +1,12 @@
-// GEMV path (m <= 8) for the super-block formats against q8_K activations:
+// GEMV path (m <= 16) for the super-block formats against q8_K activations:
 // q4_K (llama_reference.cpp:113-132) and iq2_xxs (llama_reference.cpp:148-161,
 // kernels/common/iq2_xxs.h:29-41). No MFMA: one wavefront per weight row,
 // the weight stream read with aligned 16-byte (q4_K) or realigned dword
 // (iq2_xxs, 66-byte blocks) loads, all loads of a step issued before any
-// arithmetic, int8 dots with v_dot4_i32_i8.
+// arithmetic, int8 dots with v_dot4_i32_i8. gemv_q4_K_kernel and
+// gemv_iq2_xxs_kernel (m <= 8) read the activations from global memory: m == 1,
+// and rows too long to stage; the *_staged_kernel variants (m = 2..16) stage
+// them in LDS once per 16-row workgroup.
 //
 // q4_K: four lanes per super-block, lane e owning sub-blocks 2e and 2e+1 (the
 // 32 nibble bytes qs[32e .. 32e+32): low nibbles of sub-block 2e, high of
