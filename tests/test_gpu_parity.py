@@ -35,6 +35,36 @@ def host_blocks(t, dtype):
     return b.reshape(-1).view(dtype).reshape(b.shape[0], -1)
 
 
+def doubled_scales(w):
+    """Copy of weight blocks with every fp16 `d` (and q4_K's `dmin`) multiplied
+    by 2 exactly (the exponent field raised by one; all scales here are normal
+    and far from the fp16 maximum). Every output of a correct product doubles
+    exactly."""
+    w2 = w.copy()
+    for field in ("d", "dmin"):
+        if field not in w2.dtype.names:
+            continue
+        bits = w2[field].view(np.uint16)
+        exp = (bits >> 10) & 0x1F
+        assert ((exp >= 1) & (exp <= 29)).all()
+        w2[field] = (bits + np.uint16(1 << 10)).view(w2[field].dtype)
+    return w2
+
+
+def check_full_size_properties(hip, torch, qtype, w, wt, aq_t, got, m, n, k):
+    """Size-independent checks on a whole output: permuting weight rows
+    permutes output columns bit for bit (each column's arithmetic is independent
+    of its tile), and doubling every weight scale doubles every output exactly."""
+    permn = torch.randperm(n, generator=torch.Generator().manual_seed(1)).cuda()
+    got_n = hip.mul_mat(qtype, wt[permn].contiguous(), aq_t, m, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(got_n, got[:, permn])
+    del got_n
+    got_2 = hip.mul_mat(qtype, dev(torch, doubled_scales(w)), aq_t, m, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(got_2, got * 2)
+
+
 def run_mul_mat(hip, torch, qtype, w, aq, m, n, k, path):
     out = hip.mul_mat(qtype, dev(torch, w), dev(torch, aq), m, n, k, path=path)
     torch.cuda.synchronize()
@@ -198,7 +228,8 @@ def test_config1_gemv_full_size(hip, torch_gpu, oracle):
 
 def test_config4_prefill_full_size_sampled(hip, torch_gpu, oracle):
     """c4: q4_0 GEMM M=2048 N=11008 K=4096; oracle on 24 seeded rows plus
-    size-independent checks on the whole output (finite, row-permutation equivariance)."""
+    size-independent checks on the whole output (finite, activation-row and
+    weight-row permutation equivariance, exact doubling with the weight scales)."""
     torch = torch_gpu
     m, n, k = 2048, 11008, 4096
     say("c4 mfma 2048x11008x4096")
@@ -219,6 +250,8 @@ def test_config4_prefill_full_size_sampled(hip, torch_gpu, oracle):
     got_p = hip.mul_mat(0, wt, aq_t[perm].contiguous(), m, n, k)
     torch.cuda.synchronize()
     assert torch.equal(got_p, got[perm])
+    del got_p
+    check_full_size_properties(hip, torch, 0, w, wt, aq_t, got, m, n, k)
 
 
 # ------------------------------------------------- q4_K / iq2_xxs MFMA ----
@@ -287,20 +320,29 @@ def test_mfma_kquant(hip, torch_gpu, oracle, qtype, m, n, k):
 
 
 def test_config2_q4_K_full_size(hip, torch_gpu, oracle):
-    """c2: q4_K x q8_K M=480 N=1536 K=1536 through pfng_hip_compute, whole output checked."""
+    """c2: q4_K x q8_K M=480 N=1536 K=1536 through pfng_hip_compute, whole output
+    checked; then weight-row permutation equivariance and exact doubling with
+    the weight scales on the product."""
     torch = torch_gpu
     m, n, k = 480, 1536, 1536
     say("c2 q4_K 480x1536x1536")
     act, w = oracle.create_input(1, m, n, k, seed=1)
-    got = hip.compute(1, dev(torch, act), dev(torch, w), n)
+    wt, at = dev(torch, w), dev(torch, act)
+    got = hip.compute(1, at, wt, n)
     torch.cuda.synchronize()
     aq = oracle.quantize_q8_K(act)
     check_close(oracle, 1, got.cpu().numpy(), w, aq, m, n, k, label="c2")
+    aq_t = hip.quantize_q8_K(at)
+    prod = hip.mul_mat(1, wt, aq_t, m, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(prod, got)
+    check_full_size_properties(hip, torch, 1, w, wt, aq_t, prod, m, n, k)
 
 
 def test_config3_iq2_xxs_full_size_sampled(hip, torch_gpu, oracle):
     """c3: iq2_xxs x q8_K M=512 N=4096 K=4096 with the baseline weight generator;
-    oracle on 48 seeded rows, exact block sums on a corner, row-permutation equivariance."""
+    oracle on 48 seeded rows, activation-row and weight-row permutation
+    equivariance, exact doubling with the weight scales."""
     torch = torch_gpu
     m, n, k = 512, 4096, 4096
     say("c3 iq2_xxs 512x4096x4096")
@@ -319,6 +361,7 @@ def test_config3_iq2_xxs_full_size_sampled(hip, torch_gpu, oracle):
     got_p = hip.mul_mat(2, wt, aq_t[perm].contiguous(), m, n, k)
     torch.cuda.synchronize()
     assert torch.equal(got_p, got[perm])
+    check_full_size_properties(hip, torch, 2, w, wt, aq_t, got, m, n, k)
 
 
 # ------------------------------------------------- small-shape configs ----
