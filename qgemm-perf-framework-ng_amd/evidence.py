@@ -235,17 +235,33 @@ def bench_stats(args):
         name = name[5:] if name.startswith("void ") else name
         return name.split("(int")[0].split("(unsigned")[0].split("(float")[0].split("(__")[0][:110]
 
+    # per-dispatch durations, for medians: under --kernel-trace a dispatch of a
+    # few microseconds carries the tracer's own overhead (an empty kernel
+    # records about 4.3 us), so the median is the steadier figure for them
+    durations = {}
+    for r in read_csvs(args.trace, "kernel_trace.csv"):
+        durations.setdefault(r["Kernel_Name"], []).append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+
+    def median_us(name):
+        d = sorted(durations.get(name, []))
+        return f"{d[len(d) // 2]:.3f}" if d else "-"
+
     rows = sorted(stats, key=lambda r: -float(r["TotalDurationNs"]))
     out = ["# bench.py kernel statistics (rocprofv3 --kernel-trace --stats)", "",
            "Command (repository root on the GPU box), then the summary:", "```"]
     out += list(args.command or [])
-    out += ["```", "", "| kernel | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
+    out += ["```", "", "| kernel | calls | avg us | median us | min us | max us |", "|---|---|---|---|---|---|"]
     for r in rows:
         out.append(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.3f} | "
-                   f"{float(r['MinNs']) / 1e3:.3f} | {float(r['MaxNs']) / 1e3:.3f} |")
-    out += ["", "Bench items (HIP events over graph replays, same run) against the profiler's average",
-            "for the kernel family each item names:", "",
-            "| item | kernel | bench kernel_us | profiler avg us (matching dispatches) |", "|---|---|---|---|"]
+                   f"{median_us(r['Name'])} | {float(r['MinNs']) / 1e3:.3f} | {float(r['MaxNs']) / 1e3:.3f} |")
+    out += ["", "Bench items (HIP events over back-to-back graph replays, unprofiled run) against the",
+            "profiler's average and median for the kernel family each item names. Traced dispatches",
+            "are spaced apart and carry the tracer's overhead (an empty kernel records about 4.3 us,",
+            "profiles/launch_and_read_floor.md), so for kernels of a few microseconds the traced",
+            "figures sit above the back-to-back ones:", "",
+            "| item | kernel | bench kernel_us | profiler avg / median us (matching dispatches) |",
+            "|---|---|---|---|"]
     for label, roof in items:
         if not roof:
             continue
@@ -257,8 +273,8 @@ def bench_stats(args):
         match = [r for r in stats if base in r["Name"] and tag in short(r["Name"])]
         # one line per instantiation: the plan picks the tile configuration by shape
         for r in match or [None]:
-            prof = (f"{float(r['AverageNs']) / 1e3:.3f} (`{short(r['Name'])}`, {r['Calls']} dispatches)"
-                    if r else "not profiled")
+            prof = (f"{float(r['AverageNs']) / 1e3:.3f} / {median_us(r['Name'])} "
+                    f"(`{short(r['Name'])}`, {r['Calls']} dispatches)" if r else "not profiled")
             out.append(f"| {label} | `{kname}` | {roof['kernel_us']} | {prof} |")
     out.append("")
     with open(args.md, "w") as f:
