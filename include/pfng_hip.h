@@ -51,7 +51,7 @@ typedef enum {
                             m * (k / 64) * 76 + 16 <= 163840, and for m = 2..8
                             also every k % 256 == 0; q4_K and iq2_xxs with
                             k % 256 == 0 for m <= 8, and for m = 9..16 while
-                            m * (k / 256) * 320 + 2048 <= 163840 */
+                            m * (k / 256) * 320 + 3072 <= 163840 */
     PFNG_PATH_MFMA = 2,  /* int8-MFMA GEMM, LDS-staged tiles: q4_0 with k % 128 == 0,
                             q4_K and iq2_xxs for every k % 256 == 0 */
     PFNG_PATH_NAIVE = 3  /* one thread per output, the reference's exact fp32 order */

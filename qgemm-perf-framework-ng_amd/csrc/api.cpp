@@ -156,7 +156,7 @@ int pfng_hip_mul_mat(int type, const void *weight, const void *act_q, float *out
         if (mfma_ok) return launch_mfma(type, weight, act_q, out, m, n, k, s);
         return hip_status(pfng::launch_naive_mul_mat(type, weight, act_q, out, m, n, k, s), "naive launch");
     case PFNG_PATH_GEMV:
-        if (!gemv_ok) return fail(PFNG_ERR_UNSUPPORTED, "%s GEMV path needs m<=16 (q4_0: k%%64==0 for m==1, else k%%64==0 with m*(k/64)*76+16<=163840, or k%%256==0 for m<=8; q4_K/iq2_xxs: k%%256==0, for m>8 also m*(k/256)*320+2048<=163840) and 16-byte aligned operands (m=%lld k=%lld)", type_name(type), (long long)m, (long long)k);
+        if (!gemv_ok) return fail(PFNG_ERR_UNSUPPORTED, "%s GEMV path needs m<=16 (q4_0: k%%64==0 for m==1, else k%%64==0 with m*(k/64)*76+16<=163840, or k%%256==0 for m<=8; q4_K/iq2_xxs: k%%256==0, for m>8 also m*(k/256)*320+3072<=163840) and 16-byte aligned operands (m=%lld k=%lld)", type_name(type), (long long)m, (long long)k);
         return hip_status(pfng::launch_gemv(type, weight, act_q, out, m, n, k, s), "gemv launch");
     case PFNG_PATH_MFMA:
         if (!mfma_ok) return fail(PFNG_ERR_UNSUPPORTED, "%s MFMA path not available for m=%lld k=%lld", type_name(type), (long long)m, (long long)k);

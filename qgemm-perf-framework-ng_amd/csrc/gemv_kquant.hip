@@ -28,7 +28,82 @@ namespace {
 constexpr int kThreads = 256;  // four rows per workgroup, one per wave
 constexpr int kQ8KBytes = 292, kQ4KBytes = 144, kIq2Bytes = 66;
 
-__constant__ uint16_t kIq2GridCodes[256] = PFNG_IQ2XXS_GRID_CODES_INIT;
+// The 256 grid entries expanded at compile time to their eight magnitude
+// bytes (kernels/iq2_xxs-q8_K-RVV-common/ggml_min.h:69-134: two bits per byte
+// select 8, 25 or 43), so a workgroup fills its LDS copy with one 8-byte load
+// and store per thread.
+struct Iq2Grid {
+    uint32_t v[256][2];
+};
+constexpr Iq2Grid expand_iq2_grid() {
+    constexpr uint16_t codes[256] = PFNG_IQ2XXS_GRID_CODES_INIT;
+    Iq2Grid t{};
+    for (int e = 0; e < 256; ++e)
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t c2 = (codes[e] >> (2 * j)) & 3u;
+            t.v[e][j / 4] |= (c2 == 0 ? 8u : (c2 == 1 ? 25u : 43u)) << (8 * (j % 4));
+        }
+    return t;
+}
+__constant__ Iq2Grid kIq2Grid = expand_iq2_grid();
+
+// Sign masks: entry i is 0xff in byte j where bit j of i | parity(i) << 7 is
+// set (the reference's ksigns_iq2xs, ggml_min.h:58-67, which stores exactly
+// that byte, expanded to one mask byte per element).
+struct Iq2Signs {
+    uint32_t v[128][2];
+};
+constexpr Iq2Signs expand_iq2_signs() {
+    Iq2Signs t{};
+    for (int i = 0; i < 128; ++i) {
+        int par = 0;
+        for (int b = 0; b < 7; ++b) par ^= (i >> b) & 1;
+        const int sgn = i | (par << 7);
+        for (int j = 0; j < 8; ++j)
+            if ((sgn >> j) & 1) t.v[i][j / 4] |= 0xffu << (8 * (j % 4));
+    }
+    return t;
+}
+__constant__ Iq2Signs kIq2Signs = expand_iq2_signs();
+
+constexpr int kIq2TableBytes = 256 * 8 + 128 * 8;  // grid, then sign masks
+
+// The LDS copy of both tables (384 entries of 8 bytes), one 8-byte load and
+// store per entry, spread over the workgroup's threads.
+__device__ __forceinline__ void fill_iq2_tables(uint8_t *tab) {
+    for (int e = threadIdx.x; e < 384; e += blockDim.x) {
+        const uint32_t *src = e < 256 ? kIq2Grid.v[e] : kIq2Signs.v[e - 256];
+        *reinterpret_cast<uint2 *>(tab + 8 * e) = make_uint2(src[0], src[1]);
+    }
+}
+
+// The 32 signed weights of one sub-block from its four grid indices (gidx)
+// and its 28 sign-index bits plus scale nibble (ss): magnitudes are >= 8, so
+// (x ^ 0xff) + 1 negates a byte without a carry into the next. kSignTable:
+// the sign masks come from the LDS table (fewer VALU instructions, four more
+// LDS gathers); otherwise sign bit i of group g is computed as bit i of
+// idx | parity(idx) << 7 and spread over the bytes by a multiply. The table
+// measured faster where the decode dominates (few activation rows), the
+// arithmetic form where LDS reads of many activation rows do.
+template <bool kSignTable>
+__device__ __forceinline__ void iq2_decode_subblock(uint32_t gidx, uint32_t ss, const uint8_t *tab, uint32_t (&v)[8]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const uint2 mag = *reinterpret_cast<const uint2 *>(tab + ((gidx >> (8 * g)) & 0xffu) * 8);
+        const uint32_t idx = (ss >> (7 * g)) & 0x7fu;
+        if constexpr (kSignTable) {
+            const uint2 neg = *reinterpret_cast<const uint2 *>(tab + 256 * 8 + idx * 8);
+            v[2 * g] = (mag.x ^ neg.x) + (neg.x & 0x01010101u);
+            v[2 * g + 1] = (mag.y ^ neg.y) + (neg.y & 0x01010101u);
+        } else {
+            const uint32_t sgn = idx | ((__builtin_popcount(idx) & 1u) << 7);
+            const uint32_t s0 = ((sgn & 0xfu) * 0x00204081u) & 0x01010101u;
+            const uint32_t s1 = (((sgn >> 4) & 0xfu) * 0x00204081u) & 0x01010101u;
+            v[2 * g] = (mag.x ^ (s0 * 0xffu)) + s0;
+            v[2 * g + 1] = (mag.y ^ (s1 * 0xffu)) + s1;
+        }
+    }
+}
 
 __device__ __forceinline__ int dot8(const uint32_t *w, const uint32_t *x) {
     int s = 0;
@@ -119,24 +194,16 @@ template <int M>
 __global__ __launch_bounds__(kThreads) void gemv_iq2_xxs_kernel(const uint8_t *__restrict__ w,
                                                                const uint8_t *__restrict__ a, float *__restrict__ c,
                                                                int n, int nb) {
-    __shared__ __align__(16) uint8_t grid[256 * 8];
-    // grid magnitudes (kernels/iq2_xxs-q8_K-RVV-common/ggml_min.h:69-134): two
-    // bits per byte select 8, 25 or 43
-    {
-        const uint32_t code = kIq2GridCodes[threadIdx.x];
-        uint32_t v[2] = {0, 0};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t c2 = (code >> (2 * j)) & 3u;
-            v[j / 4] |= (c2 == 0 ? 8u : (c2 == 1 ? 25u : 43u)) << (8 * (j % 4));
-        }
-        *reinterpret_cast<uint2 *>(grid + 8 * threadIdx.x) = make_uint2(v[0], v[1]);
-    }
+    __shared__ __align__(16) uint8_t grid[kIq2TableBytes];
+    fill_iq2_tables(grid);
     __syncthreads();
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
     const int lrow = row < n ? row : n - 1;
     const int slot = lane >> 3, j = lane & 7;
+    // the row's base once; per step only the block offset
+    const size_t wbase = (size_t)lrow * nb * kIq2Bytes;
+    const uint8_t *wrow = w + wbase;
     float acc[M];
 #pragma unroll
     for (int mi = 0; mi < M; ++mi) acc[mi] = 0.0f;
@@ -146,40 +213,28 @@ __global__ __launch_bounds__(kThreads) void gemv_iq2_xxs_kernel(const uint8_t *_
         const int lb = valid ? b : nb - 1;
         // 66-byte blocks are 2-byte aligned: the covering dwords plus a
         // trailing half-word, never past the sub-block's last byte
-        const size_t base = ((size_t)lrow * nb + lb) * kIq2Bytes;
-        const size_t o = base + 2 + 8 * j;
-        const uint32_t *p4 = reinterpret_cast<const uint32_t *>(w + (o & ~(size_t)3));
+        const size_t boff = (size_t)lb * kIq2Bytes;
+        const size_t o = boff + 2 + 8 * j;
+        const bool sh = ((wbase + o) & 3) != 0;
+        const uint32_t *p4 = reinterpret_cast<const uint32_t *>(wrow + o - (sh ? 2 : 0));
         const uint32_t d0 = p4[0], d1 = p4[1];
-        const uint32_t tail = *reinterpret_cast<const uint16_t *>(w + o + 6);
-        const uint32_t dh = *reinterpret_cast<const uint16_t *>(w + base);
+        const uint32_t tail = *reinterpret_cast<const uint16_t *>(wrow + o + 6);
+        const uint32_t dh = *reinterpret_cast<const uint16_t *>(wrow + boff);
         uint32_t x[M][8];
         float ad[M];
 #pragma unroll
         for (int mi = 0; mi < M; ++mi) {
-            const uint8_t *ab = a + ((size_t)mi * nb + lb) * kQ8KBytes;
+            const uint8_t *ab = a + (size_t)(mi * nb + lb) * kQ8KBytes;
             const uint32_t *xs = reinterpret_cast<const uint32_t *>(ab + 4 + 32 * j);
 #pragma unroll
             for (int i = 0; i < 8; ++i) x[mi][i] = xs[i];
             ad[mi] = *reinterpret_cast<const float *>(ab);
         }
         __builtin_amdgcn_sched_barrier(0);
-        const bool sh = (o & 3) != 0;
         const uint32_t gidx = sh ? __builtin_amdgcn_alignbyte(d1, d0, 2) : d0;
         const uint32_t ss = sh ? ((d1 >> 16) | (tail << 16)) : d1;
-        // decode: magnitudes from the grid, sign bit i of group g is bit i of
-        // (idx | parity(idx) << 7), idx the 7-bit field g of ss; magnitudes are
-        // >= 8, so (x ^ 0xff) + 1 negates a byte without a carry
         uint32_t v[8];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const uint2 mag = *reinterpret_cast<const uint2 *>(grid + ((gidx >> (8 * g)) & 0xffu) * 8);
-            const uint32_t idx = (ss >> (7 * g)) & 0x7fu;
-            const uint32_t sgn = idx | ((__builtin_popcount(idx) & 1u) << 7);
-            const uint32_t s0 = ((sgn & 0xfu) * 0x00204081u) & 0x01010101u;
-            const uint32_t s1 = (((sgn >> 4) & 0xfu) * 0x00204081u) & 0x01010101u;
-            v[2 * g] = (mag.x ^ (s0 * 0xffu)) + s0;
-            v[2 * g + 1] = (mag.y ^ (s1 * 0xffu)) + s1;
-        }
+        iq2_decode_subblock<true>(gidx, ss, grid, v);
         const int scale = 2 * (int)(ss >> 28) + 1;
         const float t0 = 0.125f * fp16_to_f32(dh);
 #pragma unroll
@@ -216,7 +271,7 @@ constexpr int kStagedThreads = 1024;
 constexpr int kQsStride = 272, kSideStride = 48;
 
 __host__ __device__ constexpr int64_t kq_staged_lds_bytes(int64_t m, int64_t nsb) {
-    return m * nsb * (kQsStride + kSideStride) + 256 * 8;  // + the iq2_xxs grid table
+    return m * nsb * (kQsStride + kSideStride) + kIq2TableBytes;  // + the iq2_xxs tables
 }
 
 // four threads per block: quarter t copies qs[64t, 64t + 64), forms the bsum
@@ -349,18 +404,7 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(con
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t *qs = lds, *side = lds + (size_t)M * nb * kQsStride;
     uint8_t *grid = side + (size_t)M * nb * kSideStride;
-    if (threadIdx.x < 256) {
-        // grid magnitudes (kernels/iq2_xxs-q8_K-RVV-common/ggml_min.h:69-134): two
-        // bits per byte select 8, 25 or 43
-        const uint32_t code = kIq2GridCodes[threadIdx.x];
-        uint32_t v[2] = {0, 0};
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-            const uint32_t c2 = (code >> (2 * jj)) & 3u;
-            v[jj / 4] |= (c2 == 0 ? 8u : (c2 == 1 ? 25u : 43u)) << (8 * (jj % 4));
-        }
-        *reinterpret_cast<uint2 *>(grid + 8 * threadIdx.x) = make_uint2(v[0], v[1]);
-    }
+    fill_iq2_tables(grid);
     stage_q8_K<M>(a, qs, side, nb);
     __syncthreads();
     const int lane = threadIdx.x & 63;
@@ -391,16 +435,7 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(con
         const uint32_t gidx = sh ? __builtin_amdgcn_alignbyte(d1, d0, 2) : d0;
         const uint32_t ss = sh ? ((d1 >> 16) | (tail << 16)) : d1;
         uint32_t v[8];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const uint2 mag = *reinterpret_cast<const uint2 *>(grid + ((gidx >> (8 * g)) & 0xffu) * 8);
-            const uint32_t idx = (ss >> (7 * g)) & 0x7fu;
-            const uint32_t sgn = idx | ((__builtin_popcount(idx) & 1u) << 7);
-            const uint32_t s0 = ((sgn & 0xfu) * 0x00204081u) & 0x01010101u;
-            const uint32_t s1 = (((sgn >> 4) & 0xfu) * 0x00204081u) & 0x01010101u;
-            v[2 * g] = (mag.x ^ (s0 * 0xffu)) + s0;
-            v[2 * g + 1] = (mag.y ^ (s1 * 0xffu)) + s1;
-        }
+        iq2_decode_subblock<(M <= 4)>(gidx, ss, grid, v);
         const int scale = 2 * (int)(ss >> 28) + 1;
         const float t0 = valid ? 0.125f * fp16_to_f32(dh) : 0.0f;
         int is[NA];

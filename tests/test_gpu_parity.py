@@ -425,9 +425,9 @@ def test_mfma_in_graph_replays(hip, torch_gpu, oracle):
 @pytest.mark.parametrize("n,k", [(4096, 4096), (257, 1536), (64, 256), (33, 8192), (20, 20480)])
 def test_gemv_kquant(hip, torch_gpu, oracle, qtype, m, n, k):
     """m = 1 reads the activations from global memory; m = 2..16 stage them in
-    LDS while m * (k / 256) * 320 + 2048 bytes fit 160 KB (at k = 20480 only
+    LDS while m * (k / 256) * 320 + 3072 bytes fit 160 KB (at k = 20480 only
     m <= 6 do; m = 7, 8 take the global-read kernel, m > 8 has no GEMV there)."""
-    if m > 8 and m * (k // 256) * 320 + 2048 > 160 * 1024:
+    if m > 8 and m * (k // 256) * 320 + 3072 > 160 * 1024:
         pytest.skip("m > 8 takes the GEMV only while the staged activations fit in LDS")
     torch = torch_gpu
     say(f"gemv type={qtype} m={m} n={n} k={k}")
