@@ -75,31 +75,95 @@ __device__ __forceinline__ uint32_t q8_quantize4(float4 v, float id) {
 }
 
 // Butterfly reductions inside groups of W lanes (W a power of two <= 64).
-template <int W>
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
-}
 
 // largest power of two <= v for v in 1..16, and the log2 of a power of two
 constexpr int pow2_floor16(int v) { return v >= 16 ? 16 : (v >= 8 ? 8 : (v >= 4 ? 4 : (v >= 2 ? 2 : 1))); }
 constexpr int log2_pow2(int v) { return v == 16 ? 4 : (v == 8 ? 3 : (v == 4 ? 2 : (v == 2 ? 1 : 0))); }
 constexpr int pow2_ceil16(int v) { return v <= 1 ? 1 : (v <= 2 ? 2 : (v <= 4 ? 4 : (v <= 8 ? 8 : 16))); }
 
-template <int W>
-__device__ __forceinline__ int group_sum(int v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+
+// Sums over aligned groups of G lanes with DPP adds: two quad permutes, the
+// half-row and row mirrors, then the gfx9 family's row_bcast:15 and
+// row_bcast:31. One VALU add per step, no LDS permute. For G <= 16 every lane
+// of a group ends with the group's sum; for G = 32 and 64 the group's last
+// lane does (the others hold partial sums). Every lane must be active.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_src(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, false);
+}
+template <int G>
+__device__ __forceinline__ float group_sum_dpp(float v) {
+    static_assert(G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "group of 4..64 lanes");
+    auto add = [](float x, int t) { return x + __builtin_bit_cast(float, t); };
+    v = add(v, dpp_src<0xB1, 0xf>(__builtin_bit_cast(int, v)));       // quad_perm [1,0,3,2]
+    v = add(v, dpp_src<0x4E, 0xf>(__builtin_bit_cast(int, v)));       // quad_perm [2,3,0,1]
+    if constexpr (G >= 8) v = add(v, dpp_src<0x141, 0xf>(__builtin_bit_cast(int, v)));  // row_half_mirror
+    if constexpr (G >= 16) v = add(v, dpp_src<0x140, 0xf>(__builtin_bit_cast(int, v))); // row_mirror
+    if constexpr (G >= 32) v = add(v, dpp_src<0x142, 0xa>(__builtin_bit_cast(int, v))); // row_bcast:15
+    if constexpr (G >= 64) v = add(v, dpp_src<0x143, 0xc>(__builtin_bit_cast(int, v))); // row_bcast:31
     return v;
+}
+template <int G>
+__device__ __forceinline__ int group_sum_dpp(int v) {
+    static_assert(G == 4 || G == 8 || G == 16, "integer groups of 4..16 lanes");
+    v += dpp_src<0xB1, 0xf>(v);
+    v += dpp_src<0x4E, 0xf>(v);
+    if constexpr (G >= 8) v += dpp_src<0x141, 0xf>(v);
+    if constexpr (G >= 16) v += dpp_src<0x140, 0xf>(v);
+    return v;
+}
+__device__ __forceinline__ float wave_sum_lane63(float v) { return group_sum_dpp<64>(v); }
+
+// v of lane (lane ^ O), O a power of two below 64, with the cheapest exact
+// exchange: DPP quad permutes for 1 and 2, ds_swizzle's bit-mask mode for 4,
+// 8 and 16 (within 32 lanes), ds_bpermute for 32.
+template <int O>
+__device__ __forceinline__ int xor_shfl(int v) {
+    static_assert(O == 1 || O == 2 || O == 4 || O == 8 || O == 16 || O == 32, "xor offset");
+    if constexpr (O == 1) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);
+    else if constexpr (O == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);
+    else if constexpr (O <= 16) return __builtin_amdgcn_ds_swizzle(v, (O << 10) | 0x1f);
+    else return __shfl_xor(v, O, 64);
+}
+template <int O>
+__device__ __forceinline__ float xor_shfl(float v) {
+    return __builtin_bit_cast(float, xor_shfl<O>(__builtin_bit_cast(int, v)));
 }
 
+// Butterfly over aligned groups of W lanes (exchange offsets W/2, ..., 1):
+// every lane ends with op over its group, combined in the same pairs and
+// order as a __shfl_xor loop, through xor_shfl's cheaper exchanges.
+template <int O, class T, class Op>
+__device__ __forceinline__ T butterfly(T v, Op op) {
+    v = op(v, xor_shfl<O>(v));
+    if constexpr (O > 1) return butterfly<O / 2>(v, op);
+    else return v;
+}
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+    return butterfly<W / 2>(v, [](float a, float b) { return fmaxf(a, b); });
+}
+template <int W>
+__device__ __forceinline__ int group_sum(int v) {
+    return butterfly<W / 2>(v, [](int a, int b) { return a + b; });
+}
 template <int W>
 __device__ __forceinline__ float group_sumf(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
+    return butterfly<W / 2>(v, [](float a, float b) { return a + b; });
 }
+
+// Reduce-scatter exchanges: x[i] += x[i + H] of lane (lane ^ O) for i < H,
+// then H/2 with O/2, down to H = 1. A lane whose O bit is clear keeps the
+// lower half; callers lay out their values so that every lane keeps the lower
+// half and sends the upper (lane-dependent rows, constant indices).
+template <int H, int O, int BASE = 0, class T, int N>
+__device__ __forceinline__ void reduce_scatter_steps(T (&x)[N]) {
+    static_assert(H >= 1 && BASE + 2 * H <= N, "halves within the array");
+#pragma unroll
+    for (int i = 0; i < H; ++i) x[BASE + i] += xor_shfl<O>(x[BASE + i + H]);
+    if constexpr (H > 1) reduce_scatter_steps<H / 2, O / 2, BASE>(x);
+}
+
 
 // D(32x32, int32) = A(32x32 int8) . B(32x32 int8)^T + C.
 // Operand lane l supplies row (l % 32) with the 16 bytes of K-half (l / 32);

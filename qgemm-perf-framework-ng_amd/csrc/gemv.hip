@@ -246,9 +246,8 @@ __global__ __launch_bounds__(kLdsAct ? 1024 : kThreads) void gemv_q4_0_m1_kernel
         acc += q4_0_block_dot16(q0, u[0] & 0xffffu, x0, v[0] & 0xffffu);
         acc += q4_0_block_dot16(q1, u[4] >> 16, x1, v[8] >> 16);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    if (row < n && lane == 0) c[row] = acc * 0.0625f;
+    acc = wave_sum_lane63(acc);
+    if (row < n && lane == 63) c[row] = acc * 0.0625f;
 }
 
 // m = 2..16 when the m activation rows fit the 160 KB of LDS in the layout below.
@@ -363,21 +362,19 @@ __global__ __launch_bounds__(kPairsThreads) void gemv_q4_0_pairs_kernel(const ui
             acc[j] += (float)s1 * (dw1 * da.y);
         }
     }
-    // reduce-scatter over accumulators 0..P-1: exchange offsets 32, 16, ...
+    // reduce-scatter over accumulators 0..P-1 (exchange offsets 32, 16, ...),
+    // then a DPP sum over the 64 / P lanes left: the group's last lane holds it
+    constexpr int G = 1 << kLaneShift;
+    reduce_scatter_steps<P / 2, 32>(acc);
+    acc[0] = group_sum_dpp<G>(acc[0]);
 #pragma unroll
-    for (int h = P / 2, o = 32; h >= 1; h >>= 1, o >>= 1) {
-#pragma unroll
-        for (int i = 0; i < h; ++i) acc[i] += __shfl_xor(acc[i + h], o, 64);
-    }
-#pragma unroll
-    for (int o = (1 << kLaneShift) / 2; o > 0; o >>= 1) acc[0] += __shfl_xor(acc[0], o, 64);
-#pragma unroll
-    for (int j = P; j < M; ++j) acc[j] = group_sumf<64>(acc[j]);
+    for (int j = P; j < M; ++j) acc[j] = wave_sum_lane63(acc[j]);
     if (row < n) {
-        if ((lane & ((1 << kLaneShift) - 1)) == 0 && f < M) c[(size_t)f * n + row] = acc[0] * 0.0625f;
+        if ((lane & (G - 1)) == G - 1 && f < M) c[(size_t)f * n + row] = acc[0] * 0.0625f;
+        if (lane == 63) {
 #pragma unroll
-        for (int j = P; j < M; ++j)
-            if (lane == 63 - (j - P)) c[(size_t)j * n + row] = acc[j] * 0.0625f;
+            for (int j = P; j < M; ++j) c[(size_t)j * n + row] = acc[j] * 0.0625f;
+        }
     }
 }
 
@@ -438,13 +435,20 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_q4_0_fused_kernel(const ui
             acc[mi] += q4_0_block_dot16(q1, u[4] >> 16, x1, v[8] >> 16);
         }
     }
-#pragma unroll
-    for (int mi = 0; mi < M; ++mi) acc[mi] = group_sumf<64>(acc[mi]);
-    if (row < n && lane < M) {
-        float v = acc[0];
-#pragma unroll
-        for (int mi = 1; mi < M; ++mi) v = lane == mi ? acc[mi] : v;
-        c[(size_t)lane * n + row] = v * 0.0625f;
+    // the same sums as the unfused kernels, so the outputs are equal bit for
+    // bit: m == 1 as gemv_q4_0_m1_kernel, m == 2 as gemv_q4_0_pairs_kernel<2>
+    // (one exchange between the wave halves, then a 32-lane DPP sum)
+    static_assert(M == 1 || M == 2, "fused for m <= 2");
+    if constexpr (M == 1) {
+        const float v = wave_sum_lane63(acc[0]);
+        if (row < n && lane == 63) c[row] = v * 0.0625f;
+    } else {
+        const bool up = lane >= 32;
+        float x = up ? acc[1] : acc[0];
+        const float y = up ? acc[0] : acc[1];
+        x += xor_shfl<32>(y);
+        x = group_sum_dpp<32>(x);
+        if (row < n && (lane & 31) == 31) c[(size_t)(up ? 1 : 0) * n + row] = x * 0.0625f;
     }
 }
 

@@ -181,12 +181,10 @@ __global__ __launch_bounds__(kThreads) void gemv_q4_K_kernel(const uint8_t *__re
         }
     }
 #pragma unroll
-    for (int mi = 0; mi < M; ++mi) acc[mi] = group_sumf<64>(acc[mi]);
-    if (row < n && lane < M) {
-        float v = acc[0];
+    for (int mi = 0; mi < M; ++mi) acc[mi] = wave_sum_lane63(acc[mi]);
+    if (row < n && lane == 63) {
 #pragma unroll
-        for (int mi = 1; mi < M; ++mi) v = lane == mi ? acc[mi] : v;
-        c[(size_t)lane * n + row] = v;
+        for (int mi = 0; mi < M; ++mi) c[(size_t)mi * n + row] = acc[mi];
     }
 }
 
@@ -240,17 +238,15 @@ __global__ __launch_bounds__(kThreads) void gemv_iq2_xxs_kernel(const uint8_t *_
 #pragma unroll
         for (int mi = 0; mi < M; ++mi) {
             // exact integer sum of the super-block over its eight lanes
-            const int is = group_sum<8>(scale * dot8(v, x[mi]));
+            const int is = group_sum_dpp<8>(scale * dot8(v, x[mi]));
             if (j == 0 && valid) acc[mi] += (t0 * ad[mi]) * (float)is;
         }
     }
 #pragma unroll
-    for (int mi = 0; mi < M; ++mi) acc[mi] = group_sumf<64>(acc[mi]);
-    if (row < n && lane < M) {
-        float v = acc[0];
+    for (int mi = 0; mi < M; ++mi) acc[mi] = wave_sum_lane63(acc[mi]);
+    if (row < n && lane == 63) {
 #pragma unroll
-        for (int mi = 1; mi < M; ++mi) v = lane == mi ? acc[mi] : v;
-        c[(size_t)lane * n + row] = v;
+        for (int mi = 0; mi < M; ++mi) c[(size_t)mi * n + row] = acc[mi];
     }
 }
 
@@ -365,20 +361,19 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_q4_K_staged_kernel(const 
             acc[q] += valid ? part : 0.0f;
         }
     }
+    // reduce-scatter (exchange offsets 32, 16, ...), then a DPP sum over the
+    // 64 / P lanes left: the group's last lane holds it
+    constexpr int G = 1 << kLaneShift;
+    reduce_scatter_steps<P / 2, 32>(acc);
+    acc[0] = group_sum_dpp<G>(acc[0]);
 #pragma unroll
-    for (int h = P / 2, o = 32; h >= 1; h >>= 1, o >>= 1) {
-#pragma unroll
-        for (int i = 0; i < h; ++i) acc[i] += __shfl_xor(acc[i + h], o, 64);
-    }
-#pragma unroll
-    for (int o = (1 << kLaneShift) / 2; o > 0; o >>= 1) acc[0] += __shfl_xor(acc[0], o, 64);
-#pragma unroll
-    for (int q = P; q < M; ++q) acc[q] = group_sumf<64>(acc[q]);
+    for (int q = P; q < M; ++q) acc[q] = wave_sum_lane63(acc[q]);
     if (row < n) {
-        if ((lane & ((1 << kLaneShift) - 1)) == 0 && f < M) c[(size_t)f * n + row] = acc[0];
+        if ((lane & (G - 1)) == G - 1 && f < M) c[(size_t)f * n + row] = acc[0];
+        if (lane == 63) {
 #pragma unroll
-        for (int q = P; q < M; ++q)
-            if (lane == 63 - (q - P)) c[(size_t)q * n + row] = acc[q];
+            for (int q = P; q < M; ++q) c[(size_t)q * n + row] = acc[q];
+        }
     }
 }
 
@@ -451,13 +446,11 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(con
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
             // exact integer sums over the eight lanes of the super-block
-#pragma unroll
-            for (int h = P / 2; h >= 1; h >>= 1) {
-#pragma unroll
-                for (int i = 0; i < h; ++i) is[P * g + i] += __shfl_xor(is[P * g + i + h], h, 64);
-            }
-#pragma unroll
-            for (int off = P; off < 8; off <<= 1) is[P * g] += __shfl_xor(is[P * g], off, 64);
+            if (g == 0) reduce_scatter_steps<P / 2, P / 2, 0>(is);
+            if constexpr (NG > 1)
+                if (g == 1) reduce_scatter_steps<P / 2, P / 2, P>(is);
+            if constexpr (P <= 2) is[P * g] += xor_shfl<2>(is[P * g]);
+            if constexpr (P <= 4) is[P * g] += xor_shfl<4>(is[P * g]);
             const int rp = P * g + f;
             const float adp = *reinterpret_cast<const float *>(
                 side + (size_t)((rp < M ? rp : M - 1) * nb + lb) * kSideStride + 32);
@@ -465,7 +458,7 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(con
         }
 #pragma unroll
         for (int q = NG * P; q < NA; ++q) {
-            const int tot = group_sum<8>(is[q]);
+            const int tot = group_sum_dpp<8>(is[q]);
             const float adq = *reinterpret_cast<const float *>(side + (size_t)(q * nb + lb) * kSideStride + 32);
             if (j == 0) accx[q - NG * P] += (t0 * adq) * (float)tot;
         }
@@ -473,18 +466,20 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(con
     // across the eight super-block slots
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-#pragma unroll
-        for (int off = 8; off < 64; off <<= 1) accp[g] += __shfl_xor(accp[g], off, 64);
+        accp[g] += xor_shfl<8>(accp[g]);
+        accp[g] += xor_shfl<16>(accp[g]);
+        accp[g] += xor_shfl<32>(accp[g]);
     }
 #pragma unroll
-    for (int q = 0; q < NX; ++q) accx[q] = group_sumf<64>(accx[q]);
+    for (int q = 0; q < NX; ++q) accx[q] = wave_sum_lane63(accx[q]);
     if (row < n) {
 #pragma unroll
         for (int g = 0; g < NG; ++g)
             if (lane < P && P * g + lane < M) c[(size_t)(P * g + lane) * n + row] = accp[g];
+        if (lane == 63) {
 #pragma unroll
-        for (int q = 0; q < NX; ++q)
-            if (lane == 63 - q) c[(size_t)(NG * P + q) * n + row] = accx[q];
+            for (int q = 0; q < NX; ++q) c[(size_t)(NG * P + q) * n + row] = accx[q];
+        }
     }
 }
 
