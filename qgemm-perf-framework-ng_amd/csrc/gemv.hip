@@ -214,10 +214,16 @@ __global__ __launch_bounds__(kLdsAct ? 1024 : kThreads) void gemv_q4_0_m1_kernel
     extern __shared__ __align__(16) uint8_t sact[];
     const uint8_t *act = a;
     if constexpr (kLdsAct) {
-        // nb is even (k % 64 == 0), so the row is a whole number of dwords
+        // 16-byte copies (the row base is 16-byte aligned), then the dword
+        // tail (nb is even, so the row is a whole number of dwords): one round
+        // trip per thread for rows up to 16 KB
+        const int n16 = nb * 34 / 16, nd = nb * 34 / 4;
+        const uint4 *src4 = reinterpret_cast<const uint4 *>(a);
+        uint4 *dst4 = reinterpret_cast<uint4 *>(sact);
+        for (int i = threadIdx.x; i < n16; i += kBlockThreads) dst4[i] = src4[i];
         const uint32_t *src = reinterpret_cast<const uint32_t *>(a);
         uint32_t *dst = reinterpret_cast<uint32_t *>(sact);
-        for (int i = threadIdx.x; i < nb * 34 / 4; i += kBlockThreads) dst[i] = src[i];
+        for (int i = 4 * n16 + threadIdx.x; i < nd; i += kBlockThreads) dst[i] = src[i];
         __syncthreads();
         act = sact;
     }
