@@ -422,11 +422,13 @@ def test_mfma_in_graph_replays(hip, torch_gpu, oracle):
 
 @pytest.mark.parametrize("qtype", [1, 2])
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 13, 16])
-@pytest.mark.parametrize("n,k", [(4096, 4096), (257, 1536), (64, 256), (33, 8192), (20, 20480)])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (257, 1536), (64, 256), (33, 8192), (20, 20480), (8, 65536)])
 def test_gemv_kquant(hip, torch_gpu, oracle, qtype, m, n, k):
-    """m = 1 reads the activations from global memory; m = 2..16 stage them in
-    LDS while m * (k / 256) * 320 + 3072 bytes fit 160 KB (at k = 20480 only
-    m <= 6 do; m = 7, 8 take the global-read kernel, m > 8 has no GEMV there)."""
+    """m = 1: q4_K copies the activation row into LDS while it fits 64 KB
+    (k <= 57344; k = 65536 takes the global-read kernel), iq2_xxs reads it from
+    global memory; m = 2..16 stage the rows in LDS while m * (k / 256) * 320 +
+    3072 bytes fit 160 KB (at k = 20480 only m <= 6 do, at k = 65536 none; the
+    others up to m = 8 take the global-read kernel, m > 8 has no GEMV there)."""
     if m > 8 and m * (k // 256) * 320 + 3072 > 160 * 1024:
         pytest.skip("m > 8 takes the GEMV only while the staged activations fit in LDS")
     torch = torch_gpu
