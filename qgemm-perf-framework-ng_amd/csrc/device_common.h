@@ -214,14 +214,51 @@ __device__ __forceinline__ uint32_t shift2(uint32_t lo, uint32_t hi) {
     return __builtin_amdgcn_alignbyte(hi, lo, 2);
 }
 
-// Q4_0 nibbles of one qs dword -> 16 * (nibble - 8) as packed int8.
-// x ^ 0x88 flips bit 3 of each nibble, which turns (nibble - 8) into the same
-// nibble read as a signed 4-bit number; placing it in the upper half of the
-// byte yields 16 * (nibble - 8) with no carries between bytes.
+// Q4_0 nibbles of one qs dword -> 16 * (nibble - 8) as packed int8, for the
+// bytes kMask keeps (0xF0 per byte kept, 0x00 per byte zeroed). With the
+// nibble q in the upper half of a byte, the byte is 16 * q; flipping its top
+// bit subtracts 128 modulo 256, which read as int8 is 16 * (q - 8) for every
+// q, with no carries between bytes. Each is a shift (low nibbles only) and
+// one and-xor (v_bitop3).
+template <uint32_t kMask = 0xF0F0F0F0u>
+__device__ __forceinline__ uint32_t q4_0_lo16(uint32_t x) {
+    return ((x << 4) & kMask) ^ (kMask & 0x80808080u);
+}
+template <uint32_t kMask = 0xF0F0F0F0u>
+__device__ __forceinline__ uint32_t q4_0_hi16(uint32_t x) {
+    return (x & kMask) ^ (kMask & 0x80808080u);
+}
 __device__ __forceinline__ void q4_0_unpack16(uint32_t x, uint32_t &lo16, uint32_t &hi16) {
-    const uint32_t y = x ^ 0x88888888u;
-    lo16 = (y << 4) & 0xF0F0F0F0u;
-    hi16 = y & 0xF0F0F0F0u;
+    lo16 = q4_0_lo16(x);
+    hi16 = q4_0_hi16(x);
+}
+
+// Marks the N registers of x as used at this point: the loads that produce
+// them can then not be sunk below it (into a later branch that is the only
+// other user, say), and the compiler waits for exactly those loads here.
+template <int N>
+__device__ __forceinline__ void use_here(const uint32_t (&x)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) asm volatile("" ::"v"(x[i]));
+}
+
+// Marks the N registers of x as redefined at this point: nothing computed
+// from them can be moved above it (arithmetic on loaded values hoisted above
+// a workgroup barrier makes the barrier wait for those loads).
+template <int N>
+__device__ __forceinline__ void redefine_here(uint32_t (&x)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(x[i]));
+}
+
+// dw * da of two fp16 scales (the low or high halves of a and b) in fp32: the
+// product of two fp16 values is exact in fp32, so this equals
+// fp16_to_f32(dw) * fp16_to_f32(da) and compiles to one mixed-precision fma.
+template <bool kAHi, bool kBHi>
+__device__ __forceinline__ float fp16_product(uint32_t a, uint32_t b) {
+    const _Float16 ha = __builtin_bit_cast(_Float16, (uint16_t)(kAHi ? a >> 16 : a));
+    const _Float16 hb = __builtin_bit_cast(_Float16, (uint16_t)(kBHi ? b >> 16 : b));
+    return __builtin_fmaf((float)ha, (float)hb, 0.0f);
 }
 
 }  // namespace pfng

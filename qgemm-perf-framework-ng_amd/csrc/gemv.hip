@@ -84,22 +84,39 @@ __device__ __forceinline__ void load_q4_0_group(const uint8_t *__restrict__ w, b
     }
 }
 
-// 16 * (dot of one q4_0 block with one q8_0 block) * dw * da, from the block's
-// four nibble dwords q and the activation's eight int8 dwords x (element order).
-__device__ __forceinline__ float q4_0_block_dot16(const uint32_t (&q)[4], uint32_t dw16, const uint32_t (&x)[8],
-                                                  uint32_t da16) {
-    uint32_t lo[4], hi[4];
+// isum16 of the first block of a q4_0 pair read at its natural two-byte
+// offset, against the first block of a q8_0 pair likewise: weight dwords
+// u[0..4] = d | qs[0..1], qs[2..5], ..., qs[14..15] | d', activation dwords
+// v[0..8] = d | qs[0..1], qs[2..5], ..., qs[30..31] | d'. Both sit two bytes
+// into their dwords, so byte b of u[k] (weight element 4k-2+b as its low
+// nibble, 4k+14+b as its high nibble) faces activation element 4k-2+b in byte
+// b of v[k] and element 4k+14+b in byte b of v[k+4]: no realignment, two more
+// v_dot4, and the masks of u[0] and u[4] zero the bytes that hold scales.
+__device__ __forceinline__ int q4_0_dot16_at2(const uint32_t *u, const uint32_t *v) {
+    int s = __builtin_amdgcn_sdot4((int)q4_0_lo16<0xF0F00000u>(u[0]), (int)v[0], 0, false);
+    s = __builtin_amdgcn_sdot4((int)q4_0_hi16<0xF0F00000u>(u[0]), (int)v[4], s, false);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) q4_0_unpack16(q[i], lo[i], hi[i]);
-    int s = __builtin_amdgcn_sdot4((int)lo[0], (int)x[0], 0, false);
-    s = __builtin_amdgcn_sdot4((int)lo[1], (int)x[1], s, false);
-    s = __builtin_amdgcn_sdot4((int)lo[2], (int)x[2], s, false);
-    s = __builtin_amdgcn_sdot4((int)lo[3], (int)x[3], s, false);
-    s = __builtin_amdgcn_sdot4((int)hi[0], (int)x[4], s, false);
-    s = __builtin_amdgcn_sdot4((int)hi[1], (int)x[5], s, false);
-    s = __builtin_amdgcn_sdot4((int)hi[2], (int)x[6], s, false);
-    s = __builtin_amdgcn_sdot4((int)hi[3], (int)x[7], s, false);
-    return (float)s * (fp16_to_f32(dw16) * fp16_to_f32(da16));
+    for (int k = 1; k < 4; ++k) {
+        s = __builtin_amdgcn_sdot4((int)q4_0_lo16(u[k]), (int)v[k], s, false);
+        s = __builtin_amdgcn_sdot4((int)q4_0_hi16(u[k]), (int)v[k + 4], s, false);
+    }
+    s = __builtin_amdgcn_sdot4((int)q4_0_lo16<0x0000F0F0u>(u[4]), (int)v[4], s, false);
+    return __builtin_amdgcn_sdot4((int)q4_0_hi16<0x0000F0F0u>(u[4]), (int)v[8], s, false);
+}
+
+// acc + 16 * (dot of a q4_0 block pair with a q8_0 block pair): u = the pair's
+// nine weight dwords as loaded, v = the activation pair's seventeen dwords.
+// Per block acc = fma(float(isum16), dw * da, acc), the scale product exact.
+__device__ __forceinline__ float q4_0_pair_dot16(const uint32_t (&u)[9], const uint32_t (&v)[17], float acc) {
+    const int s0 = q4_0_dot16_at2(u, v);
+    int s1 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        s1 = __builtin_amdgcn_sdot4((int)q4_0_lo16(u[5 + i]), (int)v[9 + i], s1, false);
+        s1 = __builtin_amdgcn_sdot4((int)q4_0_hi16(u[5 + i]), (int)v[13 + i], s1, false);
+    }
+    acc = __builtin_fmaf((float)s0, fp16_product<false, false>(u[0], v[0]), acc);
+    return __builtin_fmaf((float)s1, fp16_product<true, true>(u[4], v[8]), acc);
 }
 
 // Block j of a group sits at byte 18*j: fp16 d, then 16 bytes of nibbles.
@@ -199,58 +216,80 @@ __global__ __launch_bounds__(kThreads) void gemv_q4_0_kernel(const uint8_t *__re
 
 // m == 1. Each lane owns one q4_0 block pair of its row (36 bytes, nine dword
 // loads, 4-byte aligned when k % 64 == 0) and reads the matching q8_0 block
-// pair of the activation row (68 bytes, seventeen dwords). All of a lane's
-// loads are issued before any arithmetic, so each lane pays one memory round
-// trip. One wavefront covers 64 block pairs of one row (a whole row at
-// k = 4096). kLdsAct: workgroups of 16 rows copy the activation row into LDS
-// once (the 16 waves then read it from there instead of each fetching it from
-// L2); measured 5 % faster at 4096 x 4096. Without it (activation rows above
-// 64 KB), 4-row workgroups read the activation directly.
+// pair of the activation row (68 bytes, seventeen dwords); both pairs are
+// dotted as loaded (q4_0_pair_dot16: the first blocks at their common
+// two-byte offset, nothing realigned). All of a lane's loads are issued
+// before any arithmetic, so each lane pays one memory round trip. One
+// wavefront covers 64 block pairs of one row (a whole row at k = 4096).
+//
+// kLdsAct (activation rows up to 64 KB): workgroups of 16 rows copy the
+// activation row into LDS once, and the 16 waves read it from there instead
+// of each fetching it from L2. The copy uses direct loads into LDS
+// (global_load_lds_dwordx4: lane i of a wave writes 16 bytes at the wave's
+// LDS base + 16 i, no VGPR round trip), and every lane issues the three load
+// instructions of its first weight pair (clamped into the row, so they are
+// always issued) before any wave waits: each wave then waits for its own
+// copies only (s_waitcnt vmcnt(3): memory loads complete in issue order, so
+// at most the three weight loads are left) and meets the others at the
+// barrier, and the activation's trip from L2 overlaps the weight stream
+// instead of preceding it. Without kLdsAct, 4-row workgroups read the
+// activation directly.
 template <bool kLdsAct>
 __global__ __launch_bounds__(kLdsAct ? 1024 : kThreads) void gemv_q4_0_m1_kernel(const uint8_t *__restrict__ w,
                                                                                const uint8_t *__restrict__ a,
                                                                                float *__restrict__ c, int n, int nb) {
     constexpr int kBlockThreads = kLdsAct ? 1024 : kThreads;
     extern __shared__ __align__(16) uint8_t sact[];
+    const int lane = threadIdx.x & 63;
+    // the row is uniform across the wave: its base address lives in scalar registers
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int row = blockIdx.x * (kBlockThreads / 64) + wave;
+    const int lrow = row < n ? row : n - 1;  // clamped: loads stay unconditional, the store is guarded
+    const uint8_t *wrow = w + (size_t)lrow * nb * 18;
+    const int np = nb / 2;
     const uint8_t *act = a;
+    float acc = 0.0f;
+    int p = lane;
     if constexpr (kLdsAct) {
-        // 16-byte copies (the row base is 16-byte aligned), then the dword
-        // tail (nb is even, so the row is a whole number of dwords): one round
-        // trip per thread for rows up to 16 KB
+        // 16-byte chunks (the row base is 16-byte aligned), wave w taking
+        // chunks 64 w + lane (+ 1024 per round), then the dword tail (nb is
+        // even, so the row is a whole number of dwords) from the last wave
         const int n16 = nb * 34 / 16, nd = nb * 34 / 4;
-        const uint4 *src4 = reinterpret_cast<const uint4 *>(a);
-        uint4 *dst4 = reinterpret_cast<uint4 *>(sact);
-        for (int i = threadIdx.x; i < n16; i += kBlockThreads) dst4[i] = src4[i];
-        const uint32_t *src = reinterpret_cast<const uint32_t *>(a);
-        uint32_t *dst = reinterpret_cast<uint32_t *>(sact);
-        for (int i = 4 * n16 + threadIdx.x; i < nd; i += kBlockThreads) dst[i] = src[i];
-        __syncthreads();
+        for (int c0 = wave * 64; c0 < n16; c0 += kBlockThreads) {
+            if (c0 + lane < n16)
+                __builtin_amdgcn_global_load_lds(a + (size_t)(c0 + lane) * 16, (__attribute__((address_space(3))) void *)(sact + c0 * 16),
+                                                 16, 0, 0);
+        }
+        if (wave == kBlockThreads / 64 - 1 && 4 * n16 + lane < nd)
+            __builtin_amdgcn_global_load_lds(a + (size_t)(4 * n16 + lane) * 4, (__attribute__((address_space(3))) void *)(sact + n16 * 16),
+                                             4, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        const int pc = lane < np ? lane : np - 1;
+        const uint32_t *ws = reinterpret_cast<const uint32_t *>(wrow + (uint32_t)pc * 36u);
+        uint32_t u[9], v[17];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) u[i] = ws[i];
+        asm volatile("s_waitcnt vmcnt(3)\n\ts_barrier" ::: "memory");
+        const uint32_t *as = reinterpret_cast<const uint32_t *>(sact + (size_t)pc * 68);
+#pragma unroll
+        for (int i = 0; i < 17; ++i) v[i] = as[i];
+        // lanes past the row's last pair dot a clamped duplicate and drop it
+        // (a select, not a branch, so the loads stay ahead of the wait)
+        const float first = q4_0_pair_dot16(u, v, 0.0f);
+        acc = lane < np ? first : 0.0f;
+        p += 64;
         act = sact;
     }
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (kBlockThreads / 64) + (threadIdx.x >> 6);
-    const int lrow = row < n ? row : n - 1;  // clamped: loads stay unconditional, the store is guarded
-    float acc = 0.0f;
-    for (int p = lane; p < nb / 2; p += 64) {
-        const uint32_t *ws = reinterpret_cast<const uint32_t *>(w + ((size_t)lrow * nb + 2 * p) * 18);
-        const uint32_t *as = reinterpret_cast<const uint32_t *>(act + (size_t)(2 * p) * 34);
+    for (; p < np; p += 64) {
+        const uint32_t *ws = reinterpret_cast<const uint32_t *>(wrow + (uint32_t)p * 36u);
+        const uint32_t *as = reinterpret_cast<const uint32_t *>(act + (size_t)p * 68);
         uint32_t u[9], v[17];
 #pragma unroll
         for (int i = 0; i < 9; ++i) u[i] = ws[i];
 #pragma unroll
         for (int i = 0; i < 17; ++i) v[i] = as[i];
         __builtin_amdgcn_sched_barrier(0);
-        // block 2p: d at byte 0, qs at 2 (realign by two bytes); block 2p+1: d at 18 / 34, qs at 20 / 36
-        const uint32_t q0[4] = {shift2(u[0], u[1]), shift2(u[1], u[2]), shift2(u[2], u[3]), shift2(u[3], u[4])};
-        const uint32_t q1[4] = {u[5], u[6], u[7], u[8]};
-        uint32_t x0[8], x1[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            x0[i] = shift2(v[i], v[i + 1]);
-            x1[i] = v[9 + i];
-        }
-        acc += q4_0_block_dot16(q0, u[0] & 0xffffu, x0, v[0] & 0xffffu);
-        acc += q4_0_block_dot16(q1, u[4] >> 16, x1, v[8] >> 16);
+        acc = q4_0_pair_dot16(u, v, acc);
     }
     acc = wave_sum_lane63(acc);
     if (row < n && lane == 63) c[row] = acc * 0.0625f;
@@ -306,40 +345,73 @@ __global__ __launch_bounds__(kPairsThreads) void gemv_q4_0_pairs_kernel(const ui
     const int np = nb / 2;
     uint32_t *xq = reinterpret_cast<uint32_t *>(lds);                          // [M][np][17]
     float2 *xd = reinterpret_cast<float2 *>(lds + pairs_scale_offset(M, nb));  // [M][np]
-    for (int task = threadIdx.x; task < M * np; task += kPairsThreads) {
-        // task = row * np + pair: the pair's 68 bytes, 4-byte aligned (nb even)
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (kPairsThreads / 64) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lrow = row < n ? row : n - 1;  // clamped: loads stay unconditional, the store is guarded
+    const uint8_t *wrow = w + (size_t)lrow * nb * 18;
+    const int ntask = M * np;
+    // task = row * np + pair: the pair's 68 bytes (4-byte aligned, nb even)
+    // realigned into xq, its scales widened into xd
+    auto stage = [&](const uint32_t (&v)[17], int task, bool store) {
+        uint32_t q[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = shift2(v[i], v[i + 1]);
+        const float2 d = make_float2(fp16_to_f32(v[0] & 0xffffu), fp16_to_f32(v[8] >> 16));
+        if (store) {
+            uint32_t *dst = xq + (size_t)task * kPairDwords;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                dst[i] = q[i];
+                dst[8 + i] = v[9 + i];
+            }
+            xd[task] = d;
+        }
+    };
+    // each thread's first staging task (the only one while m * k / 64 <=
+    // 1024, so always at k <= 4096), then the lane's first weight pair
+    // (clamped into the row, so always issued): the staging waits for its
+    // own loads only, and the weights' trip from HBM overlaps it and the
+    // barrier. Threads without a task load nothing (clamping them onto the
+    // last task would send every idle wave of the grid to one L2 channel).
+    int task = threadIdx.x;
+    uint32_t v0[17];
+    if (task < ntask) {
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(a + (size_t)task * 68);
+#pragma unroll
+        for (int i = 0; i < 17; ++i) v0[i] = src[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 17; ++i) v0[i] = 0;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int pc = lane < np ? lane : np - 1;
+    uint32_t u0[9];
+    {
+        const uint32_t *ws = reinterpret_cast<const uint32_t *>(wrow + (uint32_t)pc * 36u);
+#pragma unroll
+        for (int i = 0; i < 9; ++i) u0[i] = ws[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    use_here(v0);
+    stage(v0, task, task < ntask);
+    for (task += kPairsThreads; task < ntask; task += kPairsThreads) {
         const uint32_t *src = reinterpret_cast<const uint32_t *>(a + (size_t)task * 68);
         uint32_t v[17];
 #pragma unroll
         for (int i = 0; i < 17; ++i) v[i] = src[i];
-        uint32_t *dst = xq + (size_t)task * kPairDwords;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            dst[i] = shift2(v[i], v[i + 1]);
-            dst[8 + i] = v[9 + i];
-        }
-        xd[task] = make_float2(fp16_to_f32(v[0] & 0xffffu), fp16_to_f32(v[8] >> 16));
+        stage(v, task, true);
     }
     __syncthreads();
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (kPairsThreads / 64) + (threadIdx.x >> 6);
-    const int lrow = row < n ? row : n - 1;  // clamped: loads stay unconditional, the store is guarded
-    const int f = lane >> kLaneShift;        // < P
-    int arow[NA];                            // activation row read for accumulator j (clamped)
+    redefine_here(u0);  // the weights are decoded after the barrier, which then waits for the staging only
+    const int f = lane >> kLaneShift;  // < P
+    int arow[NA];                      // activation row read for accumulator j (clamped)
 #pragma unroll
     for (int j = 0; j < NA; ++j) {
         const int r = j < P ? j ^ f : j;
         arow[j] = r < M ? r : M - 1;
     }
-    float acc[NA];
-#pragma unroll
-    for (int j = 0; j < NA; ++j) acc[j] = 0.0f;
-    for (int p = lane; p < np; p += 64) {
-        const uint32_t *ws = reinterpret_cast<const uint32_t *>(w + ((size_t)lrow * nb + 2 * p) * 18);
-        uint32_t u[9];
-#pragma unroll
-        for (int i = 0; i < 9; ++i) u[i] = ws[i];
-        __builtin_amdgcn_sched_barrier(0);
+    // acc[j] += the pair's two block dots with activation row arow[j]
+    auto pair_step = [&](const uint32_t (&u)[9], int p, float (&acc)[NA]) {
         // block 2p: d at byte 0, qs at 2 (realign by two bytes); block 2p+1: d at 18, qs at 20
         uint32_t lo0[4], hi0[4], lo1[4], hi1[4];
 #pragma unroll
@@ -367,6 +439,20 @@ __global__ __launch_bounds__(kPairsThreads) void gemv_q4_0_pairs_kernel(const ui
             acc[j] += (float)s0 * (dw0 * da.x);
             acc[j] += (float)s1 * (dw1 * da.y);
         }
+    };
+    float acc[NA];
+#pragma unroll
+    for (int j = 0; j < NA; ++j) acc[j] = 0.0f;
+    pair_step(u0, pc, acc);
+#pragma unroll
+    for (int j = 0; j < NA; ++j) acc[j] = lane < np ? acc[j] : 0.0f;  // past the last pair: a clamped duplicate
+    for (int p = lane + 64; p < np; p += 64) {
+        const uint32_t *ws = reinterpret_cast<const uint32_t *>(wrow + (uint32_t)p * 36u);
+        uint32_t u[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) u[i] = ws[i];
+        __builtin_amdgcn_sched_barrier(0);
+        pair_step(u, p, acc);
     }
     // reduce-scatter over accumulators 0..P-1 (exchange offsets 32, 16, ...),
     // then a DPP sum over the 64 / P lanes left: the group's last lane holds it
@@ -398,47 +484,73 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_q4_0_fused_kernel(const ui
                                                                        const float *__restrict__ x,
                                                                        float *__restrict__ c, int n, int nb) {
     extern __shared__ __align__(16) uint8_t aq[];  // M rows of nb q8_0 blocks, HBM layout
-    const int tid = threadIdx.x, sub = tid & 7;
-    for (int blk = tid >> 3; blk < M * nb; blk += kFusedThreads / 8) {
-        const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)blk * 32 + sub * 4);
+    const int tid = threadIdx.x, sub = tid & 7, lane = tid & 63;
+    const int row = blockIdx.x * (kFusedThreads / 64) + __builtin_amdgcn_readfirstlane((int)(tid >> 6));
+    const int lrow = row < n ? row : n - 1;
+    const uint8_t *wrow = w + (size_t)lrow * nb * 18;
+    const int np = nb / 2, nblk = M * nb;
+    // one quantization task = 4 elements of one block (8 lanes per block)
+    auto quantize = [&](const float4 &v, int blk, bool store) {
         float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
         amax = group_max<8>(amax);
         const float d = amax / 127.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         const uint32_t q = q8_quantize4(v, id);
-        uint16_t *ob = reinterpret_cast<uint16_t *>(aq + blk * 34);
-        ob[1 + 2 * sub] = (uint16_t)(q & 0xffffu);
-        ob[2 + 2 * sub] = (uint16_t)(q >> 16);
-        if (sub == 0) ob[0] = (uint16_t)f32_to_fp16_bits(d);
+        if (store) {
+            uint16_t *ob = reinterpret_cast<uint16_t *>(aq + blk * 34);
+            ob[1 + 2 * sub] = (uint16_t)(q & 0xffffu);
+            ob[2 + 2 * sub] = (uint16_t)(q >> 16);
+            if (sub == 0) ob[0] = (uint16_t)f32_to_fp16_bits(d);
+        }
+    };
+    // the activations of each thread's first M tasks (all of them while
+    // k <= 4096), then the first weight pair (all clamped, so the loads are
+    // unconditional): the quantization waits for its own loads only, and the
+    // weights' trip from HBM overlaps it and the barrier
+    constexpr int kTaskStride = kFusedThreads / 8;
+    int blk = tid >> 3;
+    float4 x0[M];
+#pragma unroll
+    for (int t = 0; t < M; ++t) {
+        const int b = blk + t * kTaskStride;
+        x0[t] = *reinterpret_cast<const float4 *>(x + (size_t)(b < nblk ? b : nblk - 1) * 32 + sub * 4);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    const int pc = lane < np ? lane : np - 1;
+    uint32_t u0[9];
+    {
+        const uint32_t *ws = reinterpret_cast<const uint32_t *>(wrow + (uint32_t)pc * 36u);
+#pragma unroll
+        for (int i = 0; i < 9; ++i) u0[i] = ws[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < M; ++t) quantize(x0[t], blk + t * kTaskStride, blk + t * kTaskStride < nblk);
+    for (blk += M * kTaskStride; blk < nblk; blk += kTaskStride)
+        quantize(*reinterpret_cast<const float4 *>(x + (size_t)blk * 32 + sub * 4), blk, true);
     __syncthreads();
-    const int lane = tid & 63;
-    const int row = blockIdx.x * (kFusedThreads / 64) + (tid >> 6);
-    const int lrow = row < n ? row : n - 1;
     float acc[M];
 #pragma unroll
-    for (int mi = 0; mi < M; ++mi) acc[mi] = 0.0f;
-    for (int p = lane; p < nb / 2; p += 64) {
-        const uint32_t *ws = reinterpret_cast<const uint32_t *>(w + ((size_t)lrow * nb + 2 * p) * 18);
+    for (int mi = 0; mi < M; ++mi) {
+        const uint32_t *as = reinterpret_cast<const uint32_t *>(aq + (mi * nb + 2 * pc) * 34);
+        uint32_t v[17];
+#pragma unroll
+        for (int i = 0; i < 17; ++i) v[i] = as[i];
+        const float first = q4_0_pair_dot16(u0, v, 0.0f);
+        acc[mi] = lane < np ? first : 0.0f;  // lanes past the last pair drop their clamped duplicate
+    }
+    for (int p = lane + 64; p < np; p += 64) {
+        const uint32_t *ws = reinterpret_cast<const uint32_t *>(wrow + (uint32_t)p * 36u);
         uint32_t u[9];
 #pragma unroll
         for (int i = 0; i < 9; ++i) u[i] = ws[i];
-        const uint32_t q0[4] = {shift2(u[0], u[1]), shift2(u[1], u[2]), shift2(u[2], u[3]), shift2(u[3], u[4])};
-        const uint32_t q1[4] = {u[5], u[6], u[7], u[8]};
 #pragma unroll
         for (int mi = 0; mi < M; ++mi) {
             const uint32_t *as = reinterpret_cast<const uint32_t *>(aq + (mi * nb + 2 * p) * 34);
             uint32_t v[17];
 #pragma unroll
             for (int i = 0; i < 17; ++i) v[i] = as[i];
-            uint32_t x0[8], x1[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                x0[i] = shift2(v[i], v[i + 1]);
-                x1[i] = v[9 + i];
-            }
-            acc[mi] += q4_0_block_dot16(q0, u[0] & 0xffffu, x0, v[0] & 0xffffu);
-            acc[mi] += q4_0_block_dot16(q1, u[4] >> 16, x1, v[8] >> 16);
+            acc[mi] = q4_0_pair_dot16(u, v, acc[mi]);
         }
     }
     // the same sums as the unfused kernels, so the outputs are equal bit for

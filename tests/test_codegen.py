@@ -1,0 +1,80 @@
+"""Instruction-order checks on the gfx950 assembly of kernels whose
+synchronisation depends on it (CPU only: hipcc cross-compiles here).
+
+gemv_q4_0_m1_kernel<true> copies the activation row into LDS with direct
+loads (global_load_lds_*) and then issues the loads of each lane's first
+weight pair before waiting; the wait before the workgroup barrier is
+`s_waitcnt vmcnt(3)`, which covers the copies only because vector-memory
+loads complete in issue order and at least three weight loads were issued
+after the last copy on every path. If the compiler ever moved those weight
+loads below the wait (into a branch, say), vmcnt(3) would no longer wait for
+the copies and waves could read LDS before it is filled; this test fails
+instead.
+"""
+from __future__ import annotations
+
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG_DIR = os.path.join(REPO, "qgemm-perf-framework-ng_amd")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+
+def _kernel_lines(asm: str, symbol_part: str) -> list[str]:
+    """Instruction and label lines of the first function whose label contains symbol_part."""
+    lines = [ln.split(";")[0].strip() for ln in asm.splitlines()]
+    start = next(i for i, ln in enumerate(lines) if ln.endswith(":") and symbol_part in ln and not ln.startswith("."))
+    out = []
+    for t in lines[start + 1:]:
+        if not t or (t.startswith(".") and not t.endswith(":")):
+            continue
+        out.append(t)
+        if t.startswith("s_endpgm"):
+            break
+    return out
+
+
+def check_copy_then_wait(lines: list[str], min_loads: int = 3) -> None:
+    """The order the vmcnt(3) wait needs (raises AssertionError otherwise)."""
+    wait = next(i for i in range(len(lines) - 1)
+                if lines[i] == "s_waitcnt vmcnt(3)" and lines[i + 1] == "s_barrier")
+    dma = [i for i, t in enumerate(lines) if t.startswith("global_load_lds")]
+    assert dma, "no direct-to-LDS copy found"
+    assert max(dma) < wait, "a direct-to-LDS copy is issued after the wait"
+    # straight-line stretch that every path to the wait runs through
+    labels = [i for i in range(wait) if lines[i].endswith(":")]
+    first = labels[-1] + 1 if labels else 0
+    assert first > max(dma), "a path to the wait may skip the weight loads"
+    seg = lines[first:wait]
+    assert not any(re.match(r"s_(c)?branch", t) for t in seg), "branch between the copies and the wait"
+    loads = [t for t in seg if re.match(r"(global|buffer)_load_(?!lds)", t)]
+    assert len(loads) >= min_loads, f"only {len(loads)} weight loads between the copies and vmcnt(3)"
+
+
+def test_checker_rejects_sunk_loads():
+    """The checker itself: loads moved below the wait must fail it."""
+    good = ["global_load_lds_dwordx4 v[0:1], off", ".LBB0_2:", "global_load_dwordx4 v[0:3], v9, s[4:5]",
+            "global_load_dword v4, v9, s[4:5] offset:32", "global_load_dwordx4 v[5:8], v9, s[4:5] offset:16",
+            "s_waitcnt vmcnt(3)", "s_barrier", "ds_read_b32 v1, v2", "s_endpgm"]
+    check_copy_then_wait(good)
+    sunk = good[:2] + ["s_waitcnt vmcnt(3)", "s_barrier"] + good[2:5] + good[7:]
+    with pytest.raises(AssertionError):
+        check_copy_then_wait(sunk)
+    branchy = good[:2] + ["s_cbranch_execz .LBB0_3"] + good[2:]
+    with pytest.raises(AssertionError):
+        check_copy_then_wait(branchy)
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC) or shutil.which("make") is None, reason="needs hipcc and make")
+def test_m1_gemv_copy_precedes_wait():
+    out = os.path.join(PKG_DIR, "_build", "gemv.hip.s")
+    subprocess.run(["make", "-s", "-C", PKG_DIR, out], check=True, capture_output=True, timeout=600)
+    with open(out) as f:
+        asm = f.read()
+    lines = _kernel_lines(asm, "gemv_q4_0_m1_kernelILb1E")
+    check_copy_then_wait(lines)

@@ -166,10 +166,12 @@ def test_naive_bit_exact(hip, torch_gpu, oracle, qtype, m, n, k):
 
 @pytest.mark.parametrize("m", [1, 2, 3, 5, 7, 8, 9, 12, 13, 15, 16])
 @pytest.mark.parametrize("n,k", [(4096, 4096), (257, 1536), (64, 256), (33, 8192), (40, 65536), (129, 7680),
-                                 (77, 320), (50, 64)])
+                                 (77, 320), (50, 64), (21, 20480)])
 def test_gemv_q4_0(hip, torch_gpu, oracle, m, n, k):
-    """m = 1 (block pair per lane), m = 2..16 with the activations staged in
-    LDS (m * (k / 64) * 76 + 16 <= 160 KB), m = 2..8 beyond that (groups of 8
+    """m = 1 (block pair per lane; the activation row copied into LDS in
+    rounds of 16 KB up to 64 KB, k = 20480 taking two rounds, a dword tail at
+    k = 320 and 64), m = 2..16 with the activations staged in LDS
+    (m * (k / 64) * 76 + 16 <= 160 KB), m = 2..8 beyond that (groups of 8
     blocks per lane)."""
     torch = torch_gpu
     if m > 8 and m * (k // 64) * 76 + 16 > 160 * 1024:
