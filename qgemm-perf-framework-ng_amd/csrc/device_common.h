@@ -245,8 +245,8 @@ __device__ __forceinline__ void use_here(const uint32_t (&x)[N]) {
 // Marks the N registers of x as redefined at this point: nothing computed
 // from them can be moved above it (arithmetic on loaded values hoisted above
 // a workgroup barrier makes the barrier wait for those loads).
-template <int N>
-__device__ __forceinline__ void redefine_here(uint32_t (&x)[N]) {
+template <class T, int N>
+__device__ __forceinline__ void redefine_here(T (&x)[N]) {
 #pragma unroll
     for (int i = 0; i < N; ++i) asm volatile("" : "+v"(x[i]));
 }

@@ -69,13 +69,20 @@ __constant__ Iq2Signs kIq2Signs = expand_iq2_signs();
 
 constexpr int kIq2TableBytes = 256 * 8 + 128 * 8;  // grid, then sign masks
 
-// The LDS copy of both tables (384 entries of 8 bytes), one 8-byte load and
-// store per entry, spread over the workgroup's threads.
-__device__ __forceinline__ void fill_iq2_tables(uint8_t *tab) {
-    for (int e = threadIdx.x; e < 384; e += blockDim.x) {
-        const uint32_t *src = e < 256 ? kIq2Grid.v[e] : kIq2Signs.v[e - 256];
-        *reinterpret_cast<uint2 *>(tab + 8 * e) = make_uint2(src[0], src[1]);
-    }
+// The LDS copy of both tables (384 entries of 8 bytes) for workgroups of 256
+// threads, its loads and stores separate so that other loads can be issued
+// between them: thread t loads entries t and t + 256 (the latter clamped into
+// the table, stored only where it exists).
+__device__ __forceinline__ void load_iq2_table_entries(uint32_t (&t)[4]) {
+    const int e1 = (int)threadIdx.x + 256 < 384 ? (int)threadIdx.x + 256 : 383;
+    t[0] = kIq2Grid.v[threadIdx.x][0];
+    t[1] = kIq2Grid.v[threadIdx.x][1];
+    t[2] = kIq2Signs.v[e1 - 256][0];
+    t[3] = kIq2Signs.v[e1 - 256][1];
+}
+__device__ __forceinline__ void store_iq2_table_entries(uint8_t *tab, const uint32_t (&t)[4]) {
+    *reinterpret_cast<uint2 *>(tab + 8 * threadIdx.x) = make_uint2(t[0], t[1]);
+    if (threadIdx.x < 128) *reinterpret_cast<uint2 *>(tab + 8 * (threadIdx.x + 256)) = make_uint2(t[2], t[3]);
 }
 
 // The 32 signed weights of one sub-block from its four grid indices (gidx)
@@ -113,23 +120,34 @@ __device__ __forceinline__ int dot8(const uint32_t *w, const uint32_t *x) {
     return s;
 }
 
-// Scale and min of q4_K sub-block j from the 12 packed bytes (dwords 1..3 of
-// the block header), with the reference's decode (llama_reference.cpp:116-121).
-__device__ __forceinline__ void q4_K_scale_min(const uint4 &hd, int j, int &sc, int &mn) {
-    const uint32_t words[3] = {hd.y, hd.z, hd.w};
-    auto byte = [&](int i) { return (int)((words[i / 4] >> (8 * (i % 4))) & 0xffu); };
-    if (j < 4) {
-        sc = byte(j) & 63;
-        mn = byte(j + 4) & 63;
-    } else {
-        sc = (byte(j + 4) & 15) | ((byte(j - 4) >> 6) << 4);
-        mn = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
-    }
+// Scales and mins of q4_K sub-blocks 2e and 2e + 1 (e = 0..3) from the 12
+// packed bytes (dwords 1..3 of the block header), the reference's decode
+// (llama_reference.cpp:116-121) done four sub-blocks per dword and without a
+// branch on the lane: sub-blocks 0..3 take the low six bits of bytes 0..3
+// (scales) and 4..7 (mins); sub-blocks 4..7 take the low (scales) or high
+// (mins) nibble of bytes 8..11 with the top two bits of bytes 0..3 (scales)
+// or 4..7 (mins) above it. Lane e then picks bytes 2e % 4 and 2e % 4 + 1.
+__device__ __forceinline__ void q4_K_scale_min_pair(const uint4 &hd, int e, int &sc0, int &m0, int &sc1, int &m1) {
+    const uint32_t sc_lo = hd.y & 0x3f3f3f3fu, mn_lo = hd.z & 0x3f3f3f3fu;
+    const uint32_t sc_hi = (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u);
+    const uint32_t mn_hi = ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u);
+    const uint32_t scw = e < 2 ? sc_lo : sc_hi, mnw = e < 2 ? mn_lo : mn_hi;
+    const int sh = 16 * (e & 1);
+    sc0 = (int)((scw >> sh) & 0xffu);
+    sc1 = (int)((scw >> (sh + 8)) & 0xffu);
+    m0 = (int)((mnw >> sh) & 0xffu);
+    m1 = (int)((mnw >> (sh + 8)) & 0xffu);
 }
 
 // kLdsAct (m == 1, rows up to 64 KB): workgroups of 16 weight rows copy the
-// activation row into LDS once with 16-byte loads, and the waves read it
-// there instead of each fetching it from L2.
+// activation row into LDS once, and the waves read it there instead of each
+// fetching it from L2. The copy uses direct loads into LDS
+// (global_load_lds_dwordx4: lane i of a wave writes 16 bytes at the wave's
+// LDS base + 16 i), and every lane issues the three 16-byte loads of its
+// first weight step (clamped, so always issued) before any wave waits: each
+// wave then waits for its own copies only (s_waitcnt vmcnt(3): memory loads
+// complete in issue order) and meets the others at the barrier, so the
+// activation's trip from L2 overlaps the weight stream.
 constexpr int kM1LdsThreads = 1024;
 
 template <int M, bool kLdsAct = false>
@@ -137,34 +155,29 @@ __global__ __launch_bounds__(kLdsAct ? kM1LdsThreads : kThreads) void gemv_q4_K_
     const uint8_t *__restrict__ w, const uint8_t *__restrict__ a_global, float *__restrict__ c, int n, int nb) {
     constexpr int kBlockThreads = kLdsAct ? kM1LdsThreads : kThreads;
     extern __shared__ __align__(16) uint8_t sact[];
-    const uint8_t *a = a_global;
-    if constexpr (kLdsAct) {
-        static_assert(M == 1, "one activation row");
-        const int n16 = nb * kQ8KBytes / 16, nd = nb * kQ8KBytes / 4;
-        const uint4 *src4 = reinterpret_cast<const uint4 *>(a_global);
-        uint4 *dst4 = reinterpret_cast<uint4 *>(sact);
-        for (int i = threadIdx.x; i < n16; i += kBlockThreads) dst4[i] = src4[i];
-        const uint32_t *src = reinterpret_cast<const uint32_t *>(a_global);
-        uint32_t *dst = reinterpret_cast<uint32_t *>(sact);
-        for (int i = 4 * n16 + threadIdx.x; i < nd; i += kBlockThreads) dst[i] = src[i];
-        __syncthreads();
-        a = sact;
-    }
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (kBlockThreads / 64) + (threadIdx.x >> 6);
+    // the row is uniform across the wave: its base address lives in scalar registers
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int row = blockIdx.x * (kBlockThreads / 64) + wave;
     const int lrow = row < n ? row : n - 1;  // clamped: loads stay unconditional, the store is guarded
+    const uint8_t *wrow = w + (size_t)lrow * nb * kQ4KBytes;
     const int slot = lane >> 2, e = lane & 3;
+    // lane's header and 32 nibble bytes of super-block b0 + slot (clamped)
+    auto load_w = [&](int b0, uint4 (&wq)[3]) {
+        const int b = b0 + slot;
+        const uint8_t *blk = wrow + (uint32_t)(b < nb ? b : nb - 1) * (uint32_t)kQ4KBytes;
+        wq[0] = *reinterpret_cast<const uint4 *>(blk);
+        wq[1] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * e);
+        wq[2] = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * e);
+    };
     float acc[M];
 #pragma unroll
     for (int mi = 0; mi < M; ++mi) acc[mi] = 0.0f;
-    for (int b0 = 0; b0 < nb; b0 += 16) {
+    // acc += the step's super-block parts against activations a
+    auto step = [&](int b0, const uint4 (&wq)[3], const uint8_t *a) {
         const int b = b0 + slot;
         const bool valid = b < nb;
         const int lb = valid ? b : nb - 1;
-        const uint8_t *blk = w + ((size_t)lrow * nb + lb) * kQ4KBytes;
-        const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
-        const uint4 qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * e);
-        const uint4 qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * e);
         uint32_t x[M][16], bs[M][2];
         float ad[M];
 #pragma unroll
@@ -179,6 +192,7 @@ __global__ __launch_bounds__(kLdsAct ? kM1LdsThreads : kThreads) void gemv_q4_K_
             ad[mi] = *reinterpret_cast<const float *>(ab);
         }
         __builtin_amdgcn_sched_barrier(0);
+        const uint4 &hd = wq[0], &qa = wq[1], &qb = wq[2];
         const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
         uint32_t lo[8], hi[8];
 #pragma unroll
@@ -187,8 +201,7 @@ __global__ __launch_bounds__(kLdsAct ? kM1LdsThreads : kThreads) void gemv_q4_K_
             hi[i] = (q[i] >> 4) & 0x0f0f0f0fu;
         }
         int sc0, m0, sc1, m1;
-        q4_K_scale_min(hd, 2 * e, sc0, m0);
-        q4_K_scale_min(hd, 2 * e + 1, sc1, m1);
+        q4_K_scale_min_pair(hd, e, sc0, m0, sc1, m1);
         const float d = fp16_to_f32(hd.x & 0xffffu), dmin = fp16_to_f32(hd.x >> 16);
 #pragma unroll
         for (int mi = 0; mi < M; ++mi) {
@@ -199,6 +212,35 @@ __global__ __launch_bounds__(kLdsAct ? kM1LdsThreads : kThreads) void gemv_q4_K_
             const float part = ad[mi] * fmaf(-dmin, (float)im, d * (float)is);
             acc[mi] += valid ? part : 0.0f;
         }
+    };
+    int b0 = 0;
+    const uint8_t *a = a_global;
+    if constexpr (kLdsAct) {
+        static_assert(M == 1, "one activation row");
+        // 16-byte chunks (the row base is 16-byte aligned), wave w taking
+        // chunks 64 w + lane (+ 1024 per round), then the dword tail from the
+        // last wave
+        const int n16 = nb * kQ8KBytes / 16, nd = nb * kQ8KBytes / 4;
+        for (int c0 = wave * 64; c0 < n16; c0 += kBlockThreads) {
+            if (c0 + lane < n16)
+                __builtin_amdgcn_global_load_lds(a_global + (size_t)(c0 + lane) * 16,
+                                                 (__attribute__((address_space(3))) void *)(sact + c0 * 16), 16, 0, 0);
+        }
+        if (wave == kBlockThreads / 64 - 1 && 4 * n16 + lane < nd)
+            __builtin_amdgcn_global_load_lds(a_global + (size_t)(4 * n16 + lane) * 4,
+                                             (__attribute__((address_space(3))) void *)(sact + n16 * 16), 4, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        uint4 wq[3];
+        load_w(0, wq);
+        asm volatile("s_waitcnt vmcnt(3)\n\ts_barrier" ::: "memory");
+        a = sact;
+        step(0, wq, a);
+        b0 = 16;
+    }
+    for (; b0 < nb; b0 += 16) {
+        uint4 wq[3];
+        load_w(b0, wq);
+        step(b0, wq, a);
     }
 #pragma unroll
     for (int mi = 0; mi < M; ++mi) acc[mi] = wave_sum_lane63(acc[mi]);
@@ -208,47 +250,61 @@ __global__ __launch_bounds__(kLdsAct ? kM1LdsThreads : kThreads) void gemv_q4_K_
     }
 }
 
+// The tables' trip into LDS overlaps the first step's weight and activation
+// loads: each thread issues its table loads, then the first step's loads,
+// stores its table entries (waiting for the table loads only) and meets the
+// others at the barrier; the weight words are decoded after it.
 template <int M>
 __global__ __launch_bounds__(kThreads) void gemv_iq2_xxs_kernel(const uint8_t *__restrict__ w,
                                                                const uint8_t *__restrict__ a, float *__restrict__ c,
                                                                int n, int nb) {
+    static_assert(kThreads == 256, "table copy in halves of 256 entries");
     __shared__ __align__(16) uint8_t grid[kIq2TableBytes];
-    fill_iq2_tables(grid);
-    __syncthreads();
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int row = blockIdx.x * (kThreads / 64) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lrow = row < n ? row : n - 1;
     const int slot = lane >> 3, j = lane & 7;
     // the row's base once; per step only the block offset
     const size_t wbase = (size_t)lrow * nb * kIq2Bytes;
     const uint8_t *wrow = w + wbase;
-    float acc[M];
-#pragma unroll
-    for (int mi = 0; mi < M; ++mi) acc[mi] = 0.0f;
-    for (int b0 = 0; b0 < nb; b0 += 8) {
+    // one step's loads: the lane's sub-block words (66-byte blocks are 2-byte
+    // aligned: the covering dwords plus a trailing half-word, never past the
+    // sub-block's last byte), the block's d, and the activation sub-blocks
+    struct Step {
+        uint32_t wv[2];  // d0, d1
+        uint16_t th[2];  // tail, dh (widened after the barrier)
+        uint32_t x[M][8];
+        float ad[M];
+    };
+    auto load = [&](int b0, Step &st) {
         const int b = b0 + slot;
-        const bool valid = b < nb;
-        const int lb = valid ? b : nb - 1;
-        // 66-byte blocks are 2-byte aligned: the covering dwords plus a
-        // trailing half-word, never past the sub-block's last byte
+        const int lb = b < nb ? b : nb - 1;
         const size_t boff = (size_t)lb * kIq2Bytes;
         const size_t o = boff + 2 + 8 * j;
         const bool sh = ((wbase + o) & 3) != 0;
         const uint32_t *p4 = reinterpret_cast<const uint32_t *>(wrow + o - (sh ? 2 : 0));
-        const uint32_t d0 = p4[0], d1 = p4[1];
-        const uint32_t tail = *reinterpret_cast<const uint16_t *>(wrow + o + 6);
-        const uint32_t dh = *reinterpret_cast<const uint16_t *>(wrow + boff);
-        uint32_t x[M][8];
-        float ad[M];
+        st.wv[0] = p4[0];
+        st.wv[1] = p4[1];
+        st.th[0] = *reinterpret_cast<const uint16_t *>(wrow + o + 6);
+        st.th[1] = *reinterpret_cast<const uint16_t *>(wrow + boff);
 #pragma unroll
         for (int mi = 0; mi < M; ++mi) {
             const uint8_t *ab = a + (size_t)(mi * nb + lb) * kQ8KBytes;
             const uint32_t *xs = reinterpret_cast<const uint32_t *>(ab + 4 + 32 * j);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) x[mi][i] = xs[i];
-            ad[mi] = *reinterpret_cast<const float *>(ab);
+            for (int i = 0; i < 8; ++i) st.x[mi][i] = xs[i];
+            st.ad[mi] = *reinterpret_cast<const float *>(ab);
         }
-        __builtin_amdgcn_sched_barrier(0);
+    };
+    float acc[M];
+#pragma unroll
+    for (int mi = 0; mi < M; ++mi) acc[mi] = 0.0f;
+    auto compute = [&](int b0, const Step &st) {
+        const int b = b0 + slot;
+        const bool valid = b < nb;
+        const int lb = valid ? b : nb - 1;
+        const bool sh = ((wbase + (size_t)lb * kIq2Bytes + 2 + 8 * j) & 3) != 0;
+        const uint32_t d0 = st.wv[0], d1 = st.wv[1], tail = st.th[0], dh = st.th[1];
         const uint32_t gidx = sh ? __builtin_amdgcn_alignbyte(d1, d0, 2) : d0;
         const uint32_t ss = sh ? ((d1 >> 16) | (tail << 16)) : d1;
         uint32_t v[8];
@@ -258,9 +314,27 @@ __global__ __launch_bounds__(kThreads) void gemv_iq2_xxs_kernel(const uint8_t *_
 #pragma unroll
         for (int mi = 0; mi < M; ++mi) {
             // exact integer sum of the super-block over its eight lanes
-            const int is = group_sum_dpp<8>(scale * dot8(v, x[mi]));
-            if (j == 0 && valid) acc[mi] += (t0 * ad[mi]) * (float)is;
+            const int is = group_sum_dpp<8>(scale * dot8(v, st.x[mi]));
+            if (j == 0 && valid) acc[mi] += (t0 * st.ad[mi]) * (float)is;
         }
+    };
+    uint32_t tab[4];
+    load_iq2_table_entries(tab);
+    __builtin_amdgcn_sched_barrier(0);
+    Step st0;
+    load(0, st0);
+    __builtin_amdgcn_sched_barrier(0);
+    use_here(tab);
+    store_iq2_table_entries(grid, tab);
+    __syncthreads();
+    redefine_here(st0.wv);  // decoded after the barrier, which then waits for the tables only
+    redefine_here(st0.th);
+    compute(0, st0);
+    for (int b0 = 8; b0 < nb; b0 += 8) {
+        Step st;
+        load(b0, st);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(b0, st);
     }
 #pragma unroll
     for (int mi = 0; mi < M; ++mi) acc[mi] = wave_sum_lane63(acc[mi]);
@@ -290,28 +364,60 @@ __host__ __device__ constexpr int64_t kq_staged_lds_bytes(int64_t m, int64_t nsb
     return m * nsb * (kQsStride + kSideStride) + kIq2TableBytes;  // + the iq2_xxs tables
 }
 
-// four threads per block: quarter t copies qs[64t, 64t + 64), forms the bsum
-// pairs 2t and 2t + 1, and quarter 0 widens nothing (d is fp32 already)
-template <int M>
-__device__ __forceinline__ void stage_q8_K(const uint8_t *__restrict__ a, uint8_t *qs, uint8_t *side, int nsb) {
-    for (int task = threadIdx.x; task < M * nsb * 4; task += kStagedThreads) {
-        const int blk = task >> 2, t = task & 3;
-        const uint8_t *src = a + (size_t)blk * kQ8KBytes;
-        const uint32_t *q = reinterpret_cast<const uint32_t *>(src + 4 + 64 * t);
-        uint32_t v[16];
+// Four tasks per block: quarter t copies qs[64t, 64t + 64), forms the bsum
+// pairs 2t and 2t + 1, and quarter 0 also copies d (fp32 already). A task's
+// loads (16 qs dwords, two bsum dwords, d) and its LDS stores are separate
+// steps, so that a kernel can issue other loads between them.
+__device__ __forceinline__ void load_q8_K_quarter(const uint8_t *__restrict__ a, int task, uint32_t (&r)[19]) {
+    const int blk = task >> 2, t = task & 3;
+    const uint8_t *src = a + (size_t)blk * kQ8KBytes;
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(src + 4 + 64 * t);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = q[i];
-        const uint32_t *bp = reinterpret_cast<const uint32_t *>(src + 260 + 8 * t);
-        const uint32_t b0 = bp[0], b1 = bp[1];
-        const float d = *reinterpret_cast<const float *>(src);
-        uint4 *dq = reinterpret_cast<uint4 *>(qs + (size_t)blk * kQsStride + 64 * t);
+    for (int i = 0; i < 16; ++i) r[i] = q[i];
+    const uint32_t *bp = reinterpret_cast<const uint32_t *>(src + 260 + 8 * t);
+    r[16] = bp[0];
+    r[17] = bp[1];
+    r[18] = *reinterpret_cast<const uint32_t *>(src);
+}
+__device__ __forceinline__ void store_q8_K_quarter(uint8_t *qs, uint8_t *side, int task, const uint32_t (&r)[19]) {
+    const int blk = task >> 2, t = task & 3;
+    uint4 *dq = reinterpret_cast<uint4 *>(qs + (size_t)blk * kQsStride + 64 * t);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dq[i] = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-        uint8_t *sd = side + (size_t)blk * kSideStride;
-        *reinterpret_cast<int2 *>(sd + 8 * t) =
-            make_int2((int)(int16_t)(b0 & 0xffffu) + (int)(int16_t)(b0 >> 16),
-                      (int)(int16_t)(b1 & 0xffffu) + (int)(int16_t)(b1 >> 16));
-        if (t == 0) *reinterpret_cast<float *>(sd + 32) = d;
+    for (int i = 0; i < 4; ++i) dq[i] = make_uint4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
+    uint8_t *sd = side + (size_t)blk * kSideStride;
+    *reinterpret_cast<int2 *>(sd + 8 * t) = make_int2((int)(int16_t)(r[16] & 0xffffu) + (int)(int16_t)(r[16] >> 16),
+                                                      (int)(int16_t)(r[17] & 0xffffu) + (int)(int16_t)(r[17] >> 16));
+    if (t == 0) *reinterpret_cast<uint32_t *>(sd + 32) = r[18];
+}
+
+// The staging prologue shared by the staged kernels: each thread loads its
+// first staging task (the only one while m * k / 64 <= 1024, so always at
+// k <= 4096; threads without one load nothing) and then calls issue(), which
+// issues the loads of the lane's first weight step; only then are the first
+// tasks stored (waiting for their own loads) and the remaining tasks staged.
+// The caller's barrier then waits for the staging alone, and the weights'
+// trip from HBM overlaps it.
+template <int M, class Issue>
+__device__ __forceinline__ void stage_q8_K_overlapped(const uint8_t *__restrict__ a, uint8_t *qs, uint8_t *side, int nsb,
+                                                      Issue issue) {
+    const int ntask = M * nsb * 4;
+    int task = threadIdx.x;
+    uint32_t r0[19];
+    if (task < ntask) {
+        load_q8_K_quarter(a, task, r0);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 19; ++i) r0[i] = 0;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    issue();
+    __builtin_amdgcn_sched_barrier(0);
+    use_here(r0);
+    if (task < ntask) store_q8_K_quarter(qs, side, task, r0);
+    for (task += kStagedThreads; task < ntask; task += kStagedThreads) {
+        uint32_t r[19];
+        load_q8_K_quarter(a, task, r);
+        store_q8_K_quarter(qs, side, task, r);
     }
 }
 
@@ -328,35 +434,39 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_q4_K_staged_kernel(const 
     constexpr int kLaneShift = 6 - log2_pow2(P);
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t *qs = lds, *side = lds + (size_t)M * nb * kQsStride;
-    stage_q8_K<M>(a, qs, side, nb);
-    __syncthreads();
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (kStagedThreads / 64) + (threadIdx.x >> 6);
+    const int row = blockIdx.x * (kStagedThreads / 64) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lrow = row < n ? row : n - 1;  // clamped: loads stay unconditional, the store is guarded
+    const uint8_t *wrow = w + (size_t)lrow * nb * kQ4KBytes;
     const int slot = lane >> 2, e = lane & 3;
     const int f = lane >> kLaneShift;
-    float acc[NA];
-#pragma unroll
-    for (int q = 0; q < NA; ++q) acc[q] = 0.0f;
-    for (int b0 = 0; b0 < nb; b0 += 16) {
+    // the lane's header and 32 nibble bytes of super-block b0 + slot (clamped)
+    auto load_w = [&](int b0, uint32_t (&wq)[12]) {
         const int b = b0 + slot;
-        const bool valid = b < nb;
-        const int lb = valid ? b : nb - 1;
-        const uint8_t *blk = w + ((size_t)lrow * nb + lb) * kQ4KBytes;
+        const uint8_t *blk = wrow + (uint32_t)(b < nb ? b : nb - 1) * (uint32_t)kQ4KBytes;
         const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
         const uint4 qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * e);
         const uint4 qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * e);
-        __builtin_amdgcn_sched_barrier(0);
-        const uint32_t qw[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        const uint32_t t[12] = {hd.x, hd.y, hd.z, hd.w, qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+        for (int i = 0; i < 12; ++i) wq[i] = t[i];
+    };
+    float acc[NA];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) acc[q] = 0.0f;
+    auto step = [&](int b0, const uint32_t (&wq)[12]) {
+        const int b = b0 + slot;
+        const bool valid = b < nb;
+        const int lb = valid ? b : nb - 1;
+        const uint4 hd = make_uint4(wq[0], wq[1], wq[2], wq[3]);
         uint32_t lo[8], hi[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            lo[i] = qw[i] & 0x0f0f0f0fu;
-            hi[i] = (qw[i] >> 4) & 0x0f0f0f0fu;
+            lo[i] = wq[4 + i] & 0x0f0f0f0fu;
+            hi[i] = (wq[4 + i] >> 4) & 0x0f0f0f0fu;
         }
         int sc0, m0, sc1, m1;
-        q4_K_scale_min(hd, 2 * e, sc0, m0);
-        q4_K_scale_min(hd, 2 * e + 1, sc1, m1);
+        q4_K_scale_min_pair(hd, e, sc0, m0, sc1, m1);
         const float d = fp16_to_f32(hd.x & 0xffffu), dmin = fp16_to_f32(hd.x >> 16);
 #pragma unroll
         for (int q = 0; q < NA; ++q) {
@@ -380,6 +490,17 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_q4_K_staged_kernel(const 
             const float part = ad * fmaf(-dmin, (float)im, d * (float)is);
             acc[q] += valid ? part : 0.0f;
         }
+    };
+    uint32_t wq0[12];
+    stage_q8_K_overlapped<M>(a, qs, side, nb, [&] { load_w(0, wq0); });
+    __syncthreads();
+    redefine_here(wq0);  // decoded after the barrier, which then waits for the staging only
+    step(0, wq0);
+    for (int b0 = 16; b0 < nb; b0 += 16) {
+        uint32_t wq[12];
+        load_w(b0, wq);
+        __builtin_amdgcn_sched_barrier(0);
+        step(b0, wq);
     }
     // reduce-scatter (exchange offsets 32, 16, ...), then a DPP sum over the
     // 64 / P lanes left: the group's last lane holds it
@@ -419,34 +540,39 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(con
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t *qs = lds, *side = lds + (size_t)M * nb * kQsStride;
     uint8_t *grid = side + (size_t)M * nb * kSideStride;
-    fill_iq2_tables(grid);
-    stage_q8_K<M>(a, qs, side, nb);
-    __syncthreads();
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (kStagedThreads / 64) + (threadIdx.x >> 6);
+    const int row = blockIdx.x * (kStagedThreads / 64) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lrow = row < n ? row : n - 1;
+    const size_t wbase = (size_t)lrow * nb * kIq2Bytes;  // offsets from w, which is 4-byte aligned
+    const uint8_t *wrow = w + wbase;
     const int slot = lane >> 3, j = lane & 7;
     const int f = j & (P - 1);
-    float accp[NG];                          // row P * g + f, in lanes j < P
-    float accx[NX > 0 ? NX : 1];             // rows NG * P.., in lanes j == 0
+    // 66-byte blocks are 2-byte aligned: the covering dwords plus a trailing
+    // half-word, never past the sub-block's last byte; wv = d0, d1, th = tail,
+    // dh (kept 16-bit until decoded)
+    auto load_w = [&](int b0, uint32_t (&wv)[2], uint16_t (&th)[2]) {
+        const int b = b0 + slot;
+        const size_t boff = (size_t)(b < nb ? b : nb - 1) * kIq2Bytes;
+        const size_t o = boff + 2 + 8 * j;
+        const bool sh = ((wbase + o) & 3) != 0;
+        const uint32_t *p4 = reinterpret_cast<const uint32_t *>(wrow + o - (sh ? 2 : 0));
+        wv[0] = p4[0];
+        wv[1] = p4[1];
+        th[0] = *reinterpret_cast<const uint16_t *>(wrow + o + 6);
+        th[1] = *reinterpret_cast<const uint16_t *>(wrow + boff);
+    };
+    float accp[NG];               // row P * g + f, in lanes j < P
+    float accx[NX > 0 ? NX : 1];  // rows NG * P.., in lanes j == 0
 #pragma unroll
     for (int g = 0; g < NG; ++g) accp[g] = 0.0f;
 #pragma unroll
     for (int q = 0; q < (NX > 0 ? NX : 1); ++q) accx[q] = 0.0f;
-    for (int b0 = 0; b0 < nb; b0 += 8) {
+    auto step = [&](int b0, const uint32_t (&wv)[2], const uint16_t (&th)[2]) {
         const int b = b0 + slot;
         const bool valid = b < nb;
         const int lb = valid ? b : nb - 1;
-        // 66-byte blocks are 2-byte aligned: the covering dwords plus a
-        // trailing half-word, never past the sub-block's last byte
-        const size_t base = ((size_t)lrow * nb + lb) * kIq2Bytes;
-        const size_t o = base + 2 + 8 * j;
-        const uint32_t *p4 = reinterpret_cast<const uint32_t *>(w + (o & ~(size_t)3));
-        const uint32_t d0 = p4[0], d1 = p4[1];
-        const uint32_t tail = *reinterpret_cast<const uint16_t *>(w + o + 6);
-        const uint32_t dh = *reinterpret_cast<const uint16_t *>(w + base);
-        __builtin_amdgcn_sched_barrier(0);
-        const bool sh = (o & 3) != 0;
+        const bool sh = ((wbase + (size_t)lb * kIq2Bytes + 2 + 8 * j) & 3) != 0;
+        const uint32_t d0 = wv[0], d1 = wv[1], tail = th[0], dh = th[1];
         const uint32_t gidx = sh ? __builtin_amdgcn_alignbyte(d1, d0, 2) : d0;
         const uint32_t ss = sh ? ((d1 >> 16) | (tail << 16)) : d1;
         uint32_t v[8];
@@ -482,6 +608,28 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(con
             const float adq = *reinterpret_cast<const float *>(side + (size_t)(q * nb + lb) * kSideStride + 32);
             if (j == 0) accx[q - NG * P] += (t0 * adq) * (float)tot;
         }
+    };
+    // the table entry of this thread (384 entries, one per thread) is loaded
+    // with the first staging task, ahead of the weights
+    static_assert(kStagedThreads >= 384, "one table entry per thread");
+    const int te = (int)threadIdx.x < 384 ? (int)threadIdx.x : 383;
+    const uint32_t *tsrc = te < 256 ? kIq2Grid.v[te] : kIq2Signs.v[te - 256];
+    uint32_t tab[2] = {tsrc[0], tsrc[1]};
+    uint32_t wv0[2];
+    uint16_t th0[2];
+    stage_q8_K_overlapped<M>(a, qs, side, nb, [&] { load_w(0, wv0, th0); });
+    use_here(tab);
+    if (threadIdx.x < 384) *reinterpret_cast<uint2 *>(grid + 8 * threadIdx.x) = make_uint2(tab[0], tab[1]);
+    __syncthreads();
+    redefine_here(wv0);  // decoded after the barrier, which then waits for the staging only
+    redefine_here(th0);
+    step(0, wv0, th0);
+    for (int b0 = 8; b0 < nb; b0 += 8) {
+        uint32_t wv[2];
+        uint16_t th[2];
+        load_w(b0, wv, th);
+        __builtin_amdgcn_sched_barrier(0);
+        step(b0, wv, th);
     }
     // across the eight super-block slots
 #pragma unroll

@@ -1,15 +1,15 @@
 """Instruction-order checks on the gfx950 assembly of kernels whose
 synchronisation depends on it (CPU only: hipcc cross-compiles here).
 
-gemv_q4_0_m1_kernel<true> copies the activation row into LDS with direct
-loads (global_load_lds_*) and then issues the loads of each lane's first
-weight pair before waiting; the wait before the workgroup barrier is
-`s_waitcnt vmcnt(3)`, which covers the copies only because vector-memory
-loads complete in issue order and at least three weight loads were issued
-after the last copy on every path. If the compiler ever moved those weight
-loads below the wait (into a branch, say), vmcnt(3) would no longer wait for
-the copies and waves could read LDS before it is filled; this test fails
-instead.
+gemv_q4_0_m1_kernel<true> and gemv_q4_K_kernel<1, true> copy the activation
+row into LDS with direct loads (global_load_lds_*) and then issue the loads
+of each lane's first weight step before waiting; the wait before the
+workgroup barrier is `s_waitcnt vmcnt(3)`, which covers the copies only
+because vector-memory loads complete in issue order and at least three
+weight loads were issued after the last copy on every path. If the compiler
+ever moved those weight loads below the wait (into a branch, say), vmcnt(3)
+would no longer wait for the copies and waves could read LDS before it is
+filled; this test fails instead.
 """
 from __future__ import annotations
 
@@ -54,6 +54,11 @@ def check_copy_then_wait(lines: list[str], min_loads: int = 3) -> None:
     assert not any(re.match(r"s_(c)?branch", t) for t in seg), "branch between the copies and the wait"
     loads = [t for t in seg if re.match(r"(global|buffer)_load_(?!lds)", t)]
     assert len(loads) >= min_loads, f"only {len(loads)} weight loads between the copies and vmcnt(3)"
+    # a shorter wait before the barrier (weights decoded above it) would be
+    # correct but would make every wave wait for its weights there
+    for t in seg:
+        m = re.match(r"s_waitcnt .*vmcnt\((\d+)\)", t)
+        assert not (m and int(m.group(1)) < 3), f"early weight wait before the barrier: {t}"
 
 
 def test_checker_rejects_sunk_loads():
@@ -68,13 +73,17 @@ def test_checker_rejects_sunk_loads():
     branchy = good[:2] + ["s_cbranch_execz .LBB0_3"] + good[2:]
     with pytest.raises(AssertionError):
         check_copy_then_wait(branchy)
+    early = good[:5] + ["s_waitcnt vmcnt(0)", "v_and_b32_e32 v1, 15, v2"] + good[5:]
+    with pytest.raises(AssertionError):
+        check_copy_then_wait(early)
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC) or shutil.which("make") is None, reason="needs hipcc and make")
-def test_m1_gemv_copy_precedes_wait():
-    out = os.path.join(PKG_DIR, "_build", "gemv.hip.s")
+@pytest.mark.parametrize("source,kernel", [("gemv.hip", "gemv_q4_0_m1_kernelILb1E"),
+                                           ("gemv_kquant.hip", "gemv_q4_K_kernelILi1ELb1E")])
+def test_m1_gemv_copy_precedes_wait(source, kernel):
+    out = os.path.join(PKG_DIR, "_build", source + ".s")
     subprocess.run(["make", "-s", "-C", PKG_DIR, out], check=True, capture_output=True, timeout=600)
     with open(out) as f:
         asm = f.read()
-    lines = _kernel_lines(asm, "gemv_q4_0_m1_kernelILb1E")
-    check_copy_then_wait(lines)
+    check_copy_then_wait(_kernel_lines(asm, kernel))
