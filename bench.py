@@ -337,7 +337,7 @@ def main():
         prefill = gemm_item(torch, pkg, "c4: q4_0 x q8_0 GEMM M=2048 N=11008 K=4096", 0, 2048, 11008, 4096,
                             args.prefill_steps, 8, pkg.INPUT_REFERENCE, "gemm_q4_0_kernel", rows_to_verify=256)
 
-    gemv_kq = [gemv_item(torch, pkg, f"{name} x q8_K GEMV M=1 N=4096 K=4096, 32 rotating weight copies", qt, 1, 4096,
+    gemv_kq = [gemv_item(torch, pkg, f"m1_{name}: {name} x q8_K GEMV M=1 N=4096 K=4096, 32 rotating weight copies", qt, 1, 4096,
                          4096, args.steps // 4, args.warmup // 4, variant, f"gemv_{name}_kernel<1>")
                for qt, name, variant in ((1, "q4_K", pkg.INPUT_REFERENCE), (2, "iq2_xxs", pkg.INPUT_BASELINE))]
 

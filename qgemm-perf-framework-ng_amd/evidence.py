@@ -59,6 +59,11 @@ CONFIGS = {
                 "gemv_q4_K_staged_kernel", "hbm"),
     "m8_iq2_xxs": ("iq2_xxs x q8_K GEMV M=8 N=4096 K=4096, 32 rotating weight copies", 2, 8, 4096, 4096, 1,
                    "gemv_iq2_xxs_staged_kernel", "hbm"),
+    # the M = 1 GEMVs of the other two formats (bench.py's gemv_q4_K / gemv_iq2_xxs lines)
+    "m1_q4_K": ("q4_K x q8_K GEMV M=1 N=4096 K=4096, 32 rotating weight copies", 1, 1, 4096, 4096, 0,
+                "gemv_q4_K_kernel", "hbm"),
+    "m1_iq2_xxs": ("iq2_xxs x q8_K GEMV M=1 N=4096 K=4096, 32 rotating weight copies", 2, 1, 4096, 4096, 1,
+                   "gemv_iq2_xxs_kernel", "hbm"),
 }
 WB = {0: 18, 1: 144, 2: 66}
 AB = {0: 34, 1: 292, 2: 292}
