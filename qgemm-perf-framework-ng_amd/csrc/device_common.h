@@ -174,6 +174,15 @@ __device__ __forceinline__ i32x16 mfma_i8_32x32x32(i32x4 a, i32x4 b, i32x16 c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
+// D(16x16, int32) = A(16x32 int8) . B(16x32 int8)^T + C.
+// Operand lane l supplies row (l % 16) with the 8 bytes of K-quarter (l / 16);
+// A and B use the same K mapping, so any assignment of the 32 K positions to
+// (quarter, byte) that is the same on both sides yields the full dot product.
+// Result lane l, register r holds row 4*(l/16) + r, column l%16.
+__device__ __forceinline__ i32x4 mfma_i8_16x16x32(uint64_t a, uint64_t b, i32x4 c) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)a, (long)b, c, 0, 0, 0);
+}
+
 // D(32x32, fp32) = A(32x8 fp16) . B(32x8 fp16)^T + C, same result layout.
 __device__ __forceinline__ f32x16 mfma_f16_32x32x8(f16x4 a, f16x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x8f16(a, b, c, 0, 0, 0);

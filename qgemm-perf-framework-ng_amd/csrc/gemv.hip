@@ -1,5 +1,5 @@
-// q4_0 x q8_0 GEMV path (m <= 16) for gfx950: no MFMA, the weight stream is
-// the roofline. Four kernels, picked in launch_gemv / launch_fused_gemv:
+// q4_0 x q8_0 GEMV path (m <= 16) for gfx950: the weight stream is the
+// roofline. Five kernels, picked in launch_gemv / launch_fused_gemv:
 //
 //   gemv_q4_0_m1_kernel        m == 1: one wavefront per weight row, one q4_0
 //                              block pair (36 B) per lane, the activation row
@@ -15,6 +15,10 @@
 //                              bytes, then the 8 fp16 scales).
 //   gemv_q4_0_fused_kernel     pfng_hip_compute for m <= 2: quantizes the fp32
 //                              activation rows into LDS, then as the m1 kernel.
+//   gemv_q4_0_mfma_kernel      m = 9..16 (k % 4096 == 0; from m = 12 also
+//                              k % 2048 == 0): 16x16 int8 MFMA tiles of 16
+//                              weight rows, K split over the workgroup's waves,
+//                              each wave's slices copied into LDS by direct loads.
 //
 // Every lane issues all the loads of a step before any arithmetic, so the
 // weight stream of the grid is in flight at once; weight rows are clamped so
@@ -470,6 +474,120 @@ __global__ __launch_bounds__(kPairsThreads) void gemv_q4_0_pairs_kernel(const ui
     }
 }
 
+// m = 9..16 with k % 4096 == 0 (16 waves), m = 12..16 with k % 2048 == 0 (8
+// waves): 16x16 int8 MFMA tiles. A workgroup takes 16 weight rows (output
+// columns) and all m activation rows; its WV waves split K into equal slices
+// of a multiple of 8 blocks, and each wave copies just its own slice of the 16 weight
+// rows and of the m activation rows into its own LDS region with direct loads
+// (global_load_lds_dwordx4), waits for its own copies and needs no barrier
+// until the cross-wave sum at the end. Per block the wave reads its MFMA
+// operands from LDS: lane l takes weight row l % 16 (B) and activation row
+// l % 16 (A, clamped below m) with K positions 4q..4q+3 and 16+4q..16+4q+3,
+// q = l / 16 — one nibble dword as loaded gives both (low nibbles, then high),
+// and the activation's two dwords sit at the same byte offsets. The first
+// block of a pair sits two bytes into its dwords (realigned with
+// v_alignbyte), the second is dword-aligned. Per block and lane: one
+// v_mfma_i32_16x16x32_i8 (16 * S_b), four dw*da products (v_fma_mix), four
+// fp32 fma. The wave partial sums are added in wave order through LDS.
+// Against the pairs kernel this trades its 16 v_dot4 and 17-dword LDS read
+// per activation row and block pair for a few LDS reads and one MFMA per
+// block.
+__host__ __device__ constexpr int64_t mf_gemv_lds_bytes(int64_t m, int64_t nb) {
+    return nb * (16 * 18 + m * 34);  // the waves' slices: 16 weight rows, m activation rows
+}
+
+struct MfGemvGeom {
+    int cprw, cpra;         // 16-byte chunks per weight / activation row slice
+    uint32_t magw, maga;    // ceil(2^32 / cpr): chunk -> row by one v_mul_hi_u32
+};
+
+template <int M, int WV>
+__global__ __launch_bounds__(WV * 64) void gemv_q4_0_mfma_kernel(const uint8_t *__restrict__ w,
+                                                                       const uint8_t *__restrict__ a,
+                                                                       float *__restrict__ c, int n, int nb,
+                                                                       MfGemvGeom geo) {
+    static_assert(M >= 1 && M <= 16, "one 16-row tile of activation rows");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int n0 = blockIdx.x * 16;
+    const int bw = nb / WV;  // blocks per wave
+    const int kb0 = wave * bw;
+    const int rw = bw * 18, ra = bw * 34;  // slice bytes per row (multiples of 16: bw % 8 == 0)
+    uint8_t *ws = lds + (size_t)wave * (16 * rw + M * ra);
+    uint8_t *as = ws + 16 * rw;
+    // this wave's slices, 16 bytes per lane and load
+    const int nw = 16 * geo.cprw, na = M * geo.cpra;
+    for (int c0 = 0; c0 < nw; c0 += 64) {
+        const uint32_t ch = (uint32_t)(c0 + lane);
+        const int row = (int)__umulhi(ch, geo.magw);
+        const int col = (int)ch - row * geo.cprw;
+        if ((int)ch < nw && n0 + row < n)
+            __builtin_amdgcn_global_load_lds(w + ((size_t)(n0 + row) * nb + kb0) * 18 + col * 16,
+                                             (__attribute__((address_space(3))) void *)(ws + c0 * 16), 16, 0, 0);
+    }
+    for (int c0 = 0; c0 < na; c0 += 64) {
+        const uint32_t ch = (uint32_t)(c0 + lane);
+        const int row = (int)__umulhi(ch, geo.maga);
+        const int col = (int)ch - row * geo.cpra;
+        if ((int)ch < na)
+            __builtin_amdgcn_global_load_lds(a + ((size_t)row * nb + kb0) * 34 + col * 16,
+                                             (__attribute__((address_space(3))) void *)(as + c0 * 16), 16, 0, 0);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave reads only what it copied
+    const int li = lane & 15, q = lane >> 4;
+    const int arow = li < M ? li : M - 1;
+    const uint8_t *wl = ws + li * rw + 2 + 4 * q;          // + 18 j: block j's nibble dword q
+    const uint8_t *al = as + arow * ra + 2 + 4 * q;        // + 34 j: activation dwords q, q + 4
+    const uint8_t *dwp = ws + li * rw;                      // + 18 j: dw of weight row li
+    int orow[4];                                            // output rows of this lane's results
+#pragma unroll
+    for (int r = 0; r < 4; ++r) orow[r] = 4 * q + r < M ? 4 * q + r : M - 1;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto block = [&](int j, uint32_t wq, uint32_t x0, uint32_t x1) {
+        const uint64_t bop = (uint64_t)q4_0_lo16(wq) | ((uint64_t)q4_0_hi16(wq) << 32);
+        const uint64_t aop = (uint64_t)x0 | ((uint64_t)x1 << 32);
+        const i32x4 s16 = mfma_i8_16x16x32(aop, bop, (i32x4){0, 0, 0, 0});
+        const uint32_t dw = *reinterpret_cast<const uint16_t *>(dwp + j * 18);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t da = *reinterpret_cast<const uint16_t *>(as + orow[r] * ra + j * 34);
+            acc[r] = __builtin_fmaf((float)s16[r], fp16_product<false, false>(da, dw), acc[r]);
+        }
+    };
+    for (int j = 0; j < bw; j += 2) {
+        // block j: two bytes into its dwords; block j + 1: dword-aligned
+        const uint32_t *w0 = reinterpret_cast<const uint32_t *>(wl + j * 18 - 2);
+        const uint32_t *a0 = reinterpret_cast<const uint32_t *>(al + j * 34 - 2);
+        const uint32_t wq0 = shift2(w0[0], w0[1]);
+        const uint32_t x00 = shift2(a0[0], a0[1]), x01 = shift2(a0[4], a0[5]);
+        const uint32_t wq1 = *reinterpret_cast<const uint32_t *>(wl + (j + 1) * 18);
+        const uint32_t *a1 = reinterpret_cast<const uint32_t *>(al + (j + 1) * 34);
+        block(j, wq0, x00, x01);
+        block(j + 1, wq1, a1[0], a1[4]);
+    }
+    // wave partials through LDS, added in wave order by wave 0
+    __syncthreads();
+    float *red = reinterpret_cast<float *>(lds);
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[((wave - 1) * 4 + r) * 64 + lane] = acc[r];
+    }
+    __syncthreads();
+    if (wave == 0) {
+        for (int v = 1; v < WV; ++v) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] += red[((v - 1) * 4 + r) * 64 + lane];
+        }
+        const int col = n0 + li;
+        if (col < n) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (4 * q + r < M) c[(size_t)(4 * q + r) * n + col] = acc[r] * 0.0625f;
+        }
+    }
+}
+
 // Fused activation quantization + GEMV (m <= 2): each workgroup quantizes the
 // m fp32 activation rows into q8_0 blocks in LDS (the same arithmetic as
 // quantize_q8_0_kernel, so the bytes equal the standalone quantizer's), then
@@ -579,9 +697,40 @@ hipError_t launch_fused_m(const void *w, const float *x, float *c, int64_t n, in
     return hipGetLastError();
 }
 
+// Waves of the MFMA tile kernel for m activation rows and k, 0 where the
+// pairs kernel runs instead: 16 waves of 8-block slices (k % 4096 == 0) from
+// m = 9, where they measured faster than the pairs kernel (4096 x 4096, µs:
+// m = 8 5.93 against 5.98, m = 10 6.15 / 6.95, m = 12 6.11 / 7.86, m = 16
+// 6.21 / 9.54); 8 waves of 8-block slices (k % 2048 == 0) from m = 12 (m = 12
+// 7.14 / 7.86, m = 10 7.18 / 6.95). Both while the slices fit the LDS.
+int mf_gemv_waves(int64_t m, int64_t k) {
+    if (m > 16 || mf_gemv_lds_bytes(m, k / 32) > kPairsMaxLds) return 0;
+    if (m >= 9 && k % 4096 == 0) return 16;
+    if (m >= 12 && k % 2048 == 0) return 8;
+    return 0;
+}
+
 template <int M>
 hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n, int64_t k, hipStream_t stream) {
     const int nb = (int)(k / 32);
+    if (const int wv = mf_gemv_waves(M, k)) {
+        const int bw = nb / wv;  // blocks per wave, a multiple of 8
+        MfGemvGeom geo;
+        geo.cprw = bw * 18 / 16;
+        geo.cpra = bw * 34 / 16;
+        geo.magw = (uint32_t)((((uint64_t)1 << 32) + geo.cprw - 1) / geo.cprw);
+        geo.maga = (uint32_t)((((uint64_t)1 << 32) + geo.cpra - 1) / geo.cpra);
+        const dim3 grid((unsigned)((n + 15) / 16));
+        const size_t lds = (size_t)mf_gemv_lds_bytes(M, nb);
+        const uint8_t *wp = static_cast<const uint8_t *>(w), *ap = static_cast<const uint8_t *>(a);
+        if (wv == 16)
+            hipLaunchKernelGGL((gemv_q4_0_mfma_kernel<M, 16>), grid, dim3(16 * 64), lds, stream, wp, ap, c, (int)n, nb,
+                               geo);
+        else
+            hipLaunchKernelGGL((gemv_q4_0_mfma_kernel<M, 8>), grid, dim3(8 * 64), lds, stream, wp, ap, c, (int)n, nb,
+                               geo);
+        return hipGetLastError();
+    }
     if (k % 64 == 0 && pairs_lds_bytes(M, nb) <= kPairsMaxLds) {
         const int grid = (int)((n + kPairsThreads / 64 - 1) / (kPairsThreads / 64));
         hipLaunchKernelGGL(gemv_q4_0_pairs_kernel<M>, dim3(grid), dim3(kPairsThreads), (size_t)pairs_lds_bytes(M, nb),
