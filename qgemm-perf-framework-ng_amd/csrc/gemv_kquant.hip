@@ -1,13 +1,14 @@
 // GEMV path (m <= 16) for the super-block formats against q8_K activations:
 // q4_K (llama_reference.cpp:113-132) and iq2_xxs (llama_reference.cpp:148-161,
-// kernels/common/iq2_xxs.h:29-41). No MFMA: one wavefront per weight row,
-// the weight stream read with aligned 16-byte (q4_K) or realigned dword
-// (iq2_xxs, 66-byte blocks) loads, all loads of a step issued before any
-// arithmetic, int8 dots with v_dot4_i32_i8. gemv_q4_K_kernel and
-// gemv_iq2_xxs_kernel (m <= 8) take m == 1 and rows too long to stage; for
-// q4_K at m == 1 the 16-row workgroups copy the activation row into LDS first.
-// The *_staged_kernel variants (m = 2..16) stage the rows in LDS once per
-// 16-row workgroup.
+// kernels/common/iq2_xxs.h:29-41). One wavefront per weight row, the weight
+// stream read with aligned 16-byte (q4_K) or realigned dword (iq2_xxs,
+// 66-byte blocks) loads, all loads of a step issued before any arithmetic,
+// int8 dots with v_dot4_i32_i8. gemv_q4_K_kernel and gemv_iq2_xxs_kernel
+// (m <= 8) take m == 1 and rows too long to stage; for q4_K at m == 1 the
+// 16-row workgroups copy the activation row into LDS first. The
+// *_staged_kernel variants (m = 2..16) stage the rows in LDS once per 16-row
+// workgroup. q4_K from m = 9 at k % 4096 == 0 runs gemv_q4_K_mfma_kernel
+// instead: 16x16 int8 MFMA tiles of 16 weight rows, K split over 16 waves.
 //
 // q4_K: four lanes per super-block, lane e owning sub-blocks 2e and 2e+1 (the
 // 32 nibble bytes qs[32e .. 32e+32): low nibbles of sub-block 2e, high of
@@ -670,12 +671,157 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(con
     }
 }
 
+// q4_K, m = 9..16 with k % 4096 == 0: 16x16 int8 MFMA tiles, as
+// gemv_q4_0_mfma_kernel. A workgroup takes 16 weight rows; each of its 16
+// waves takes nsb / 16 super-blocks of the 16 weight rows and the m
+// activation rows, copies them into its own LDS region with direct loads
+// (16 bytes per lane for the weights; 4 for the activations, whose 292-byte
+// blocks are only dword-aligned) and waits for its own copies. Per 32-element
+// sub-block j: one v_mfma_i32_16x16x32_i8 of the unsigned nibbles (q4_K has
+// no offset) with the activation bytes (lane l: K positions 4q..4q+3 and
+// 16+4q..16+4q+3, q = l / 16) gives S_j, and IS += sc_j * S_j for the lane's
+// four results (24-bit multiplies; sc_j of the lane's weight row). Per
+// super-block: IM = sum_j m_j * (bsums[2j] + bsums[2j+1]) with one
+// v_dot2_i32_i16 per sub-block, and acc += d_a * (d * IS - dmin * IM) as the
+// reference forms it (llama_reference.cpp:107-131). The wave partials are
+// added in wave order at the end.
+constexpr int kKqMfWaves = 16;
+
+__host__ __device__ constexpr int64_t kq_mf_region(int64_t m, int64_t s) {
+    return 16 * 144 * s + (m * 292 * s + 15) / 16 * 16;  // one wave: weight rows, then activation rows
+}
+__host__ __device__ constexpr int64_t kq_mf_lds_bytes(int64_t m, int64_t nsb) {
+    return kKqMfWaves * kq_mf_region(m, nsb / kKqMfWaves);
+}
+
+struct KqMfGeom {
+    int cprw, cpra;       // 16-byte chunks per weight row slice, dwords per activation row slice
+    uint32_t magw, maga;  // ceil(2^32 / cpr): index -> row by one v_mul_hi_u32
+};
+
+template <int M>
+__global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_kernel(const uint8_t *__restrict__ w,
+                                                                         const uint8_t *__restrict__ a,
+                                                                         float *__restrict__ c, int n, int nsb,
+                                                                         KqMfGeom geo) {
+    static_assert(M >= 1 && M <= 16, "one 16-row tile of activation rows");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int n0 = blockIdx.x * 16;
+    const int s = nsb / kKqMfWaves;  // super-blocks per wave
+    const int sb0 = wave * s;
+    const int rw = s * 144, ra = s * 292;
+    uint8_t *ws = lds + (size_t)wave * kq_mf_region(M, s);
+    uint8_t *as = ws + 16 * rw;
+    const int nw = 16 * geo.cprw, na = M * geo.cpra;
+    for (int c0 = 0; c0 < nw; c0 += 64) {
+        const uint32_t ch = (uint32_t)(c0 + lane);
+        const int row = (int)__umulhi(ch, geo.magw);
+        const int col = (int)ch - row * geo.cprw;
+        if ((int)ch < nw && n0 + row < n)
+            __builtin_amdgcn_global_load_lds(w + ((size_t)(n0 + row) * nsb + sb0) * 144 + col * 16,
+                                             (__attribute__((address_space(3))) void *)(ws + c0 * 16), 16, 0, 0);
+    }
+    for (int c0 = 0; c0 < na; c0 += 64) {
+        const uint32_t ch = (uint32_t)(c0 + lane);
+        const int row = (int)__umulhi(ch, geo.maga);
+        const int col = (int)ch - row * geo.cpra;
+        if ((int)ch < na)
+            __builtin_amdgcn_global_load_lds(a + ((size_t)row * nsb + sb0) * kQ8KBytes + col * 4,
+                                             (__attribute__((address_space(3))) void *)(as + c0 * 4), 4, 0, 0);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave reads only what it copied
+    const int li = lane & 15, q = lane >> 4;
+    const int arow = li < M ? li : M - 1;
+    int orow[4];  // activation rows of this lane's four results (clamped)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) orow[r] = 4 * q + r < M ? 4 * q + r : M - 1;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t = 0; t < s; ++t) {
+        const uint8_t *wb = ws + li * rw + t * 144;  // weight row li, super-block t
+        const uint4 hd = *reinterpret_cast<const uint4 *>(wb);
+        // scales (bytes 0..3: sub-blocks 0..3, 4..7: 4..7) and mins, as q4_K_scale_min_pair
+        const uint32_t scw[2] = {hd.y & 0x3f3f3f3fu, (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u)};
+        const uint32_t mnw[2] = {hd.z & 0x3f3f3f3fu, ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u)};
+        const uint8_t *ab = as + arow * ra + t * kQ8KBytes + 4 + 4 * q;
+        int is[4] = {0, 0, 0, 0}, im[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            // sub-block j: nibbles of bytes 32 (j / 2) + {4q.., 16 + 4q..}, low for even j
+            const uint32_t x0 = *reinterpret_cast<const uint32_t *>(wb + 16 + 32 * (j / 2) + 4 * q);
+            const uint32_t x1 = *reinterpret_cast<const uint32_t *>(wb + 32 + 32 * (j / 2) + 4 * q);
+            const uint32_t w0 = (j & 1 ? x0 >> 4 : x0) & 0x0f0f0f0fu;
+            const uint32_t w1 = (j & 1 ? x1 >> 4 : x1) & 0x0f0f0f0fu;
+            const uint32_t y0 = *reinterpret_cast<const uint32_t *>(ab + 32 * j);
+            const uint32_t y1 = *reinterpret_cast<const uint32_t *>(ab + 32 * j + 16);
+            const i32x4 sj = mfma_i8_16x16x32((uint64_t)y0 | ((uint64_t)y1 << 32), (uint64_t)w0 | ((uint64_t)w1 << 32),
+                                              (i32x4){0, 0, 0, 0});
+            const int sc = (int)((scw[j / 4] >> (8 * (j % 4))) & 0xffu);
+            const int mn = (int)((mnw[j / 4] >> (8 * (j % 4))) & 0xffu);
+            typedef short s16x2 __attribute__((ext_vector_type(2)));
+            const s16x2 mm = {(short)mn, (short)mn};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                is[r] += __mul24(sc, sj[r]);
+                const uint32_t bs = *reinterpret_cast<const uint32_t *>(as + orow[r] * ra + t * kQ8KBytes + 260 + 4 * j);
+                im[r] = __builtin_amdgcn_sdot2(__builtin_bit_cast(s16x2, bs), mm, im[r], false);
+            }
+        }
+        const float d = fp16_to_f32(hd.x & 0xffffu), dmin = fp16_to_f32(hd.x >> 16);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float ad = *reinterpret_cast<const float *>(as + orow[r] * ra + t * kQ8KBytes);
+            acc[r] += ad * fmaf(-dmin, (float)im[r], d * (float)is[r]);
+        }
+    }
+    __syncthreads();
+    float *red = reinterpret_cast<float *>(lds);
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[((wave - 1) * 4 + r) * 64 + lane] = acc[r];
+    }
+    __syncthreads();
+    if (wave == 0) {
+        for (int v = 1; v < kKqMfWaves; ++v) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] += red[((v - 1) * 4 + r) * 64 + lane];
+        }
+        const int col = n0 + li;
+        if (col < n) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (4 * q + r < M) c[(size_t)(4 * q + r) * n + col] = acc[r];
+        }
+    }
+}
+
+// the q4_K MFMA tile kernel runs from m = 9 at k % 4096 == 0 while its slices fit the LDS
+bool kq_mf_fits(int64_t m, int64_t k) {
+    return m >= 9 && m <= 16 && k % 4096 == 0 && kq_mf_lds_bytes(m, k / 256) <= 160 * 1024;
+}
+
 template <int M>
 hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int64_t n, int64_t k,
                           hipStream_t stream) {
     const auto *wp = static_cast<const uint8_t *>(w);
     const auto *ap = static_cast<const uint8_t *>(a);
     const int64_t nsb = k / 256;
+    if constexpr (M >= 9) {
+        // measured at 4096 x 4096 against the staged kernel (µs): m = 9 6.57 / 6.96,
+        // m = 12 6.92 / 7.97, m = 16 7.59 / 9.22; m = 8 ties (6.19 / 6.17)
+        if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K && kq_mf_fits(M, k)) {
+            const int sw = (int)(nsb / kKqMfWaves);
+            KqMfGeom geo;
+            geo.cprw = sw * 144 / 16;
+            geo.cpra = sw * kQ8KBytes / 4;
+            geo.magw = (uint32_t)((((uint64_t)1 << 32) + geo.cprw - 1) / geo.cprw);
+            geo.maga = (uint32_t)((((uint64_t)1 << 32) + geo.cpra - 1) / geo.cpra);
+            hipLaunchKernelGGL(gemv_q4_K_mfma_kernel<M>, dim3((unsigned)((n + 15) / 16)), dim3(kKqMfWaves * 64),
+                               (size_t)kq_mf_lds_bytes(M, nsb), stream, wp, ap, c, (int)n, (int)nsb, geo);
+            return hipGetLastError();
+        }
+    }
     if constexpr (M >= 2) {
         if (kq_staged_lds_bytes(M, nsb) <= 160 * 1024) {
             const dim3 sgrid((unsigned)((n + kStagedThreads / 64 - 1) / (kStagedThreads / 64)));
