@@ -426,7 +426,8 @@ def test_mfma_in_graph_replays(hip, torch_gpu, oracle):
 
 @pytest.mark.parametrize("qtype", [1, 2])
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 13, 16])
-@pytest.mark.parametrize("n,k", [(4096, 4096), (257, 1536), (64, 256), (33, 8192), (20, 20480), (8, 65536)])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (257, 1536), (64, 256), (33, 8192), (20, 20480), (8, 65536),
+                                 (37, 4096)])
 def test_gemv_kquant(hip, torch_gpu, oracle, qtype, m, n, k):
     """m = 1: q4_K copies the activation row into LDS while it fits 64 KB
     (k <= 57344; k = 65536 takes the global-read kernel), iq2_xxs reads it from
