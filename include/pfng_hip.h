@@ -45,13 +45,17 @@ typedef enum {
  * where it applies, up to m = 16; then the MFMA tiles). */
 typedef enum {
     PFNG_PATH_AUTO = 0,
-    PFNG_PATH_GEMV = 1,  /* wavefront-per-row GEMV, no MFMA: q4_0 for m <= 16
-                            with k % 64 == 0 for m == 1; for m = 2..16 when the
-                            LDS-staged activations fit, k % 64 == 0 and
-                            m * (k / 64) * 76 + 16 <= 163840, and for m = 2..8
-                            also every k % 256 == 0; q4_K and iq2_xxs with
-                            k % 256 == 0 for m <= 8, and for m = 9..16 while
-                            m * (k / 256) * 320 + 3072 <= 163840 */
+    PFNG_PATH_GEMV = 1,  /* the decode-batch kernels (wavefront-per-row GEMVs;
+                            from m = 9 16x16 int8-MFMA tiles with K split over
+                            the waves, for q4_0 at k % 4096 == 0 or, from
+                            m = 12, k % 2048 == 0, q4_K at k % 4096 == 0 and
+                            iq2_xxs at k == 4096, while their slices fit LDS):
+                            q4_0 for m <= 16 with k % 64 == 0 for m == 1; for
+                            m = 2..16 when the LDS-staged activations fit,
+                            k % 64 == 0 and m * (k / 64) * 76 + 16 <= 163840,
+                            and for m = 2..8 also every k % 256 == 0; q4_K and
+                            iq2_xxs with k % 256 == 0 for m <= 8, and for
+                            m = 9..16 while m * (k / 256) * 320 + 3072 <= 163840 */
     PFNG_PATH_MFMA = 2,  /* int8-MFMA GEMM, LDS-staged tiles: q4_0 with k % 128 == 0,
                             q4_K and iq2_xxs for every k % 256 == 0 */
     PFNG_PATH_NAIVE = 3  /* one thread per output, the reference's exact fp32 order */
