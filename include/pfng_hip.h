@@ -42,7 +42,8 @@ typedef enum {
 } pfng_status;
 
 /* Matrix-product implementations; PFNG_PATH_AUTO picks per shape (the GEMV
- * where it applies, up to m = 16; then the MFMA tiles). */
+ * where it applies, up to m = 16; then the MFMA tiles) and returns
+ * PFNG_ERR_UNSUPPORTED when neither applies (see pfng_hip_auto_path). */
 typedef enum {
     PFNG_PATH_AUTO = 0,
     PFNG_PATH_GEMV = 1,  /* the decode-batch kernels (wavefront-per-row GEMVs;
@@ -98,6 +99,16 @@ int pfng_hip_mul_mat_q4_K_q8_K(const void *weight, const void *act_q8_K, float *
  * with the full 256-entry IQ2_XXS grid. */
 int pfng_hip_mul_mat_iq2_xxs_q8_K(const void *weight, const void *act_q8_K, float *out, int64_t m, int64_t n,
                                   int64_t k, int path, void *stream);
+
+/* The path PFNG_PATH_AUTO takes for this shape with 16-byte-aligned weights
+ * and activations and a 4-byte-aligned C: PFNG_PATH_GEMV or PFNG_PATH_MFMA;
+ * PFNG_PATH_AUTO for an empty product (m == 0 or n == 0); -1 (with a message
+ * in pfng_hip_last_error()) when the shape is invalid or no tiled path takes
+ * it, in which case PFNG_PATH_AUTO returns PFNG_ERR_UNSUPPORTED and only
+ * PFNG_PATH_NAIVE runs it. The counterpart of an adapter's validate()
+ * (kernels/common/adapter_common.h:28-43) for the automatic path. Host-only:
+ * touches no device. */
+int pfng_hip_auto_path(int type, int64_t m, int64_t n, int64_t k);
 
 /* Type-dispatched form; type is a pfng_quantization_type. */
 int pfng_hip_mul_mat(int type, const void *weight, const void *act_q, float *out, int64_t m, int64_t n, int64_t k,

@@ -44,6 +44,17 @@ int pfng_host_create_input(int type, int variant, uint32_t seed, size_t m, size_
  * 2 has no quantizer in the reference). */
 int pfng_host_quantize_weights(int type, const float *x, void *y, size_t rows, size_t k);
 
+/* Replaces llama_reference::compute (bench/llama_reference/llama_reference.h:18,
+ * llama_reference.cpp:165-215) on the host, as the harness's verification uses
+ * it (bench/framework/benchmark.cpp:140): quantizes the m x k fp32 activations
+ * (quantize_row_q8_0 / q8_K) and evaluates every output with the reference's
+ * scalar dot in its fp32 order (iq2_xxs with the full 256-entry grid), over
+ * `threads` host threads split by output row (the result does not depend on
+ * the thread count). out: m x n fp32, row-major. Returns 0, -1 (bad k), -2
+ * (unknown type) or -3 (out of memory). */
+int pfng_host_compute(int type, const float *activation, const void *weight, float *out, size_t m, size_t n, size_t k,
+                      size_t threads);
+
 /* ggml_compute_fp32_to_fp16 / ggml_compute_fp16_to_fp32 (include/ggml.h:83-117). */
 uint16_t pfng_host_fp32_to_fp16(float value);
 float pfng_host_fp16_to_fp32(uint16_t value);

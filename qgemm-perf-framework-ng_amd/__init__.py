@@ -62,12 +62,14 @@ def lib() -> ctypes.CDLL:
         for name in ("pfng_hip_mul_mat_q4_0_q8_0", "pfng_hip_mul_mat_q4_K_q8_K", "pfng_hip_mul_mat_iq2_xxs_q8_K"):
             getattr(L, name).argtypes = [vp, vp, vp, i64, i64, i64, ci, vp]
         L.pfng_hip_mul_mat.argtypes = [ci, vp, vp, vp, i64, i64, i64, ci, vp]
+        L.pfng_hip_auto_path.argtypes = [ci, i64, i64, i64]
         L.pfng_hip_compute_workspace_size.restype = sz
         L.pfng_hip_compute_workspace_size.argtypes = [ci, i64, i64]
         L.pfng_hip_compute.argtypes = [ci, vp, vp, vp, i64, i64, i64, vp, sz, ci, vp]
         L.pfng_hip_block_isums.argtypes = [ci, vp, vp, vp, i64, i64, i64, vp]
         L.pfng_host_create_input.argtypes = [ci, ci, ctypes.c_uint32, sz, sz, sz, vp, vp]
         L.pfng_host_quantize_weights.argtypes = [ci, vp, vp, sz, sz]
+        L.pfng_host_compute.argtypes = [ci, vp, vp, vp, sz, sz, sz, sz]
         L.pfng_host_fp32_to_fp16.restype = ctypes.c_uint16
         L.pfng_host_fp32_to_fp16.argtypes = [ctypes.c_float]
         L.pfng_host_fp16_to_fp32.restype = ctypes.c_float
@@ -83,12 +85,13 @@ EXPORTED_SYMBOLS = (
     "pfng_hip_last_error", "pfng_hip_version", "pfng_hip_device_check",
     "pfng_hip_quantize_q8_0", "pfng_hip_quantize_q8_K", "pfng_hip_quantize_q4_0", "pfng_hip_quantize_q4_K",
     "pfng_hip_mul_mat_q4_0_q8_0", "pfng_hip_mul_mat_q4_K_q8_K", "pfng_hip_mul_mat_iq2_xxs_q8_K",
-    "pfng_hip_mul_mat", "pfng_hip_compute_workspace_size", "pfng_hip_compute", "pfng_hip_block_isums",
+    "pfng_hip_mul_mat", "pfng_hip_auto_path", "pfng_hip_compute_workspace_size", "pfng_hip_compute",
+    "pfng_hip_block_isums",
 )
 # host-side C-ABI declared in include/pfng_host.h
 HOST_SYMBOLS = (
-    "pfng_host_create_input", "pfng_host_quantize_weights", "pfng_host_fp32_to_fp16", "pfng_host_fp16_to_fp32",
-    "pfng_host_checksum",
+    "pfng_host_create_input", "pfng_host_quantize_weights", "pfng_host_compute", "pfng_host_fp32_to_fp16",
+    "pfng_host_fp16_to_fp32", "pfng_host_checksum",
 )
 INPUT_REFERENCE, INPUT_BASELINE = 0, 1
 
@@ -140,6 +143,22 @@ def quantize_weights(qtype: int, x):
     if rc != 0:
         raise ValueError(f"pfng_host_quantize_weights({TYPE_NAMES.get(qtype, qtype)}, k={k}) failed: {rc}")
     return y
+
+
+def host_compute(qtype: int, activation, weight, n: int, threads: int = 1):
+    """llama_reference::compute on the host (the harness's verification
+    reference): float32 (m, k) activations and uint8 weight blocks -> float32 (m, n)."""
+    import numpy as np
+    act = np.ascontiguousarray(activation, dtype=np.float32)
+    w = np.ascontiguousarray(weight, dtype=np.uint8)
+    m, k = act.shape
+    out = np.empty((m, n), np.float32)
+    if qtype in QK and k % QK[qtype] == 0 and w.nbytes < n * (k // QK[qtype]) * WEIGHT_BLOCK_BYTES[qtype]:
+        raise ValueError("weight buffer is smaller than n rows of k/QK blocks")
+    rc = lib().pfng_host_compute(qtype, act.ctypes.data, w.ctypes.data, out.ctypes.data, m, n, k, threads)
+    if rc != 0:
+        raise ValueError(f"pfng_host_compute({TYPE_NAMES.get(qtype, qtype)}, m={m}, n={n}, k={k}) failed: {rc}")
+    return out
 
 
 def checksum(out) -> float:
@@ -238,6 +257,13 @@ def mul_mat(qtype: int, weight, act_q, m: int, n: int, k: int, path: int = PATH_
         _need(out, m * n * 4, "out")
     check(lib().pfng_hip_mul_mat(qtype, _p(weight), _p(act_q), _p(out), m, n, k, path, _stream(stream)))
     return out
+
+
+def auto_path(qtype: int, m: int, n: int, k: int) -> int:
+    """The path PATH_AUTO takes for this shape (aligned operands): PATH_GEMV or
+    PATH_MFMA, PATH_AUTO for an empty product, or -1 when PATH_AUTO declines it
+    (only PATH_NAIVE runs such a shape). Touches no device."""
+    return lib().pfng_hip_auto_path(qtype, m, n, k)
 
 
 def compute(qtype: int, activation, weight, n: int, path: int = PATH_AUTO, out=None, workspace=None, stream=None):

@@ -151,10 +151,19 @@ int pfng_hip_mul_mat(int type, const void *weight, const void *act_q, float *out
     switch (path) {
     case PFNG_PATH_AUTO:
         // measured at 4096x4096: every GEMV that applies (up to m = 16) is
-        // faster than the MFMA tiles
+        // faster than the MFMA tiles. When neither tiled path takes the shape
+        // the call is declined (as the reference's validate_shape declines,
+        // kernels/common/adapter_common.h:28-43) instead of dropping to the
+        // one-thread-per-output kernel, which is 10-500x slower; the caller
+        // may ask for PFNG_PATH_NAIVE explicitly.
         if (gemv_ok) return hip_status(pfng::launch_gemv(type, weight, act_q, out, m, n, k, s), "gemv launch");
         if (mfma_ok) return launch_mfma(type, weight, act_q, out, m, n, k, s);
-        return hip_status(pfng::launch_naive_mul_mat(type, weight, act_q, out, m, n, k, s), "naive launch");
+        return fail(PFNG_ERR_UNSUPPORTED,
+                    "%s: no tiled path takes m=%lld k=%lld with these operand alignments (%s); "
+                    "PFNG_PATH_NAIVE runs every shape in the reference's fp32 order",
+                    type_name(type), (long long)m, (long long)k,
+                    base_aligned ? "q4_0 needs k%%64==0 for m<=16 and k%%128==0 above"
+                                 : "weights and activations must be 16-byte and C 4-byte aligned");
     case PFNG_PATH_GEMV:
         if (!gemv_ok) return fail(PFNG_ERR_UNSUPPORTED, "%s GEMV path needs m<=16 (q4_0: k%%64==0 for m==1, else k%%64==0 with m*(k/64)*76+16<=163840, or k%%256==0 for m<=8; q4_K/iq2_xxs: k%%256==0, for m>8 also m*(k/256)*320+3072<=163840) and 16-byte aligned operands (m=%lld k=%lld)", type_name(type), (long long)m, (long long)k);
         return hip_status(pfng::launch_gemv(type, weight, act_q, out, m, n, k, s), "gemv launch");
@@ -165,6 +174,18 @@ int pfng_hip_mul_mat(int type, const void *weight, const void *act_q, float *out
         return hip_status(pfng::launch_naive_mul_mat(type, weight, act_q, out, m, n, k, s), "naive launch");
     default: return fail(PFNG_ERR_INVALID_ARGUMENT, "unknown path %d", path);
     }
+}
+
+int pfng_hip_auto_path(int type, int64_t m, int64_t n, int64_t k) {
+    if (check_shape(type, m, n, k)) return -1;
+    if (m == 0 || n == 0) return PFNG_PATH_AUTO;
+    if (pfng::gemv_supported(type, m, k)) return PFNG_PATH_GEMV;
+    if (pfng::mfma_supported(type, m, k)) return PFNG_PATH_MFMA;
+    fail(PFNG_ERR_UNSUPPORTED,
+         "%s: no tiled path takes m=%lld k=%lld (q4_0 needs k%%64==0 for m<=16 and k%%128==0 above); "
+         "PFNG_PATH_NAIVE runs every shape in the reference's fp32 order",
+         type_name(type), (long long)m, (long long)k);
+    return -1;
 }
 
 int pfng_hip_mul_mat_q4_0_q8_0(const void *weight, const void *act_q8_0, float *out, int64_t m, int64_t n, int64_t k,
@@ -203,6 +224,8 @@ int pfng_hip_compute(int type, const float *activation, const void *weight, floa
         return hip_status(pfng::launch_fused_gemv(type, weight, activation, out, m, n, k,
                                                   static_cast<hipStream_t>(stream)),
                           "fused gemv launch");
+    // decline before quantizing when the product would be declined
+    if (path == PFNG_PATH_AUTO && pfng_hip_auto_path(type, m, n, k) < 0) return PFNG_ERR_UNSUPPORTED;
     rc = type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0 ? pfng_hip_quantize_q8_0(activation, workspace, m, k, stream)
                                                   : pfng_hip_quantize_q8_K(activation, workspace, m, k, stream);
     if (rc) return rc;

@@ -1,7 +1,8 @@
-// Benchmark driver of the MI355X harness: the operator surface of
-// bench/framework/benchmark.h (owned inputs :8-37, result :46-66,
-// create_input/run_benchmark :68-70), timed in seconds around the adapters'
-// synchronizing run() instead of host cycle counters.
+// Benchmark driver of the standalone runner (pfng_bench): owned inputs, the
+// result record and the two entry points of bench/framework/benchmark.h
+// (:8-37, :46-66, :68-70), timed in seconds around the adapters' synchronizing
+// run() instead of host cycle counters. The reference harness itself runs the
+// same kernels through reference_overlay/ (per-host-cycle peaks).
 #pragma once
 
 #include <variant>
@@ -52,21 +53,21 @@ struct BenchmarkResult {
     double error_element_ratio = 0.0;
 };
 
-// benchmark.cpp:29-94 for request.seed, request.m/n/k and request.input_variant.
-// Throws std::runtime_error on an invalid shape.
+// Synthetic input for request.seed, request.m/n/k and request.input_variant,
+// as the reference harness makes it (benchmark.cpp:29-94). Throws
+// std::runtime_error on an invalid shape.
 OwnedBenchmarkInput create_input(QuantizationType type, const BenchmarkRequest &request);
 
-// benchmark.cpp:106-277: validate -> prepare -> (verify) -> warm-up ->
-// calibrate -> samples. The verification reference is the device's naive
-// path, which evaluates llama_reference::compute's scalar dot products in
-// their exact fp32 order (bit-identical output); an element fails when both its
-// absolute and its relative error exceed 1e-3 (benchmark.cpp:144-156).
+// validate -> prepare -> verify -> warm-up -> calibrate -> samples, the phases
+// of the reference's run_benchmark (benchmark.cpp:106-277). The expected output
+// of the verification is llama_reference::compute evaluated on the host
+// (pfng_host_compute); an element fails when both its absolute and its
+// relative error exceed 1e-3 (benchmark.cpp:144-156) or it is not finite.
 BenchmarkResult run_benchmark(const KernelRegistration &kernel, const BenchmarkRequest &request,
                               const BenchmarkInput &input);
 
-// llama_reference::compute for one input, evaluated on the device by the
-// naive path. Returns false and sets `error` on a HIP failure.
-bool reference_output(QuantizationType type, const BenchmarkInput &input, std::vector<float> &out,
-                      std::string &error);
+// llama_reference::compute for one input on the host; `out` is left empty when
+// the input cannot be evaluated.
+void expected_output(QuantizationType type, const BenchmarkInput &input, std::vector<float> &out);
 
 }  // namespace pfng::bench

@@ -171,10 +171,14 @@ template <QuantizationType T, int Path>
 ValidationResult validate(const BenchmarkRequest &r) {
     ValidationResult v = validate_base(T, r);
     if (!v.supported) return v;
+    const int auto_path = pfng_hip_auto_path((int)T, (int64_t)r.m, (int64_t)r.n, (int64_t)r.k);
+    if constexpr (Path == PFNG_PATH_AUTO) {
+        // the automatic path declines shapes no tiled kernel takes
+        if (auto_path < 0) return {false, pfng_hip_last_error()};
+    }
     if constexpr (Path == PFNG_PATH_GEMV) {
-        if (r.m > 8) return {false, "the GEMV path takes M <= 8"};
-        if (T == QuantizationType::WeightQ4_0ActivationQ8_0 && (r.m == 1 ? r.k % 64 : r.k % 256))
-            return {false, "the q4_0 GEMV path needs K % 64 == 0 (M = 1) or K % 256 == 0"};
+        // the automatic path prefers the GEMV wherever one applies
+        if (auto_path != PFNG_PATH_GEMV) return {false, "no GEMV kernel takes this shape (M <= 16 and K limits)"};
     }
     if constexpr (Path == PFNG_PATH_MFMA && T == QuantizationType::WeightQ4_0ActivationQ8_0) {
         if (r.k % 128) return {false, "the q4_0 MFMA path needs K % 128 == 0"};

@@ -1,0 +1,28 @@
+// iq2_xxs-q8_K-HIP-mi355x: dot_iq2_xxs_q8_K (bench/llama_reference/llama_reference.cpp:148-161) over every (m, n) on one MI355X, through the
+// backend's automatic path (pfng_hip_mul_mat with PFNG_PATH_AUTO). The
+// callbacks are shared by the three HIP kernel IDs (hip_adapter.h).
+#include "adapter_common.h"
+#include "hip_adapter.h"
+
+namespace pfng::bench::adapters {
+namespace {
+
+constexpr QuantizationType kPair = QuantizationType::WeightIQ2_XXSActivationQ8_K;
+
+ValidationResult validate(const BenchmarkRequest &request) { return hip_mi355x::validate(kPair, request); }
+
+PrepareResult prepare(const BenchmarkRequest &request, const BenchmarkInput &input) {
+    return hip_mi355x::prepare(kPair, request, input);
+}
+
+}  // namespace
+
+void register_iq2_xxs_hip_mi355x() {
+    register_kernel({"iq2_xxs-q8_K-HIP-mi355x",
+                     "IQ2_XXS/Q8_K HIP gfx950 (wave-per-row GEMV for M<=16, int8 MFMA tiles above)",
+                     kPair,
+                     {hip_mi355x::peak_i8_mac, validate, prepare, hip_mi355x::reset, hip_mi355x::run,
+                      hip_mi355x::export_output, hip_mi355x::checksum, hip_mi355x::destroy}});
+}
+
+}  // namespace pfng::bench::adapters

@@ -63,6 +63,13 @@ def test_version_string(pkg):
     (lambda L: L.pfng_hip_mul_mat(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 17, 4, 256, 1, None), 2),
     (lambda L: L.pfng_hip_mul_mat(1, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 17, 4, 256, 1, None), 2),
     (lambda L: L.pfng_hip_mul_mat(2, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 9, 4, 20480, 1, None), 2),
+    # the automatic path declines what no tiled path takes instead of falling
+    # back to the one-thread-per-output kernel
+    (lambda L: L.pfng_hip_mul_mat(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 17, 4, 96, 0, None), 2),
+    (lambda L: L.pfng_hip_mul_mat(0, ctypes.c_void_p(258), ctypes.c_void_p(256), ctypes.c_void_p(256), 1, 4, 64, 0, None), 2),
+    (lambda L: L.pfng_hip_mul_mat(1, ctypes.c_void_p(256), ctypes.c_void_p(264), ctypes.c_void_p(256), 64, 4, 256, 0, None), 2),
+    (lambda L: L.pfng_hip_compute(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 3, 5, 96,
+                                  ctypes.c_void_p(256), 3 * 3 * 34, 0, None), 2),
     (lambda L: L.pfng_hip_compute(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 4, 4, 64, None, 10, 0, None), 1),
     (lambda L: L.pfng_hip_block_isums(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 4, 4, 96, None), 2),
 ])
@@ -70,6 +77,19 @@ def test_argument_validation(pkg, call, expect):
     L = pkg.lib()
     assert call(L) == expect
     if expect:
+        assert pkg.last_error()
+
+
+@pytest.mark.parametrize("qtype,m,n,k,expect", [
+    (0, 1, 4096, 4096, 1), (0, 16, 4096, 4096, 1), (0, 17, 4096, 4096, 2), (0, 480, 1536, 1536, 2),
+    (0, 3, 5, 96, -1), (0, 17, 8, 96, -1), (0, 24, 32, 256, 2), (0, 0, 8, 64, 0),
+    (1, 8, 64, 512, 1), (1, 480, 1536, 1536, 2), (2, 512, 4096, 4096, 2), (2, 1, 4096, 4096, 1),
+    (0, 4, 4, 48, -1), (3, 4, 4, 64, -1),
+])
+def test_auto_path_query(pkg, qtype, m, n, k, expect):
+    """pfng_hip_auto_path names the path PFNG_PATH_AUTO runs, or -1 where it declines."""
+    assert pkg.auto_path(qtype, m, n, k) == expect
+    if expect < 0:
         assert pkg.last_error()
 
 

@@ -141,7 +141,12 @@ def test_compute_matches_reference_vectors(hip, torch_gpu, oracle, tag, qtype):
     got = hip.compute(qtype, dev(torch, act), wt, n, path=hip.PATH_NAIVE)
     torch.cuda.synchronize()
     assert np.array_equal(got.cpu().numpy().view(np.uint32), out_ref.view(np.uint32))
-    # automatic path: within tolerance
+    # automatic path: within tolerance, or declined (no tiled path takes the shape)
+    if hip.auto_path(qtype, m, n, k) < 0:
+        with pytest.raises(hip.PfngError) as e:
+            hip.compute(qtype, dev(torch, act), wt, n, path=hip.PATH_AUTO)
+        assert e.value.status == hip.ERR_UNSUPPORTED and "PFNG_PATH_NAIVE" in str(e.value)
+        return
     got = hip.compute(qtype, dev(torch, act), wt, n, path=hip.PATH_AUTO)
     torch.cuda.synchronize()
     w = w8.reshape(-1).view(oracle.WEIGHT_DTYPE[qtype]).reshape(n, -1)

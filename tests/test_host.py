@@ -61,6 +61,29 @@ def test_fp16_conversions_match_oracle(pkg, oracle):
     assert np.array_equal(got, oracle.fp32_to_fp16(f))
 
 
+@pytest.mark.parametrize("qtype,variant", [(0, 0), (1, 0), (2, 0), (2, 1)])
+@pytest.mark.parametrize("m,n,k", [(3, 5, 256), (24, 32, 512), (9, 17, 768)])
+def test_host_compute_matches_oracle(pkg, oracle, qtype, variant, m, n, k):
+    """The harness's verification reference (pfng_host_compute) is the oracle's
+    compute() bit for bit, for one and for several threads (the oracle tests pin
+    compute() to the reference build and its fixtures)."""
+    if k % pkg.QK[qtype]:
+        pytest.skip("k is not a multiple of the block")
+    act, w = pkg.create_input(qtype, m, n, k, seed=7 + m, variant=variant)
+    w_o = w.reshape(-1).view(oracle.WEIGHT_DTYPE[qtype]).reshape(n, -1)
+    expect = oracle.compute(qtype, act, w_o)
+    for threads in (1, 4):
+        got = pkg.host_compute(qtype, act, w, n, threads=threads)
+        assert np.array_equal(got.view(np.uint32), expect.view(np.uint32))
+
+
+def test_host_compute_rejects_bad_arguments(pkg):
+    with pytest.raises(ValueError):
+        pkg.host_compute(0, np.zeros((2, 48), np.float32), np.zeros((3, 27), np.uint8), 3)
+    with pytest.raises(ValueError):
+        pkg.host_compute(3, np.zeros((2, 64), np.float32), np.zeros((3, 36), np.uint8), 3)
+
+
 def test_checksum_matches_oracle(pkg, oracle):
     x = np.random.default_rng(3).standard_normal((33, 97)).astype(np.float32)
     assert pkg.checksum(x) == oracle.checksum(x)

@@ -1,0 +1,163 @@
+"""The drop-in binding (qgemm-perf-framework-ng_amd/reference_overlay/): the
+mi355x-gfx950 platform profile, the three HIP kernel IDs and the patch for the
+reference tree.
+
+CPU: the patch applies to the reference; the profile defines every variable the
+reference's cmake/PlatformConfig.cmake requires; the kernel CMakeLists register
+through the reference's own pfng_declare_kernel (cmake/Kernel.cmake); and the
+reference harness (bench/main.cpp, bench/framework, llama_reference,
+kernels/common) compiles and links with the adapters against the reference's
+kernel_registry.h / adapter_common.h. These need the reference tree and skip
+without it.
+
+GPU: the harness built that way (the reference's own pfng-bench) runs the HIP
+kernel IDs on the device and verifies them against llama_reference::compute.
+"""
+from __future__ import annotations
+
+import os
+import re
+import shutil
+import subprocess
+import textwrap
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+OVERLAY = os.path.join(REPO, "qgemm-perf-framework-ng_amd", "reference_overlay")
+REF = os.environ.get("PFNG_REFERENCE", "/root/reference")
+BUILT = os.path.join(OVERLAY, "_build", "pfng-bench")
+IDS = ("q4_0-q8_0-HIP-mi355x", "q4_K-q8_K-HIP-mi355x", "iq2_xxs-q8_K-HIP-mi355x")
+
+needs_ref = pytest.mark.skipif(not os.path.isfile(os.path.join(REF, "bench", "main.cpp")),
+                               reason="reference tree not present")
+
+
+@needs_ref
+def test_patch_applies_to_the_reference(tmp_path):
+    shutil.copytree(REF, tmp_path / "ref", ignore=shutil.ignore_patterns("docs", "machine-benchmarks"))
+    r = subprocess.run(["patch", "-p1", "--dry-run", "-d", str(tmp_path / "ref"), "-i",
+                        os.path.join(OVERLAY, "reference.patch")], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "FAILED" not in r.stdout and "fuzz" not in r.stdout.lower()
+
+
+def cmake_script(tmp_path, body):
+    path = tmp_path / "check.cmake"
+    path.write_text(textwrap.dedent(body))
+    return subprocess.run(["cmake", "-P", str(path)], capture_output=True, text=True)
+
+
+@needs_ref
+def test_profile_defines_every_required_variable(tmp_path):
+    text = open(os.path.join(REF, "cmake", "PlatformConfig.cmake")).read()
+    required = re.search(r"foreach\(required\s+(.*?)\)", text, re.S).group(1).split()
+    assert "PFNG_PLATFORM_ID" in required and len(required) >= 10
+    checks = "\n".join(
+        f'if(NOT DEFINED {v} OR "${{{v}}}" STREQUAL "")\n  message(FATAL_ERROR "missing {v}")\nendif()'
+        for v in required)
+    r = cmake_script(tmp_path, f"""
+        set(PFNG_HIP_ROOT "{REPO}")
+        include("{OVERLAY}/platforms/mi355x-gfx950.cmake")
+        {checks}
+        if(NOT PFNG_PLATFORM_ID STREQUAL "mi355x-gfx950")
+          message(FATAL_ERROR "profile id")
+        endif()
+        if(NOT "x86_64" MATCHES "${{PFNG_PLATFORM_PROCESSOR_PATTERN}}")
+          message(FATAL_ERROR "processor pattern")
+        endif()
+        message("OK ${{PFNG_PLATFORM_COMPILE_DEFINITIONS}}")
+    """)
+    assert r.returncode == 0 and "OK PFNG_PLATFORM_MI355X_GFX950" in r.stderr, r.stderr
+
+
+@needs_ref
+def test_kernel_ids_register_through_the_reference_kernel_cmake(tmp_path):
+    """pfng_declare_kernel from the reference's cmake/Kernel.cmake consumes the
+    three CMakeLists: unique IDs, the right quantization pairs, enabled for
+    mi355x-gfx950 only."""
+    includes = "\n".join(f'include("{OVERLAY}/kernels/{i}/CMakeLists.txt")' for i in IDS)
+    body = f"""
+        include("{REF}/cmake/Kernel.cmake")
+        # the root CMakeLists.txt defines these for a real build
+        function(pfng_add_kernel_sources)
+        endfunction()
+        function(target_include_directories)
+        endfunction()
+        set(PFNG_TARGET_PLATFORM "@PLATFORM@")
+        {includes}
+        get_property(ids GLOBAL PROPERTY PFNG_KERNEL_IDS)
+        get_property(fns GLOBAL PROPERTY PFNG_KERNEL_REGISTRATION_FUNCTIONS)
+        message("IDS=${{ids}}")
+        message("FNS=${{fns}}")
+    """
+    r = cmake_script(tmp_path, body.replace("@PLATFORM@", "mi355x-gfx950"))
+    assert r.returncode == 0, r.stderr
+    assert f"IDS={';'.join(IDS)}" in r.stderr
+    assert "FNS=register_q4_0_hip_mi355x;register_q4_K_hip_mi355x;register_iq2_xxs_hip_mi355x" in r.stderr
+    r = cmake_script(tmp_path, body.replace("@PLATFORM@", "spacemit-k3-a100"))
+    assert r.returncode == 0 and "FNS=\n" in r.stderr + "\n", r.stderr
+    for i, q in zip(IDS, ("WeightQ4_0ActivationQ8_0", "WeightQ4_KActivationQ8_K", "WeightIQ2_XXSActivationQ8_K")):
+        text = open(os.path.join(OVERLAY, "kernels", i, "CMakeLists.txt")).read()
+        assert f"QUANTIZATION {q}" in text and "PLATFORMS mi355x-gfx950" in text
+
+
+@needs_ref
+def test_reference_harness_builds_with_the_overlay(pkg, tmp_path):
+    """The reference's bench/main.cpp, framework, llama_reference and
+    kernels/common compile and link with the three adapters and libpfng_hip
+    (g++, -Wall -Wextra); the binary reports the mi355x-gfx950 build."""
+    pkg.lib()  # libpfng_hip.so is built
+    out = tmp_path / "out"
+    r = subprocess.run(["make", "-s", "-C", OVERLAY, f"REF={REF}", f"WORK={tmp_path / 'work'}", f"OUT={out}"],
+                       capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "warning" not in (r.stdout + r.stderr).lower(), r.stdout + r.stderr
+    env = dict(os.environ, LD_LIBRARY_PATH=os.path.dirname(pkg.LIB_PATH))  # the rpath is relative to _build/
+    info = subprocess.run([str(out / "pfng-bench"), "--build-info"], capture_output=True, text=True, timeout=60,
+                          env=env)
+    assert info.returncode == 0 and "platform: mi355x-gfx950" in info.stdout, info.stdout + info.stderr
+
+
+def run_built(*args, timeout=300):
+    return subprocess.run([BUILT, *args], capture_output=True, text=True, timeout=timeout)
+
+
+def kernel_block(text, kid):
+    """The lines of the report of one kernel id."""
+    m = re.search(r"^\[" + re.escape(kid) + r"\].*?(?=^\[|\Z)", text, re.S | re.M)
+    return m.group(0) if m else ""
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not os.path.isfile(BUILT), reason="reference harness with the overlay was not built")
+def test_reference_harness_lists_and_detects_the_device(hip):
+    r = run_built("--list", timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    for kid in IDS:
+        assert re.search(r"^" + re.escape(kid) + r"\s.*\[platform=mi355x-gfx950\]", r.stdout, re.M), r.stdout
+    r = run_built("--platform-info", timeout=120)
+    assert r.returncode == 0 and "platform check: PASS" in r.stdout, r.stdout + r.stderr
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not os.path.isfile(BUILT), reason="reference harness with the overlay was not built")
+@pytest.mark.parametrize("kid,m,n,k", [
+    ("q4_0-q8_0-HIP-mi355x", 480, 1536, 1536),
+    ("q4_0-q8_0-HIP-mi355x", 1, 4096, 4096),
+    ("q4_K-q8_K-HIP-mi355x", 480, 1536, 1536),
+    ("iq2_xxs-q8_K-HIP-mi355x", 64, 1024, 2048),
+])
+def test_reference_harness_verifies_the_hip_kernels(hip, kid, m, n, k):
+    """The reference's run_benchmark verifies the kernel against its own
+    llama_reference::compute (every element, 1e-3 rule). Its timing reads the
+    host perf_event cycles counter; where the box does not allow that counter
+    the run stops after verification, which is then what this test checks."""
+    print(f"[case] reference pfng-bench {kid} {m}x{n}x{k}", flush=True)
+    r = run_built("--kernel", kid, "--m", str(m), "--n", str(n), "--k", str(k), "--samples", "3", "--warmup", "2")
+    block = kernel_block(r.stdout, kid)
+    assert f"error elements: 0/{m * n} " in block, r.stdout + r.stderr
+    if r.returncode == 0:
+        assert "verify: PASS" in block and "i8-i32 MAC/cycle" in block, block
+    else:
+        assert "perf_event_open" in block, r.stdout + r.stderr
