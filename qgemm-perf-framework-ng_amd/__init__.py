@@ -51,6 +51,17 @@ def lib() -> ctypes.CDLL:
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C {HERE}` (no CPU fallback exists)")
+        # torch carries its own HIP runtime (torch/lib/libamdhip64.so, soname
+        # libamdhip64.so.7, which torch's libraries name without the version).
+        # Loaded first, it satisfies the library's libamdhip64.so.7 and both
+        # share one runtime; loaded after the library, it would come in as a
+        # second runtime beside ROCm's, and the library's runtime then fails on
+        # the device torch holds. The tensors and streams this binding passes
+        # belong to torch's runtime, so load torch first.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = ctypes.CDLL(LIB_PATH)
         vp, i64, sz, ci = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t, ctypes.c_int
         L.pfng_hip_last_error.restype = ctypes.c_char_p
