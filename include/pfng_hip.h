@@ -140,6 +140,19 @@ size_t pfng_hip_compute_workspace_size(int type, int64_t m, int64_t k);
 int pfng_hip_compute(int type, const float *activation, const void *weight, float *out, int64_t m, int64_t n,
                      int64_t k, void *workspace, size_t workspace_bytes, int path, void *stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): pfng_hip_compute with the same arguments and results, but
+ * without a workspace. The quantized activations go to a static 16 MiB device
+ * array of the library (one per device, held until the process ends), so
+ * m * (k/32) * 34 bytes (q4_0) or m * (k/256) * 292 bytes (q4_K, iq2_xxs) must
+ * not exceed 16 MiB (e.g. m = 2048 at k = 4096 for q4_0); larger shapes return
+ * PFNG_ERR_INVALID_ARGUMENT. The call itself allocates nothing. Every call on a
+ * device shares that device's array: calls that overlap on one device (other
+ * streams, other host threads) race and must be serialized by the caller. */
+int pfng_hip_compute_noalloc(int type, const float *activation, const void *weight, float *out, int64_t m, int64_t n,
+                             int64_t k, int path, void *stream);
+
 /* ---- diagnostics ---------------------------------------------------------- */
 
 /* Exact integer parts of every block dot, computed by the same kernel

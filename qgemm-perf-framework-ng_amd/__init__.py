@@ -77,6 +77,7 @@ def lib() -> ctypes.CDLL:
         L.pfng_hip_compute_workspace_size.restype = sz
         L.pfng_hip_compute_workspace_size.argtypes = [ci, i64, i64]
         L.pfng_hip_compute.argtypes = [ci, vp, vp, vp, i64, i64, i64, vp, sz, ci, vp]
+        L.pfng_hip_compute_noalloc.argtypes = [ci, vp, vp, vp, i64, i64, i64, ci, vp]
         L.pfng_hip_block_isums.argtypes = [ci, vp, vp, vp, i64, i64, i64, vp]
         L.pfng_host_create_input.argtypes = [ci, ci, ctypes.c_uint32, sz, sz, sz, vp, vp]
         L.pfng_host_quantize_weights.argtypes = [ci, vp, vp, sz, sz]
@@ -97,7 +98,7 @@ EXPORTED_SYMBOLS = (
     "pfng_hip_quantize_q8_0", "pfng_hip_quantize_q8_K", "pfng_hip_quantize_q4_0", "pfng_hip_quantize_q4_K",
     "pfng_hip_mul_mat_q4_0_q8_0", "pfng_hip_mul_mat_q4_K_q8_K", "pfng_hip_mul_mat_iq2_xxs_q8_K",
     "pfng_hip_mul_mat", "pfng_hip_auto_path", "pfng_hip_compute_workspace_size", "pfng_hip_compute",
-    "pfng_hip_block_isums",
+    "pfng_hip_compute_noalloc", "pfng_hip_block_isums",
 )
 # host-side C-ABI declared in include/pfng_host.h
 HOST_SYMBOLS = (
@@ -293,6 +294,21 @@ def compute(qtype: int, activation, weight, n: int, path: int = PATH_AUTO, out=N
         _need(workspace, need, "workspace")
     check(lib().pfng_hip_compute(qtype, _p(activation), _p(weight), _p(out), m, n, k, _p(workspace),
                                  workspace.numel(), path, _stream(stream)))
+    return out
+
+
+def compute_noalloc(qtype: int, activation, weight, n: int, path: int = PATH_AUTO, out=None, stream=None):
+    """compute() without a workspace: the library's static per-device scratch
+    holds the quantized activations (at most 16 MiB of them)."""
+    torch = _torch()
+    m, k = activation.shape
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=activation.device)
+    if qtype in QK and m > 0 and n > 0 and k > 0 and k % QK[qtype] == 0:
+        _need(activation, m * k * 4, "activation")
+        _need(weight, _blocks(qtype, n, k, True), "weight")
+        _need(out, m * n * 4, "out")
+    check(lib().pfng_hip_compute_noalloc(qtype, _p(activation), _p(weight), _p(out), m, n, k, path, _stream(stream)))
     return out
 
 

@@ -73,6 +73,35 @@ int device_cus(int dev) {
     return cus;
 }
 
+// Scratch of pfng_hip_compute_noalloc: the quantized activations, in a
+// file-scope device array (each device that loads the library holds its own
+// copy until the process ends; no allocation call is ever made for it). In host
+// code `scratch` names a host-side stand-in, not the device memory: kernels get
+// the address hipGetSymbolAddress returns for the current device.
+constexpr size_t kNoallocScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoallocScratchBytes];
+
+std::mutex g_scratch_mu;
+std::map<int, void *> g_scratch_ptr;  // device -> device address of its scratch
+
+// The current device's scratch address, looked up once per device (with that
+// device current) and kept.
+int noalloc_scratch(void **ptr) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(PFNG_ERR_HIP, "hipGetDevice failed");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    auto it = g_scratch_ptr.find(dev);
+    if (it == g_scratch_ptr.end()) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return fail(PFNG_ERR_HIP, "compute_noalloc: hipGetSymbolAddress(scratch) on device %d: %s",
+                                               dev, hipGetErrorString(e));
+        it = g_scratch_ptr.emplace(dev, p).first;
+    }
+    *ptr = it->second;
+    return PFNG_OK;
+}
+
 int launch_mfma(int type, const void *weight, const void *act_q, float *out, int64_t m, int64_t n, int64_t k,
                 hipStream_t s) {
     int dev = 0;
@@ -230,6 +259,24 @@ int pfng_hip_compute(int type, const float *activation, const void *weight, floa
                                                   : pfng_hip_quantize_q8_K(activation, workspace, m, k, stream);
     if (rc) return rc;
     return pfng_hip_mul_mat(type, weight, workspace, out, m, n, k, path, stream);
+}
+
+int pfng_hip_compute_noalloc(int type, const float *activation, const void *weight, float *out, int64_t m, int64_t n,
+                             int64_t k, int path, void *stream) {
+    int rc = check_shape(type, m, n, k);
+    if (rc) return rc;
+    if (m == 0 || n == 0) return PFNG_OK;
+    const size_t need = pfng_hip_compute_workspace_size(type, m, k);
+    if (need > kNoallocScratchBytes)
+        return fail(PFNG_ERR_INVALID_ARGUMENT,
+                    "compute_noalloc: the quantized activations take %zu bytes, more than the %zu-byte static "
+                    "scratch (m * k/32 * 34 for q4_0, m * k/256 * 292 for the K-quants); use pfng_hip_compute "
+                    "with a workspace",
+                    need, kNoallocScratchBytes);
+    void *scratch_ptr = nullptr;
+    rc = noalloc_scratch(&scratch_ptr);
+    if (rc) return rc;
+    return pfng_hip_compute(type, activation, weight, out, m, n, k, scratch_ptr, kNoallocScratchBytes, path, stream);
 }
 
 int pfng_hip_block_isums(int type, const void *weight, const void *act_q, int32_t *out, int64_t m, int64_t n,
