@@ -382,7 +382,7 @@ using Q40Mid = Q40Config<32, 32, 1, 1, 32, 8, 2>;
 // taking 8 of a 16-block stage), loads two stages ahead
 using Q40SmallK2 = Q40Config<64, 64, 2, 2, 16, 2, 2>;
 
-enum { kCfgBig = 0, kCfgSmall = 1, kCfgSmall4 = 2, kCfgTiny = 3, kCfgMid = 4, kCfgSmallK2 = 5 };
+enum { kCfgBig = 0, kCfgSmall = 1, kCfgSmall4 = 2, kCfgTiny = 3, kCfgMid = 4, kCfgSmallK2 = 5, kCfgWhole = 6 };
 
 int64_t tiles_of(int64_t m, int64_t n, int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); }
 
@@ -407,6 +407,10 @@ MfmaPlan plan_mfma(int type, int64_t m, int64_t n, int64_t k, int cus) {
     const int64_t enough = 2 * (int64_t)cus;
     if (k % (32 * Q40Mid::kKB) == 0 && tiles_of(m, n, 32, 32) <= cus) {
         p.config = kCfgMid;
+    } else if (q4_0_small_supported(k) && 2 * tiles_of(m, n, 32, 96) >= cus && tiles_of(m, n, 32, 96) <= cus) {
+        // whole-K 32x96 tiles, one per CU and one round (480x1536x1536:
+        // 8.6 us against 9.8 us for the 2-K-wave 32x32 tile)
+        p.config = kCfgWhole;
     } else if (tiles_of(m, n, 128, 128) >= enough) {
         p.config = kCfgBig;
     } else if (k % (32 * Q40Small::kKB) != 0) {
@@ -430,6 +434,7 @@ hipError_t launch_mfma_mul_mat(int type, const void *w, const void *a, float *c,
     case kCfgTiny: return launch_q4_0<Q40Tiny, false>(w, a, c, nullptr, m, n, k, stream);
     case kCfgMid: return launch_q4_0<Q40Mid, false>(w, a, c, nullptr, m, n, k, stream);
     case kCfgSmallK2: return launch_q4_0<Q40SmallK2, false>(w, a, c, nullptr, m, n, k, stream);
+    case kCfgWhole: return launch_q4_0_small(w, a, c, nullptr, m, n, k, stream);
     default: return launch_q4_0<Q40Small4, false>(w, a, c, nullptr, m, n, k, stream);
     }
 }
@@ -444,6 +449,7 @@ hipError_t launch_mfma_block_isums(int type, const void *w, const void *a, int32
     case kCfgTiny: return launch_q4_0<Q40Tiny, true>(w, a, nullptr, out, m, n, k, stream);
     case kCfgMid: return launch_q4_0<Q40Mid, true>(w, a, nullptr, out, m, n, k, stream);
     case kCfgSmallK2: return launch_q4_0<Q40SmallK2, true>(w, a, nullptr, out, m, n, k, stream);
+    case kCfgWhole: return launch_q4_0_small(w, a, nullptr, out, m, n, k, stream);
     default: return launch_q4_0<Q40Small4, true>(w, a, nullptr, out, m, n, k, stream);
     }
 }

@@ -1,0 +1,236 @@
+// q4_0 x q8_0 int8-MFMA GEMM for small problems whose whole K range fits in
+// LDS (e.g. 480x1536x1536): one workgroup per CU-sized output tile of
+// 32 x 32*TN, the tile's operands copied into LDS once, K split over the
+// waves.
+//
+// Copy: the tile's 32 activation rows and 32*TN weight rows are each one
+// contiguous run of memory (row-major blocks, all of K), copied with 16-byte
+// direct-to-LDS buffer loads, 1 KB per instruction and no vector ALU work per
+// copy: L2 -> LDS moves long runs several times faster than row-strided
+// pieces (measured: 68-byte row pieces by 4-byte lanes ~18 B/clk/CU, long
+// 16-byte runs ~73 B/clk/CU). Rows are laid out in LDS as in memory, each
+// padded to an odd number of 16-byte chunks, so the 32 lanes reading one row
+// each meet at most one other lane per bank.
+// Compute: wave w takes column tile w % TN and block pairs
+// [(w / TN)*PPW, (w / TN + 1)*PPW) of its rows (K slice w / TN of WS). Per
+// block: S16 = v_mfma_i32_32x32x32_i8 (exact 16*S_b) on the raw bytes (the
+// first block of a pair realigned by two bytes, nibbles widened to 16*(q-8)
+// int8), P = da (x) dw by v_mfma_f32_32x32x8_f16 on one-hot fp16 operands
+// (exact), acc = fma(S16, P, acc). The WS partial tiles of a column tile are
+// then added through LDS in slice order (results do not depend on timing);
+// C = acc / 16.
+//
+// Integer parts are exact; the fp32 result differs from the reference's
+// block-sequential sum (llama_reference.cpp:134-146) only by reassociation.
+#include "device_common.h"
+#include "kernels.h"
+
+namespace pfng {
+
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr uint32_t kBufferWord3 = 0x00020000u;  // raw buffer resource, gfx9 family
+
+// One 16-byte direct-to-LDS buffer load per lane (64 lanes: 1 KB at dst). A
+// plain function: inside a kernel template the 16-byte form of the builtin
+// makes the host pass drop the kernel's launch stub.
+__device__ __forceinline__ void copy16_to_lds(__amdgpu_buffer_rsrc_t r, uint8_t *dst, uint32_t voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 16, voffset, 0, 0, 0);
+}
+
+template <int TN, int WS, int NB>
+struct WtConfig {
+    static constexpr int WK = WS * TN;  // waves
+    static constexpr int kThreads = 64 * WK;
+    static_assert(NB % 8 == 0, "a row is whole 16-byte chunks (8 blocks)");
+    static_assert((NB / 2) % WS == 0, "every wave takes whole block pairs");
+    static constexpr int kPPW = NB / 2 / WS;  // block pairs per wave
+    // 16-byte chunks of a row: data, and the LDS row made odd
+    static constexpr int kDataA = NB * 34 / 16, kDataW = NB * 18 / 16;
+    static constexpr int kChunksA = kDataA | 1, kChunksW = kDataW | 1;
+    static constexpr int kRowsW = 32 * TN;
+    static constexpr int kCopiesA = (32 * kChunksA + 63) / 64;  // 64 chunks per copy instruction
+    static constexpr int kCopiesW = (kRowsW * kChunksW + 63) / 64;
+    static constexpr int kCopiesPerWave = (kCopiesA + kCopiesW + WK - 1) / WK;
+    static constexpr int kBytesA = kCopiesA * 1024, kBytesW = kCopiesW * 1024;
+    static constexpr int kGroupBytes = WK * 64 * 16;  // one float4 register group of every wave
+    static_assert(kBytesA + kBytesW <= 160 * 1024, "tile must fit in LDS");
+    static_assert(4 * kGroupBytes <= kBytesW, "partial tiles fit in the weight buffer");
+};
+
+// Byte offset in memory (from the tile's first row) of this lane's chunk in
+// copy instruction j of a region of `rows` LDS rows of C chunks, the first D
+// of them data (the rest padding, a copy of the row's last data chunk);
+// lanes past the region repeat its last chunk, rows past `rows_valid` repeat
+// the last valid row.
+template <int C, int D>
+__device__ __forceinline__ uint32_t chunk_source(int j, int lane, int rows, int rows_valid) {
+    int i = 64 * j + lane;
+    if (i >= rows * C) i = rows * C - 1;
+    const int r = i / C;
+    int col = i - r * C;
+    if (col >= D) col = D - 1;
+    const int rr = r < rows_valid ? r : rows_valid - 1;
+    return (uint32_t)rr * (uint32_t)(D * 16) + (uint32_t)col * 16u;
+}
+
+// This wave's copy instructions (activation rows into bufa, weight rows
+// into bufw), dealt round-robin over the waves.
+template <class Cfg>
+__device__ __forceinline__ void copy_tile(uint8_t *bufa, uint8_t *bufw, __amdgpu_buffer_rsrc_t ra,
+                                          __amdgpu_buffer_rsrc_t rw, int wave, int lane, int rows_a, int rows_w) {
+    constexpr int kTotal = Cfg::kCopiesA + Cfg::kCopiesW;
+#pragma unroll
+    for (int i = 0; i < Cfg::kCopiesPerWave; ++i) {
+        int j = wave + i * Cfg::WK;
+        if (j >= kTotal) j = kTotal - 1;
+        if (j < Cfg::kCopiesA)
+            copy16_to_lds(ra, bufa + j * 1024,
+                          chunk_source<Cfg::kChunksA, Cfg::kDataA>(j, lane, 32, rows_a));
+        else
+            copy16_to_lds(rw, bufw + (j - Cfg::kCopiesA) * 1024,
+                          chunk_source<Cfg::kChunksW, Cfg::kDataW>(j - Cfg::kCopiesA, lane, Cfg::kRowsW, rows_w));
+    }
+}
+
+// The wave's block pairs against its column tile.
+template <class Cfg, bool kIsums>
+__device__ __forceinline__ void compute_slice(const uint8_t *bufa, const uint8_t *bufw, int tile, int slice, int lane,
+                                              f32x16 &acc, int32_t *isums, int m, int n, int nb, int m0, int n0) {
+    const int li = lane & 31, h = lane >> 5;
+    const uint32_t keep = h ? 0u : 0xffffffffu;  // K-half 1 lanes feed zeros to the scale products
+    const uint32_t *arow = reinterpret_cast<const uint32_t *>(bufa) + li * Cfg::kChunksA * 4;
+    const uint32_t *wrow = reinterpret_cast<const uint32_t *>(bufw) + (tile * 32 + li) * Cfg::kChunksW * 4;
+#pragma unroll
+    for (int pp = 0; pp < Cfg::kPPW; ++pp) {
+        const int lp = slice * Cfg::kPPW + pp;  // pair within the row
+        const uint32_t *sa = arow + lp * 17, *sw = wrow + lp * 9;
+        const uint32_t *ah = sa + 2 * h, *wh = sw + 2 * h;
+        // block 0 sits two bytes into its dwords, block 1 is dword-aligned
+        const i32x4 a0 = (i32x4){(int)shift2(ah[0], ah[1]), (int)shift2(ah[1], ah[2]), (int)shift2(ah[4], ah[5]),
+                                 (int)shift2(ah[5], ah[6])};
+        const i32x4 a1 = (i32x4){(int)ah[9], (int)ah[10], (int)ah[13], (int)ah[14]};
+        const uint32_t u0 = shift2(wh[0], wh[1]), u1 = shift2(wh[1], wh[2]);
+        const uint32_t v0 = wh[5], v1 = wh[6];
+        const i32x4 b0 = (i32x4){(int)q4_0_lo16(u0), (int)q4_0_lo16(u1), (int)q4_0_hi16(u0), (int)q4_0_hi16(u1)};
+        const i32x4 b1 = (i32x4){(int)q4_0_lo16(v0), (int)q4_0_lo16(v1), (int)q4_0_hi16(v0), (int)q4_0_hi16(v1)};
+        const i32x16 s0 = mfma_i8_32x32x32(a0, b0, (i32x16){});
+        const i32x16 s1 = mfma_i8_32x32x32(a1, b1, (i32x16){});
+        if constexpr (kIsums) {
+            const int col = n0 + tile * 32 + li;
+            const int blk = 2 * lp;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int row = m0 + mfma_row(lane, q);
+                if (row < m && col < n) {
+                    int32_t *dst = isums + ((size_t)row * n + col) * nb + blk;
+                    dst[0] = s0[q] / 16;
+                    dst[1] = s1[q] / 16;
+                }
+            }
+        } else {
+            const f16x4 pa =
+                __builtin_bit_cast(f16x4, make_uint2(__builtin_amdgcn_perm(sa[8], sa[0], 0x07060100u) & keep, 0u));
+            const f16x4 pb0 = __builtin_bit_cast(f16x4, make_uint2(sw[0] & keep & 0xffffu, 0u));
+            const f16x4 pb1 = __builtin_bit_cast(f16x4, make_uint2(sw[4] & keep & 0xffff0000u, 0u));
+            const f32x16 p0 = mfma_f16_32x32x8(pa, pb0, (f32x16){});
+            const f32x16 p1 = mfma_f16_32x32x8(pa, pb1, (f32x16){});
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[q] = __builtin_fmaf((float)s0[q], p0[q], acc[q]);
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[q] = __builtin_fmaf((float)s1[q], p1[q], acc[q]);
+        }
+    }
+}
+
+template <int TN, int WS, int NB, bool kIsums>
+__global__ __launch_bounds__(64 * WS * TN) void gemm_q4_0_wt_kernel(const uint8_t *__restrict__ w,
+                                                                    const uint8_t *__restrict__ a,
+                                                                    float *__restrict__ c,
+                                                                    int32_t *__restrict__ isums, int m, int n) {
+    using Cfg = WtConfig<TN, WS, NB>;
+    __shared__ __align__(16) uint8_t a0[Cfg::kBytesA], w0[Cfg::kBytesW];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const TileOrigin to = xcd_tile(blockIdx.x, (m + 31) / 32, (n + Cfg::kRowsW - 1) / Cfg::kRowsW);
+    const int m0 = to.mi * 32, n0 = to.ni * Cfg::kRowsW;
+    const int tile = wave % TN, slice = wave / TN;
+
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a + (size_t)m0 * NB * 34), 0, (int)((uint32_t)(m - m0) * NB * 34u), kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(w + (size_t)n0 * NB * 18), 0, (int)((uint32_t)(n - n0) * NB * 18u), kBufferWord3);
+    const int rows_a = m - m0 < 32 ? m - m0 : 32;
+    const int rows_w = n - n0 < Cfg::kRowsW ? n - n0 : Cfg::kRowsW;
+    copy_tile<Cfg>(a0, w0, ra, rw, wave, lane, rows_a, rows_w);
+    // this wave's copies have landed, then every wave's
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    f32x16 acc = (f32x16){};
+    compute_slice<Cfg, kIsums>(a0, w0, tile, slice, lane, acc, isums, m, n, NB, m0, n0);
+
+    if constexpr (!kIsums) {
+        // partial tiles to LDS as float4 register groups [group][wave][lane]
+        // (in the weight array, dead after the barrier), then each wave adds
+        // one group of one column tile over the K slices in order and stores it
+        __syncthreads();
+        auto group_base = [&](int g) -> float4 * { return reinterpret_cast<float4 *>(w0) + g * Cfg::WK * 64; };
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            group_base(g)[wave * 64 + lane] = make_float4(acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]);
+        __syncthreads();
+        const int li = lane & 31;
+        for (int tg = wave; tg < TN * 4; tg += Cfg::WK) {
+            const int t = tg % TN, g = tg / TN;
+            const float4 *pg = group_base(g);
+            float4 s = pg[t * 64 + lane];
+#pragma unroll
+            for (int sl = 1; sl < WS; ++sl) {
+                const float4 v = pg[(sl * TN + t) * 64 + lane];
+                s.x += v.x;
+                s.y += v.y;
+                s.z += v.z;
+                s.w += v.w;
+            }
+            const int col = n0 + t * 32 + li;
+            const float r[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = m0 + mfma_row(lane, 4 * g + i);
+                if (row < m && col < n) c[(size_t)row * n + col] = r[i] * 0.0625f;
+            }
+        }
+    }
+}
+
+template <int TN, int WS, int NB, bool kIsums>
+hipError_t launch_wt(const void *w, const void *a, float *c, int32_t *isums, int64_t m, int64_t n, hipStream_t stream) {
+    using Cfg = WtConfig<TN, WS, NB>;
+    const dim3 grid((unsigned)(((m + 31) / 32) * ((n + Cfg::kRowsW - 1) / Cfg::kRowsW)));
+    hipLaunchKernelGGL((gemm_q4_0_wt_kernel<TN, WS, NB, kIsums>), grid, dim3(Cfg::kThreads), 0, stream,
+                       static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(a), c, isums, (int)m, (int)n);
+    return hipGetLastError();
+}
+
+template <int TN, int WS, int NB>
+hipError_t launch_wt_any(const void *w, const void *a, float *c, int32_t *isums, int64_t m, int64_t n,
+                         hipStream_t stream) {
+    return isums ? launch_wt<TN, WS, NB, true>(w, a, c, isums, m, n, stream)
+                 : launch_wt<TN, WS, NB, false>(w, a, c, isums, m, n, stream);
+}
+
+}  // namespace
+
+bool q4_0_small_supported(int64_t k) { return k == 1024 || k == 1536; }
+
+hipError_t launch_q4_0_small(const void *w, const void *a, float *c, int32_t *isums, int64_t m, int64_t n,
+                             int64_t k, hipStream_t stream) {
+    // 32 x 96 tiles, 12 waves: 4 K slices x 3 column tiles
+    if (k == 1536) return launch_wt_any<3, 4, 48>(w, a, c, isums, m, n, stream);
+    if (k == 1024) return launch_wt_any<3, 4, 32>(w, a, c, isums, m, n, stream);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace pfng

@@ -46,6 +46,13 @@ hipError_t launch_mfma_mul_mat(int type, const void *w, const void *a, float *c,
 hipError_t launch_mfma_block_isums(int type, const void *w, const void *a, int32_t *out, int64_t m, int64_t n,
                                    int64_t k, const MfmaPlan &plan, hipStream_t stream);
 
+// gemm_small.hip — q4_0 GEMMs whose 32 x 96 tiles, all of K, fit in LDS
+// (k = 1024 or 1536); one workgroup per tile, K split over the waves.
+// isums != nullptr writes the block sums instead of C.
+bool q4_0_small_supported(int64_t k);
+hipError_t launch_q4_0_small(const void *w, const void *a, float *c, int32_t *isums, int64_t m, int64_t n,
+                             int64_t k, hipStream_t stream);
+
 // gemm_kquant.hip — q4_K and iq2_xxs against q8_K
 MfmaPlan plan_kquant(int type, int64_t m, int64_t n, int64_t k, int cus);
 hipError_t launch_kquant_mul_mat(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,

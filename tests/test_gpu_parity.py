@@ -194,7 +194,7 @@ def test_gemv_q4_0(hip, torch_gpu, oracle, m, n, k):
 
 @pytest.mark.parametrize("m,n,k", [(32, 32, 128), (100, 77, 256), (480, 1536, 1536), (9, 300, 640), (2048, 4096, 256),
                                    (1, 50, 128), (16, 4096, 4096), (33, 1000, 512), (64, 100, 2048), (65, 70, 256),
-                                   (256, 4096, 4096)])
+                                   (256, 4096, 4096), (470, 1500, 1536), (256, 1536, 1024), (300, 2000, 1024)])
 def test_mfma_q4_0(hip, torch_gpu, oracle, m, n, k):
     torch = torch_gpu
     say(f"mfma q4_0 {m}x{n}x{k}")
@@ -208,10 +208,10 @@ def test_mfma_q4_0(hip, torch_gpu, oracle, m, n, k):
 # block_isums runs the configuration the MFMA plan picks for the shape: 64x64
 # with 2 waves (k % 256 != 0), 32x32 with 2 K-waves, 32x32 with 8 K-waves
 # (decode batches, k % 1024 == 0), 64x64 with 4 waves (640x2048), 64x64 with
-# 2 K-waves (200x3072x2048)
+# 2 K-waves (200x3072x2048), whole-K 32x96 tiles (250x1540x1024, 470x1500x1536)
 @pytest.mark.parametrize("m,n,k", [(32, 32, 128), (70, 45, 384), (64, 64, 1536), (9, 40, 256), (50, 33, 640),
                                    (96, 40, 512), (20, 50, 2048), (64, 33, 1024), (640, 2048, 256),
-                                   (200, 3072, 2048)])
+                                   (200, 3072, 2048), (250, 1540, 1024), (470, 1500, 1536)])
 def test_block_isums_q4_0_bit_exact(hip, torch_gpu, oracle, m, n, k):
     torch = torch_gpu
     say(f"block isums q4_0 {m}x{n}x{k}")
