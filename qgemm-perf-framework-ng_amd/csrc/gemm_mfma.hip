@@ -57,16 +57,22 @@ struct Q40Config {
     static constexpr int kAq = 0;
     static constexpr int kAd = kAq + BM * kRowStride;       // fp16 da[row][KB]
     static constexpr int kWq = kAd + BM * KB * 2;
-    static constexpr int kWd = kWq + BN * kRowStride;       // fp16 dw[row][KB]
-    static constexpr int kBufBytes = kWd + BN * KB * 2;  // one stage
-    static constexpr int kLdsBytes = 2 * kBufBytes;          // double-buffered
+    // dw[row][KB] as 32-bit words: block t's fp16 scale in the low half for
+    // even t, in the high half for odd t, zeros in the other half
+    static constexpr int kWd = kWq + BN * kRowStride;
+    static constexpr int kBufBytes = kWd + BN * KB * 4;  // one stage
+    // zeros that the upper K-half lanes read as their weight scale words
+    static constexpr int kZero = 2 * kBufBytes;
+    static constexpr int kZeroBytes = TN * 32 * KB * 4;
+    static constexpr int kLdsBytes = kZero + kZeroBytes;  // double-buffered stages + zeros
     static_assert(TM >= 1 && TN >= 1, "tile too small");
     static_assert(KB % 4 == 0, "KB must be a multiple of 4 (scale vectors are read four at a time)");
     static_assert(kActPT * kThreads == kActPairs && kWPT * kThreads == kWPairs, "pairs must split evenly over threads");
     static_assert(kActPT >= 1 && kWPT >= 1, "every thread loads at least one pair of each operand");
     static_assert(kAd % 16 == 0 && kWq % 16 == 0 && kWd % 16 == 0, "LDS regions 16-byte aligned");
     static_assert(kWaveBlocks * WK == KB && kWaveBlocks % 4 == 0, "each wave takes a multiple of 4 blocks");
-    static_assert((WK - 1) * WM * WN * TM * TN * 16 * 64 * 4 <= kLdsBytes, "K-wave reduction fits in LDS");
+    static_assert((WK - 1) * WM * WN * TM * TN * 16 * 64 * 4 <= 2 * kBufBytes, "K-wave reduction fits in LDS");
+    static_assert(kZeroBytes % 16 == 0 && kZeroBytes >= 16, "zero strip of whole 16-byte words");
 };
 
 template <class C>
@@ -75,26 +81,52 @@ struct StageRegs {
     uint32_t w[C::kWPT][9];
 };
 
+// Byte offsets of the block pairs a thread loads, from the workgroup's first
+// row at the current stage's first block. They stay the same over the K loop
+// (rows past the matrix edge are clamped to its last row), so each stage's
+// loads are a uniform stage base plus these 32-bit offsets: no per-stage
+// address arithmetic in the vector ALU. BM * nb * 34 < 2^32 for any k the
+// library takes (nb < 2^20).
 template <class C>
-__device__ __forceinline__ void load_stage(const uint8_t *__restrict__ a, const uint8_t *__restrict__ w, int m, int n,
-                                           int nb, int m0, int n0, int kb0, StageRegs<C> &r) {
+struct LoadOffsets {
+    uint32_t a[C::kActPT];
+    uint32_t w[C::kWPT];
+};
+
+template <class C>
+__device__ __forceinline__ LoadOffsets<C> load_offsets(int m, int n, int nb, int m0, int n0) {
+    LoadOffsets<C> o;
 #pragma unroll
     for (int it = 0; it < C::kActPT; ++it) {
         const int task = threadIdx.x + it * C::kThreads;
         const int row = m0 + task / C::kPairsPerRow;
-        const int p = task % C::kPairsPerRow;
         const int lrow = row < m ? row : m - 1;
-        const uint32_t *src = reinterpret_cast<const uint32_t *>(a + ((size_t)lrow * nb + kb0 + 2 * p) * 34);
-#pragma unroll
-        for (int i = 0; i < 17; ++i) r.a[it][i] = src[i];
+        o.a[it] = ((uint32_t)(lrow - m0) * (uint32_t)nb + 2u * (uint32_t)(task % C::kPairsPerRow)) * 34u;
     }
 #pragma unroll
     for (int it = 0; it < C::kWPT; ++it) {
         const int task = threadIdx.x + it * C::kThreads;
         const int row = n0 + task / C::kPairsPerRow;
-        const int p = task % C::kPairsPerRow;
         const int lrow = row < n ? row : n - 1;
-        const uint32_t *src = reinterpret_cast<const uint32_t *>(w + ((size_t)lrow * nb + kb0 + 2 * p) * 18);
+        o.w[it] = ((uint32_t)(lrow - n0) * (uint32_t)nb + 2u * (uint32_t)(task % C::kPairsPerRow)) * 18u;
+    }
+    return o;
+}
+
+// a_st / w_st: the workgroup's first activation / weight row at the stage's
+// first block (uniform across the workgroup).
+template <class C>
+__device__ __forceinline__ void load_stage(const uint8_t *a_st, const uint8_t *w_st, const LoadOffsets<C> &o,
+                                           StageRegs<C> &r) {
+#pragma unroll
+    for (int it = 0; it < C::kActPT; ++it) {
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(a_st + o.a[it]);
+#pragma unroll
+        for (int i = 0; i < 17; ++i) r.a[it][i] = src[i];
+    }
+#pragma unroll
+    for (int it = 0; it < C::kWPT; ++it) {
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(w_st + o.w[it]);
 #pragma unroll
         for (int i = 0; i < 9; ++i) r.w[it][i] = src[i];
     }
@@ -130,24 +162,21 @@ __device__ __forceinline__ void store_stage(uint8_t *lds, const StageRegs<C> &r)
         for (int i = 0; i < 4; ++i) q4_0_unpack16(u[5 + i], lo[i], hi[i]);
         dst[2] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
         dst[3] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-        *reinterpret_cast<uint32_t *>(lds + C::kWd + (row * C::kKB + 2 * p) * 2) = (u[0] & 0xffffu) | (u[4] & 0xffff0000u);
+        *reinterpret_cast<uint2 *>(lds + C::kWd + (row * C::kKB + 2 * p) * 4) = make_uint2(u[0] & 0xffffu, u[4] & 0xffff0000u);
     }
 }
 
-// f16x4 holding one fp16 value in slot `slot` (0..3) and zeros elsewhere.
-__device__ __forceinline__ f16x4 one_hot_half(uint32_t h16, int slot) {
-    const uint32_t lo = slot == 0 ? h16 : (slot == 1 ? h16 << 16 : 0u);
-    const uint32_t hi = slot == 2 ? h16 : (slot == 3 ? h16 << 16 : 0u);
-    return __builtin_bit_cast(f16x4, make_uint2(lo, hi));
-}
-
-// Operand fragments of one block t for the wave's TM x TN tiles.
+// Operand fragments of one block t for the wave's TM x TN tiles. ad holds the
+// da of blocks t4..t4+3 (t4 = t rounded down to a multiple of 4) in its four
+// fp16 slots; wd holds dw of block t in slot t % 4 and zeros elsewhere, and
+// the K-half 1 lanes read theirs from the zero strip, so the f16 MFMA of ad
+// and wd is the exact outer product da * dw of block t.
 template <class C>
 struct Frags {
     i32x4 av[C::TM];
     i32x4 wv[C::TN];
-    f16x4 ad[C::TM];  // da of blocks t4..t4+3 in the four fp16 slots
-    f16x4 wd[C::TN];  // dw of block t in slot t % 4 (zero for K-half 1 lanes)
+    f16x4 ad[C::TM];
+    f16x4 wd[C::TN];
 };
 
 // Per-lane LDS base addresses of one stage buffer; every fragment read is a
@@ -157,21 +186,22 @@ struct FragBases {
 };
 
 template <class C>
-__device__ __forceinline__ FragBases frag_bases(const uint8_t *buf, int lane, int wave_m, int wave_n) {
+__device__ __forceinline__ FragBases frag_bases(uint8_t *lds, int buf, int lane, int wave_m, int wave_n) {
     const int li = lane & 31, lh = lane >> 5;
     const int ra = wave_m * C::TM * 32 + li, rw = wave_n * C::TN * 32 + li;
+    const uint8_t *b0 = lds + buf * C::kBufBytes;
     FragBases b;
-    b.aq = buf + C::kAq + ra * C::kRowStride + lh * 16;
-    b.ad = buf + C::kAd + ra * C::kKB * 2;
-    b.wq = buf + C::kWq + rw * C::kRowStride + lh * 16;
-    b.wd = buf + C::kWd + rw * C::kKB * 2;
+    b.aq = b0 + C::kAq + ra * C::kRowStride + lh * 16;
+    b.ad = b0 + C::kAd + ra * C::kKB * 2;
+    b.wq = b0 + C::kWq + rw * C::kRowStride + lh * 16;
+    b.wd = lh ? lds + C::kZero : b0 + C::kWd + rw * C::kKB * 4;
     return b;
 }
 
 // Fragments of block tb + j (tb a multiple of 4, j known at compile time).
 template <class C>
-__device__ __forceinline__ void load_frags(const FragBases &b, int tb, int j, int lh, Frags<C> &f) {
-    const int t = tb + j, t4 = tb + (j & ~3), tt = j & 3;
+__device__ __forceinline__ void load_frags(const FragBases &b, int tb, int j, Frags<C> &f) {
+    const int t = tb + j, t4 = tb + (j & ~3);
 #pragma unroll
     for (int tm = 0; tm < C::TM; ++tm) {
         f.av[tm] = *reinterpret_cast<const i32x4 *>(b.aq + tm * 32 * C::kRowStride + t * 32);
@@ -180,8 +210,8 @@ __device__ __forceinline__ void load_frags(const FragBases &b, int tb, int j, in
 #pragma unroll
     for (int tn = 0; tn < C::TN; ++tn) {
         f.wv[tn] = *reinterpret_cast<const i32x4 *>(b.wq + tn * 32 * C::kRowStride + t * 32);
-        const uint32_t h16 = *reinterpret_cast<const uint16_t *>(b.wd + tn * 32 * C::kKB * 2 + t * 2);
-        f.wd[tn] = one_hot_half(lh ? 0u : h16, tt);
+        const uint32_t word = *reinterpret_cast<const uint32_t *>(b.wd + tn * 32 * C::kKB * 4 + t * 4);
+        f.wd[tn] = __builtin_bit_cast(f16x4, (j & 2) ? make_uint2(0u, word) : make_uint2(word, 0u));
     }
 }
 
@@ -195,9 +225,9 @@ struct ItemRegs {
 // flight while the VALU epilogue of item i runs, and the LDS fragments of
 // block t+1 load during block t.
 template <class C, bool kIsums>
-__device__ __forceinline__ void compute_stage(const uint8_t *buf, f32x16 (&acc)[C::TM][C::TN], int32_t *isums, int m,
-                                              int n, int nb, int m0, int n0, int s, int tb, int lane, int wave_m,
-                                              int wave_n) {
+__device__ __forceinline__ void compute_stage(uint8_t *lds, int buf, f32x16 (&acc)[C::TM][C::TN], int32_t *isums,
+                                              int m, int n, int nb, int m0, int n0, int s, int tb, int lane,
+                                              int wave_m, int wave_n) {
     constexpr int kTiles = C::TM * C::TN;
     constexpr int kItems = C::kWaveBlocks * kTiles;
     // With several tiles per block, the fragments of block t+1 are read while
@@ -205,15 +235,14 @@ __device__ __forceinline__ void compute_stage(const uint8_t *buf, f32x16 (&acc)[
     // such slack, so all of the stage's fragments are read up front.
     constexpr bool kAllFrags = kTiles == 1;
     constexpr int kSets = kAllFrags ? C::kWaveBlocks : 2;
-    const FragBases bases = frag_bases<C>(buf, lane, wave_m, wave_n);
-    const int lh = lane >> 5;
+    const FragBases bases = frag_bases<C>(lds, buf, lane, wave_m, wave_n);
     Frags<C> fr[kSets];
     ItemRegs it[2];
     if constexpr (kAllFrags) {
 #pragma unroll
-        for (int j = 0; j < C::kWaveBlocks; ++j) load_frags<C>(bases, tb, j, lh, fr[j]);
+        for (int j = 0; j < C::kWaveBlocks; ++j) load_frags<C>(bases, tb, j, fr[j]);
     } else {
-        load_frags<C>(bases, tb, 0, lh, fr[0]);
+        load_frags<C>(bases, tb, 0, fr[0]);
     }
     auto issue = [&](int item) {
         const int t = item / kTiles, tile = item % kTiles;
@@ -228,7 +257,7 @@ __device__ __forceinline__ void compute_stage(const uint8_t *buf, f32x16 (&acc)[
     for (int item = 0; item < kItems; ++item) {
         const int t = item / kTiles, tile = item % kTiles;
         const int tm = tile / C::TN, tn = tile % C::TN;
-        if (!kAllFrags && tile == 0 && t + 1 < C::kWaveBlocks) load_frags<C>(bases, tb, t + 1, lh, fr[(t + 1) & 1]);
+        if (!kAllFrags && tile == 0 && t + 1 < C::kWaveBlocks) load_frags<C>(bases, tb, t + 1, fr[(t + 1) & 1]);
         if (item + 1 < kItems) issue(item + 1);
         // keep the order: without the fences the scheduler sinks the MFMAs of
         // item+1 below this epilogue and reuses their result registers, which
@@ -282,29 +311,43 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWavesPerEU) void gemm_q4_0_kern
     // regs[r] holds stage s+1 while stage s (s % kDepth == r) is computed.
     const int stages = nb / C::kKB;
     auto clampst = [&](int st) { return st < stages ? st : stages - 1; };
+    // uniform row bases of the tile; stage st starts st * kKB blocks further
+    const uint8_t *a_tile = a + (size_t)m0 * nb * 34;
+    const uint8_t *w_tile = w + (size_t)n0 * nb * 18;
+    const LoadOffsets<C> offs = load_offsets<C>(m, n, nb, m0, n0);
+    for (int i = threadIdx.x; i < C::kZeroBytes / 16; i += C::kThreads)
+        reinterpret_cast<uint4 *>(lds + C::kZero)[i] = make_uint4(0u, 0u, 0u, 0u);
     StageRegs<C> regs[C::kDepth];
-    load_stage<C>(a, w, m, n, nb, m0, n0, 0, regs[0]);
+    load_stage<C>(a_tile, w_tile, offs, regs[0]);
     store_stage<C>(lds, regs[0]);
 #pragma unroll
-    for (int r = 0; r < C::kDepth; ++r) load_stage<C>(a, w, m, n, nb, m0, n0, clampst(1 + r) * C::kKB, regs[r]);
+    for (int r = 0; r < C::kDepth; ++r) {
+        const int kb = clampst(1 + r) * C::kKB;
+        load_stage<C>(a_tile + kb * 34, w_tile + kb * 18, offs, regs[r]);
+    }
     __syncthreads();
-    // The loop runs a whole number of kDepth-stage rounds; stages past the end
-    // (stages % kDepth != 0) skip only the arithmetic. Leaving the round with
-    // a break instead made the compiler wait for freshly issued loads before
+    // The loop runs whole rounds of kRound stages (a multiple of kDepth and of
+    // the two LDS buffers, so that register set and buffer are compile-time
+    // constants and every fragment address is a base plus an immediate);
+    // stages past the end skip only the arithmetic. Leaving the round with a
+    // break instead made the compiler wait for freshly issued loads before
     // every barrier, which undid the prefetch.
-    for (int s0 = 0; s0 < stages; s0 += C::kDepth) {
+    constexpr int kRound = C::kDepth % 2 == 0 ? C::kDepth : 2 * C::kDepth;
+    for (int s0 = 0; s0 < stages; s0 += kRound) {
 #pragma unroll
-        for (int r = 0; r < C::kDepth; ++r) {
-            const int s = s0 + r;
-            const int buf = s & 1;
+        for (int rr = 0; rr < kRound; ++rr) {
+            const int s = s0 + rr;
+            const int r = rr % C::kDepth;
+            const int buf = rr & 1;
             __builtin_amdgcn_sched_barrier(0);
-            if (C::kDepth == 1 || s < stages)  // uniform across the workgroup
-                compute_stage<C, kIsums>(lds + buf * C::kBufBytes, acc, isums, m, n, nb, m0, n0, s,
-                                         wk * C::kWaveBlocks, lane, wave_m, wave_n);
+            if (s < stages)  // uniform across the workgroup
+                compute_stage<C, kIsums>(lds, buf, acc, isums, m, n, nb, m0, n0, s, wk * C::kWaveBlocks, lane,
+                                         wave_m, wave_n);
             __builtin_amdgcn_sched_barrier(0);
             store_stage<C>(lds + (buf ^ 1) * C::kBufBytes, regs[r]);
             __builtin_amdgcn_sched_barrier(0);
-            load_stage<C>(a, w, m, n, nb, m0, n0, clampst(s + 1 + C::kDepth) * C::kKB, regs[r]);
+            const int kb = clampst(s + 1 + C::kDepth) * C::kKB;
+            load_stage<C>(a_tile + kb * 34, w_tile + kb * 18, offs, regs[r]);
             __builtin_amdgcn_sched_barrier(0);
             __syncthreads();
         }
