@@ -147,6 +147,36 @@ template <int W>
 __device__ __forceinline__ int group_sum(int v) {
     return butterfly<W / 2>(v, [](int a, int b) { return a + b; });
 }
+
+// One lane's share of a q8_K super-block (llama_reference.cpp:54-70) when a
+// wavefront quantizes one block, lane l owning elements 4l..4l+3: its four
+// qs bytes, the block's d, and (valid on lanes 4i) bsums[i] = the sum of
+// elements 16i..16i+15. The quantize kernel and the fused GEMVs share it, so
+// their bytes are the same.
+struct Q8KLane {
+    uint32_t q;
+    int bsum;
+    float d;
+};
+__device__ __forceinline__ Q8KLane q8_K_quantize_lane(float4 v) {
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = group_max<64>(amax);
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint32_t q = q8_quantize4(v, id);
+    int s = (int)(int8_t)(q & 0xff) + (int)(int8_t)((q >> 8) & 0xff) + (int)(int8_t)((q >> 16) & 0xff) +
+            (int)(int8_t)(q >> 24);
+    s = group_sum<4>(s);
+    return {q, s, d};
+}
+
+// Stores a lane's share into a 292-byte q8_K block (global or LDS).
+__device__ __forceinline__ void q8_K_store_lane(uint8_t *out, const Q8KLane &r, int lane) {
+    reinterpret_cast<uint32_t *>(out + 4)[lane] = r.q;
+    if ((lane & 3) == 0) reinterpret_cast<int16_t *>(out + 260)[lane >> 2] = (int16_t)r.bsum;
+    if (lane == 0) *reinterpret_cast<float *>(out) = r.d;
+}
+
 template <int W>
 __device__ __forceinline__ float group_sumf(float v) {
     return butterfly<W / 2>(v, [](float a, float b) { return a + b; });

@@ -761,13 +761,14 @@ hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n,
 // fused variant of the m = 2..16 kernel took 7.6 vs 7.4 us at m = 3 and 13.9
 // vs 9.4 us at m = 8.
 bool fused_gemv_supported(int type, int64_t m, int64_t k) {
-    return type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0 && m >= 1 && m <= 2 && k % 64 == 0 &&
-           m * (k / 32) * 34 <= 65536;
+    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return kquant_fused_gemv_fits(type, m, k);
+    return m >= 1 && m <= 2 && k % 64 == 0 && m * (k / 32) * 34 <= 65536;
 }
 
 hipError_t launch_fused_gemv(int type, const void *w, const float *x, float *c, int64_t m, int64_t n, int64_t k,
                              hipStream_t stream) {
-    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return hipErrorInvalidValue;
+    if (type != PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0)
+        return m == 1 ? launch_kquant_fused_gemv(type, w, x, c, n, k, stream) : hipErrorInvalidValue;
     switch (m) {
     case 1: return launch_fused_m<1>(w, x, c, n, k, stream);
     case 2: return launch_fused_m<2>(w, x, c, n, k, stream);

@@ -27,6 +27,10 @@ hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t
 bool fused_gemv_supported(int type, int64_t m, int64_t k);
 hipError_t launch_fused_gemv(int type, const void *w, const float *x, float *c, int64_t m, int64_t n, int64_t k,
                              hipStream_t stream);
+// fused activation quantization + GEMV for q4_K / iq2_xxs (m == 1, the q8_K row in 64 KB of LDS)
+bool kquant_fused_gemv_fits(int type, int64_t m, int64_t k);
+hipError_t launch_kquant_fused_gemv(int type, const void *w, const float *x, float *c, int64_t n, int64_t k,
+                                    hipStream_t stream);
 // q4_K / iq2_xxs GEMV rows m = 9..16 run only with the activations staged in LDS
 bool kquant_gemv_staged_fits(int64_t m, int64_t k);
 hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,

@@ -70,19 +70,7 @@ __global__ __launch_bounds__(256) void quantize_q8_K_kernel(const float *__restr
     const int64_t block = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (block >= nblocks) return;
     const float4 v = *reinterpret_cast<const float4 *>(x + block * 256 + lane * 4);
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = group_max<64>(amax);
-    const float d = amax / 127.0f;
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    const uint32_t q = q8_quantize4(v, id);
-    int s = (int)(int8_t)(q & 0xff) + (int)(int8_t)((q >> 8) & 0xff) + (int)(int8_t)((q >> 16) & 0xff) +
-            (int)(int8_t)(q >> 24);
-    s = group_sum<4>(s);
-
-    uint8_t *out = y + block * 292;
-    reinterpret_cast<uint32_t *>(out + 4)[lane] = q;
-    if ((lane & 3) == 0) reinterpret_cast<int16_t *>(out + 260)[lane >> 2] = (int16_t)s;
-    if (lane == 0) *reinterpret_cast<float *>(out) = d;
+    q8_K_store_lane(y + block * 292, q8_K_quantize_lane(v), lane);
 }
 
 }  // namespace

@@ -531,6 +531,29 @@ def test_compute_fused_gemv(hip, torch_gpu, oracle, m, n, k):
     assert torch.equal(fused, unfused)
 
 
+# q4_K / iq2_xxs at m == 1 quantize the q8_K row inside the GEMV's workgroups
+# while it (with iq2_xxs's tables) fits 64 KB of LDS: k up to 56064 for q4_K
+# (224 blocks), 53760 for iq2_xxs (210 blocks); longer rows quantize first.
+@pytest.mark.parametrize("qtype", [1, 2])
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (1, 300, 256), (1, 129, 7680), (1, 77, 53760), (1, 50, 57344),
+                                   (2, 64, 1536)])
+def test_compute_fused_kquant_gemv(hip, torch_gpu, oracle, qtype, m, n, k):
+    """pfng_hip_compute with q4_K / iq2_xxs: within the bound of the oracle's
+    compute, and equal to the separate quantize_q8_K + GEMV result bit for bit
+    (same q8_K bytes, sums in the same order)."""
+    torch = torch_gpu
+    say(f"fused kquant gemv type={qtype} m={m} n={n} k={k}")
+    act, w = oracle.create_input(qtype, m, n, k, seed=m + n + k)
+    wt, at = dev(torch, w), dev(torch, act)
+    fused = hip.compute(qtype, at, wt, n)
+    torch.cuda.synchronize()
+    aq = oracle.quantize_q8_K(act)
+    check_close(oracle, qtype, fused.cpu().numpy(), w, aq, m, n, k, label=f"fused type={qtype} m={m} n={n} k={k}")
+    unfused = hip.mul_mat(qtype, wt, hip.quantize_q8_K(at), m, n, k, path=hip.PATH_GEMV)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, unfused)
+
+
 def test_wrappers_reject_short_or_strided_buffers(hip, torch_gpu):
     """The C-ABI takes bare pointers; the Python wrappers check sizes, layout
     and device first and raise before anything is launched."""
