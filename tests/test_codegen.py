@@ -1,7 +1,7 @@
 """Instruction-order checks on the gfx950 assembly of kernels whose
 synchronisation depends on it (CPU only: hipcc cross-compiles here).
 
-gemv_q4_0_m1_kernel<true> and gemv_q4_K_kernel<1, true> copy the activation
+gemv_q4_0_m1_kernel<true> and gemv_q4_K_kernel<1, true, false> copy the activation
 row into LDS with direct loads (global_load_lds_*) and then issue the loads
 of each lane's first weight step before waiting; the wait before the
 workgroup barrier is `s_waitcnt vmcnt(3)`, which covers the copies only
@@ -80,7 +80,7 @@ def test_checker_rejects_sunk_loads():
 
 @pytest.mark.skipif(not os.path.exists(HIPCC) or shutil.which("make") is None, reason="needs hipcc and make")
 @pytest.mark.parametrize("source,kernel", [("gemv.hip", "gemv_q4_0_m1_kernelILb1E"),
-                                           ("gemv_kquant.hip", "gemv_q4_K_kernelILi1ELb1E")])
+                                           ("gemv_kquant.hip", "gemv_q4_K_kernelILi1ELb1ELb0E")])
 def test_m1_gemv_copy_precedes_wait(source, kernel):
     out = os.path.join(PKG_DIR, "_build", source + ".s")
     subprocess.run(["make", "-s", "-C", PKG_DIR, out], check=True, capture_output=True, timeout=600)
