@@ -70,7 +70,7 @@ struct KqConfig {
     static constexpr int kBufBytes = kWmin + (kQ4K ? BN * 16 : 0);
     static constexpr int kSliceBytes = 2 * kBufBytes;                // a slice's two stage buffers
     static constexpr int kGrid = WS * kSliceBytes;                   // iq2: 256 x 8-byte grid magnitudes
-    static constexpr int kLdsBytes = kGrid + (kQ4K ? 0 : 256 * 8);
+    static constexpr int kLdsBytes = kGrid + (kQ4K ? 0 : 256 * 8 + 128 * 8);
     static constexpr int kAllThreads = kThreads * WS;
     // global -> register tasks per stage: each activation row in kActE parts
     // (2 or 4) of its 128 int8 and 8 bsums, each weight row per sub-block
@@ -104,21 +104,55 @@ struct KqRegs {
 
 constexpr int kQ8KBytes = 292, kQ4KBytes = 144, kIq2Bytes = 66;
 
-// Loads of stage (b, h): super-block b, half h. Rows are clamped at the matrix
-// edge so that every load is unconditional and in bounds.
+// Byte offsets of a thread's load tasks from the tile's first row at the
+// stage's super-block: fixed over the K loop (rows past the matrix edge are
+// clamped to its last row), so each stage's loads are a uniform base plus
+// these 32-bit offsets. BM * nb * 292 < 2^32 for any k the library takes.
 template <class C>
-__device__ __forceinline__ void kq_load(const uint8_t *__restrict__ a, const uint8_t *__restrict__ w, int m, int n,
-                                        int nb, int m0, int n0, int b, int h, int tid, KqRegs<C> &r) {
+struct KqOffsets {
+    uint32_t a[C::kActPT];  // activation row + part e's qs dwords
+    uint32_t w[C::kWPT];    // weight row + sub-block e (iq2_xxs: its first byte past d)
+};
+
+template <class C>
+__device__ __forceinline__ KqOffsets<C> kq_offsets(int m, int n, int nb, int m0, int n0, int tid) {
+    KqOffsets<C> o;
 #pragma unroll
     for (int it = 0; it < C::kActPT; ++it) {
         const int task = tid + it * C::kThreads;
         const int row = m0 + task / C::kActE, e = task % C::kActE;
         const int lrow = row < m ? row : m - 1;
-        const uint8_t *blk = a + ((size_t)lrow * nb + b) * kQ8KBytes;
-        const uint32_t *qs = reinterpret_cast<const uint32_t *>(blk + 4 + 128 * h + 4 * C::kQsDw * e);
+        o.a[it] = (uint32_t)(lrow - m0) * (uint32_t)nb * (uint32_t)kQ8KBytes + 4u * C::kQsDw * (uint32_t)e;
+    }
+#pragma unroll
+    for (int it = 0; it < C::kWPT; ++it) {
+        const int task = tid + it * C::kThreads;
+        const int row = n0 + task / C::kSub, e = task % C::kSub;
+        const int lrow = row < n ? row : n - 1;
+        o.w[it] = (uint32_t)(lrow - n0) * (uint32_t)nb * (uint32_t)(C::kQ4K ? kQ4KBytes : kIq2Bytes) +
+                  (uint32_t)(C::kQ4K ? 16 * e : 2 + 8 * e);
+    }
+    return o;
+}
+
+// Loads of stage (b, H): super-block b, half H. a_t / w_t: the tile's first
+// activation / weight row (uniform). Rows are clamped at the matrix edge so
+// that every load is unconditional and in bounds.
+template <class C, int H>
+__device__ __forceinline__ void kq_load(const uint8_t *__restrict__ a_t, const uint8_t *__restrict__ w_t, int b,
+                                        const KqOffsets<C> &o, int tid, KqRegs<C> &r) {
+    const uint8_t *a_st = a_t + (size_t)b * kQ8KBytes;
+    const uint8_t *w_st = w_t + (size_t)b * (C::kQ4K ? kQ4KBytes : kIq2Bytes);
+#pragma unroll
+    for (int it = 0; it < C::kActPT; ++it) {
+        const int task = tid + it * C::kThreads;
+        const int e = task % C::kActE;
+        const uint8_t *part = a_st + o.a[it];  // qs dwords of part e at part + 4 + 128 H
+        const uint8_t *blk = part - 4 * C::kQsDw * e;
+        const uint32_t *qs = reinterpret_cast<const uint32_t *>(part + 4 + 128 * H);
 #pragma unroll
         for (int i = 0; i < C::kQsDw; ++i) r.aq[it][i] = qs[i];
-        const uint32_t *bs = reinterpret_cast<const uint32_t *>(blk + 260 + 16 * h + 4 * C::kBsDw * e);
+        const uint32_t *bs = reinterpret_cast<const uint32_t *>(blk + 260 + 16 * H + 4 * C::kBsDw * e);
         if constexpr (C::kQ4K) {
 #pragma unroll
             for (int i = 0; i < C::kBsDw; ++i) r.ab[it][i] = bs[i];
@@ -128,12 +162,11 @@ __device__ __forceinline__ void kq_load(const uint8_t *__restrict__ a, const uin
 #pragma unroll
     for (int it = 0; it < C::kWPT; ++it) {
         const int task = tid + it * C::kThreads;
-        const int row = n0 + task / C::kSub, e = task % C::kSub;
-        const int lrow = row < n ? row : n - 1;
+        const int e = task % C::kSub;
         if constexpr (C::kQ4K) {
-            const uint8_t *blk = w + ((size_t)lrow * nb + b) * kQ4KBytes;
-            const uint32_t *qs = reinterpret_cast<const uint32_t *>(blk + 16 + 64 * h + 16 * e);
-            const uint32_t *hd = reinterpret_cast<const uint32_t *>(blk);
+            const uint8_t *sub16 = w_st + o.w[it];  // = block + 16 e
+            const uint32_t *qs = reinterpret_cast<const uint32_t *>(sub16 + 16 + 64 * H);
+            const uint32_t *hd = reinterpret_cast<const uint32_t *>(sub16 - 16 * e);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 r.wq[it][i] = qs[i];
@@ -142,15 +175,14 @@ __device__ __forceinline__ void kq_load(const uint8_t *__restrict__ a, const uin
         } else {
             // 66-byte blocks are only 2-byte aligned: read the covering dwords
             // and a trailing half-word, never past the sub-block's last byte
-            const size_t base = ((size_t)lrow * nb + b) * kIq2Bytes;
-            const size_t o = base + 2 + 32 * h + 8 * e;
-            const uint32_t *p4 = reinterpret_cast<const uint32_t *>(w + (o & ~(size_t)3));
+            const uint8_t *sb = w_st + o.w[it] + 32 * H;  // sub-block e of half H
+            const bool sh = (reinterpret_cast<uintptr_t>(sb) & 3) != 0;
+            const uint32_t *p4 = reinterpret_cast<const uint32_t *>(sb - (sh ? 2 : 0));
             const uint32_t d0 = p4[0], d1 = p4[1];
-            const uint32_t tail = *reinterpret_cast<const uint16_t *>(w + o + 6);
-            const uint32_t sh = (uint32_t)(o & 3) * 8;  // 0 or 16 bits
+            const uint32_t tail = *reinterpret_cast<const uint16_t *>(sb + 6);
             r.wq[it][0] = sh ? __builtin_amdgcn_alignbyte(d1, d0, 2) : d0;
             r.wq[it][1] = sh ? ((d1 >> 16) | (tail << 16)) : d1;
-            r.wh[it][0] = *reinterpret_cast<const uint16_t *>(w + base);
+            r.wh[it][0] = *reinterpret_cast<const uint16_t *>(sb - 32 * H - 2 - 8 * e);
         }
     }
 }
@@ -170,6 +202,7 @@ __device__ __forceinline__ void q4_K_scale_min(const uint32_t hd[4], int j, uint
 
 template <class C>
 __device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int h, int tid, const KqRegs<C> &r) {
+    const uint8_t *signs = grid + 256 * 8;
 #pragma unroll
     for (int it = 0; it < C::kActPT; ++it) {
         const int task = tid + it * C::kThreads;
@@ -221,23 +254,19 @@ __device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int 
             *reinterpret_cast<float *>(lds + C::kWdm + row * 4) = fp16_to_f32(r.wh[it][0] >> 16);
         } else {
             // iq2_xxs sub-block (kernels/common/iq2_xxs.h:29-41): four groups of
-            // 8 values, magnitudes from the grid, sign bit j of group g is bit
-            // j of (idx | parity(idx) << 7) with idx the 7-bit field g of the
-            // last dword, scale 2 * (bits 28..31) + 1
+            // 8 values, magnitudes from the grid, signs from the mask table
+            // (0xff in byte j where bit j of idx | parity(idx) << 7 is set, idx
+            // the 7-bit field g of the last dword), scale 2 * (bits 28..31) + 1
             const uint32_t gidx = r.wq[it][0], ss = r.wq[it][1];
             uint32_t out[8];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const uint2 mag = *reinterpret_cast<const uint2 *>(grid + ((gidx >> (8 * g)) & 0xffu) * 8);
-                const uint32_t idx = (ss >> (7 * g)) & 0x7fu;
-                const uint32_t sgn = idx | ((__builtin_popcount(idx) & 1u) << 7);
-                // spread sign bits 0..3 / 4..7 to the low bit of each byte
-                const uint32_t b0 = ((sgn & 0xfu) * 0x00204081u) & 0x01010101u;
-                const uint32_t b1 = (((sgn >> 4) & 0xfu) * 0x00204081u) & 0x01010101u;
+                const uint2 neg = *reinterpret_cast<const uint2 *>(signs + ((ss >> (7 * g)) & 0x7fu) * 8);
                 // magnitudes are >= 8, so (x ^ 0xff) + 1 negates a byte without
                 // a carry into its neighbour
-                out[2 * g] = (mag.x ^ (b0 * 0xffu)) + b0;
-                out[2 * g + 1] = (mag.y ^ (b1 * 0xffu)) + b1;
+                out[2 * g] = (mag.x ^ neg.x) + (neg.x & 0x01010101u);
+                out[2 * g + 1] = (mag.y ^ neg.y) + (neg.y & 0x01010101u);
             }
             uint4 *dst = reinterpret_cast<uint4 *>(wrow + 32 * e);
             dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
@@ -376,8 +405,10 @@ __device__ __forceinline__ void kq_epilogue(const uint8_t *buf, KqAcc<C> &A, int
             // activation scales of the lane's 16 rows: rows 8g + 4lh + 0..3
             const float *adp = reinterpret_cast<const float *>(buf + C::kAd) + wave_m * C::TM * 32 + tm * 32 + 4 * lh;
             f32x4 ad4[4];
+            if constexpr (C::kQ4K) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) ad4[g] = *reinterpret_cast<const f32x4 *>(adp + 8 * g);
+                for (int g = 0; g < 4; ++g) ad4[g] = *reinterpret_cast<const f32x4 *>(adp + 8 * g);
+            }
 #pragma unroll
             for (int tn = 0; tn < C::TN; ++tn) {
                 const int wr = wave_n * C::TN * 32 + tn * 32 + li;
@@ -391,9 +422,15 @@ __device__ __forceinline__ void kq_epilogue(const uint8_t *buf, KqAcc<C> &A, int
                         A.acc[tm][tn][q] = fmaf(ad4[q / 4][q % 4], x, A.acc[tm][tn][q]);
                     }
                 } else {
+                    // P = ad (x) d on the matrix core: lane l supplies ad of row
+                    // l % 32 and d of column l % 32 at K index l / 32, and the
+                    // upper lanes' d is zero, so P[r][c] = ad_r * d_c, the
+                    // correctly rounded product
+                    const float adl = reinterpret_cast<const float *>(buf + C::kAd)[wave_m * C::TM * 32 + tm * 32 + li];
+                    const f32x16 pr = __builtin_amdgcn_mfma_f32_32x32x2f32(adl, lh ? 0.0f : d, (f32x16){}, 0, 0, 0);
 #pragma unroll
                     for (int q = 0; q < 16; ++q)
-                        A.acc[tm][tn][q] = fmaf(d * ad4[q / 4][q % 4], (float)A.s0[tm][tn][q], A.acc[tm][tn][q]);
+                        A.acc[tm][tn][q] = fmaf(pr[q], (float)A.s0[tm][tn][q], A.acc[tm][tn][q]);
                 }
             }
         }
@@ -434,6 +471,16 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
             }
             *reinterpret_cast<uint2 *>(grid + 8 * e) = make_uint2(v[0], v[1]);
         }
+        // sign masks (the reference's ksigns_iq2xs, ggml_min.h:58-67: byte
+        // idx | parity(idx) << 7), one mask byte per element
+        for (int e = threadIdx.x; e < 128; e += C::kAllThreads) {
+            const uint32_t sgn = (uint32_t)e | ((__builtin_popcount((uint32_t)e) & 1u) << 7);
+            uint32_t v[2] = {0, 0};
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if ((sgn >> j) & 1u) v[j / 4] |= 0xffu << (8 * (j % 4));
+            *reinterpret_cast<uint2 *>(grid + 256 * 8 + 8 * e) = make_uint2(v[0], v[1]);
+        }
         __syncthreads();
     }
 
@@ -448,12 +495,16 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
     // other buffer and the loads of the stage after it are issued. Stores and
     // loads are unconditional (the super-block index is clamped at the end);
     // every slice runs the same number of iterations, and one whose
-    // super-block is past the end skips only the arithmetic.
+    // super-block is past the end skips only the arithmetic. (Loads issued two
+    // stages ahead, from a register set per half, measured no faster on c2/c3.)
     KqRegs<C> regs;
     const int last = nb - 1;
-    kq_load<C>(a, w, m, n, nb, m0, n0, slice < nb ? slice : last, 0, tid, regs);
+    const uint8_t *a_t = a + (size_t)m0 * nb * kQ8KBytes;
+    const uint8_t *w_t = w + (size_t)n0 * nb * (C::kQ4K ? kQ4KBytes : kIq2Bytes);
+    const KqOffsets<C> offs = kq_offsets<C>(m, n, nb, m0, n0, tid);
+    kq_load<C, 0>(a_t, w_t, slice < nb ? slice : last, offs, tid, regs);
     kq_store<C>(buf0, grid, 0, tid, regs);
-    kq_load<C>(a, w, m, n, nb, m0, n0, slice < nb ? slice : last, 1, tid, regs);
+    kq_load<C, 1>(a_t, w_t, slice < nb ? slice : last, offs, tid, regs);
     __syncthreads();
     const int iters = (nb + C::kWS - 1) / C::kWS;
     for (int it = 0; it < iters; ++it) {
@@ -465,7 +516,7 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
         __builtin_amdgcn_sched_barrier(0);
         kq_store<C>(buf1, grid, 1, tid, regs);
         __builtin_amdgcn_sched_barrier(0);
-        kq_load<C>(a, w, m, n, nb, m0, n0, bn, 0, tid, regs);
+        kq_load<C, 0>(a_t, w_t, bn, offs, tid, regs);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
         if (mine) {
@@ -475,7 +526,7 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
         __builtin_amdgcn_sched_barrier(0);
         kq_store<C>(buf0, grid, 0, tid, regs);
         __builtin_amdgcn_sched_barrier(0);
-        kq_load<C>(a, w, m, n, nb, m0, n0, bn, 1, tid, regs);
+        kq_load<C, 1>(a_t, w_t, bn, offs, tid, regs);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
     }
