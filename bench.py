@@ -340,7 +340,7 @@ def main():
     head = measure(torch, pkg, "c1: q4_0 x q8_0 GEMV M=1 N=4096 K=4096, 32 rotating weight copies (302 MB)", 0, 1,
                    4096, 4096, steps, args.warmup, samples, ref, "gemv_q4_0_m1_kernel", copies=32)
     gemm = measure(torch, pkg, "c0: q4_0 x q8_0 GEMM M=480 N=1536 K=1536", 0, 480, 1536, 1536, args.gemm_steps, 256,
-                   samples, ref, "gemm_q4_0_kernel")
+                   samples, ref, "gemm_q4_0_wt_kernel")
     q4k = measure(torch, pkg, "c2: q4_K x q8_K GEMM M=480 N=1536 K=1536", 1, 480, 1536, 1536, args.gemm_steps, 256,
                   samples, ref, "gemm_kq_kernel<q4_K>")
     iq2 = None

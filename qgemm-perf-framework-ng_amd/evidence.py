@@ -45,7 +45,7 @@ MFMA_CYCLES_PER_ITEM = 32  # v_mfma_i32_32x32x32_i8 at the 5.0 POPS peak
 
 # name, qtype, m, n, k, input variant, kernel-name substring, bound
 CONFIGS = {
-    "c0": ("q4_0 x q8_0 GEMM M=480 N=1536 K=1536", 0, 480, 1536, 1536, 0, "gemm_q4_0_kernel", "mfma"),
+    "c0": ("q4_0 x q8_0 GEMM M=480 N=1536 K=1536", 0, 480, 1536, 1536, 0, "gemm_q4_0_wt_kernel", "mfma"),
     "c1": ("q4_0 x q8_0 GEMV M=1 N=4096 K=4096, 32 rotating weight copies", 0, 1, 4096, 4096, 0,
            "gemv_q4_0_m1_kernel", "hbm"),
     "c2": ("q4_K x q8_K GEMM M=480 N=1536 K=1536", 1, 480, 1536, 1536, 0, "gemm_kq_kernel", "mfma"),
