@@ -171,15 +171,16 @@ def test_naive_bit_exact(hip, torch_gpu, oracle, qtype, m, n, k):
 
 @pytest.mark.parametrize("m", [1, 2, 3, 5, 7, 8, 9, 12, 13, 15, 16])
 @pytest.mark.parametrize("n,k", [(4096, 4096), (257, 1536), (64, 256), (33, 8192), (40, 65536), (129, 7680),
-                                 (77, 320), (50, 64), (21, 20480), (37, 6144), (48, 2048)])
+                                 (77, 320), (50, 64), (21, 20480), (37, 6144), (48, 2048), (100, 4096)])
 def test_gemv_q4_0(hip, torch_gpu, oracle, m, n, k):
     """m = 1 (block pair per lane; the activation row copied into LDS in
     rounds of 16 KB up to 64 KB, k = 20480 taking two rounds, a dword tail at
     k = 320 and 64), m = 2..16 with the activations staged in LDS
     (m * (k / 64) * 76 + 16 <= 160 KB), m = 2..8 beyond that (groups of 8
     blocks per lane); the 16x16 MFMA tile kernel with 16 waves from m = 9 at
-    k = 4096 and 8192 (m = 9 only: its slices fit the LDS), with 8 waves from
-    m = 12 at k = 6144 (37 columns: a partial tile) and 2048."""
+    k = 4096 (two-half copy, 100 columns: a partial tile) and 8192 (m = 9 only:
+    its slices fit the LDS), with 8 waves from m = 12 at k = 6144 (37 columns: a
+    partial tile) and 2048."""
     torch = torch_gpu
     if m > 8 and m * (k // 64) * 76 + 16 > 160 * 1024:
         pytest.skip("m > 8 takes the GEMV only while the staged activations fit in LDS")
