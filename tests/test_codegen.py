@@ -87,3 +87,55 @@ def test_m1_gemv_copy_precedes_wait(source, kernel):
     with open(out) as f:
         asm = f.read()
     check_copy_then_wait(_kernel_lines(asm, kernel))
+
+
+def dma_m0_from_vector(lines: list[str]) -> list[str]:
+    """Direct-to-LDS loads whose LDS address (M0) was set from a
+    v_readfirstlane of a vector register: the compiler does this when it merges
+    copy sites of divergent paths into one, and lanes of the other path then
+    write to the first active lane's address."""
+    bad, rfl = [], {}
+    for i, t in enumerate(lines):
+        m = re.match(r"s_mov_b32 m0, (s\d+)", t)
+        if m and m.group(1) in rfl and any("load_lds" in u for u in lines[i:i + 6]):
+            bad.append(f"{rfl[m.group(1)]} -> {t}")
+        # a scalar register redefined by any other instruction no longer
+        # holds the read-first-lane value
+        d = re.match(r"\S+\s+s(?:\[(\d+):(\d+)\]|(\d+)\b)", t)
+        if d:
+            lo = int(d.group(1) or d.group(3))
+            hi = int(d.group(2) or d.group(3))
+            for r in range(lo, hi + 1):
+                rfl.pop(f"s{r}", None)
+        m = re.match(r"v_readfirstlane_b32 (s\d+),", t)
+        if m:
+            rfl[m.group(1)] = t
+    return bad
+
+
+def test_dma_checker_flags_vector_m0():
+    """The checker itself: an M0 taken from a readfirstlane before a copy."""
+    good = ["s_add_i32 m0, s21, 0x400", "global_load_lds_dwordx4 v[2:3], off"]
+    assert dma_m0_from_vector(good) == []
+    bad = ["v_add_u32_e32 v1, s21, v10", "v_readfirstlane_b32 s0, v1", "s_mov_b32 m0, s0",
+           "global_load_lds_dwordx4 v[6:7], off"]
+    assert dma_m0_from_vector(bad)
+    # the wave index read from lane 0, then the register reused for a scalar base
+    reused = ["v_readfirstlane_b32 s14, v0", "s_lshr_b32 s13, s14, 6", "s_add_i32 s14, s13, 0x400",
+              "s_mov_b32 m0, s14", "global_load_lds_dwordx4 v[2:3], off"]
+    assert dma_m0_from_vector(reused) == []
+    pair = ["v_readfirstlane_b32 s15, v3", "s_load_dwordx2 s[14:15], s[0:1], 0x0", "s_mov_b32 m0, s15",
+            "global_load_lds_dwordx4 v[2:3], off"]
+    assert dma_m0_from_vector(pair) == []
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC) or shutil.which("make") is None, reason="needs hipcc and make")
+@pytest.mark.parametrize("source", ["gemv.hip", "gemv_kquant.hip", "gemm_small.hip"])
+def test_dma_lds_address_is_scalar(source):
+    """Every direct-to-LDS copy in the kernels that use them takes its LDS
+    address from scalar code (a workgroup- or wave-uniform base)."""
+    out = os.path.join(PKG_DIR, "_build", source + ".s")
+    subprocess.run(["make", "-s", "-C", PKG_DIR, out], check=True, capture_output=True, timeout=600)
+    with open(out) as f:
+        lines = [ln.split(";")[0].strip() for ln in f.read().splitlines()]
+    assert dma_m0_from_vector(lines) == []
