@@ -35,7 +35,7 @@ constexpr int kQ8KBytes = 292, kQ4KBytes = 144, kIq2Bytes = 66;
 // bytes (kernels/iq2_xxs-q8_K-RVV-common/ggml_min.h:69-134: two bits per byte
 // select 8, 25 or 43), so a workgroup fills its LDS copy with one 8-byte load
 // and store per thread.
-struct Iq2Grid {
+struct alignas(16) Iq2Grid {
     uint32_t v[256][2];
 };
 constexpr Iq2Grid expand_iq2_grid() {
@@ -53,7 +53,7 @@ __constant__ Iq2Grid kIq2Grid = expand_iq2_grid();
 // Sign masks: entry i is 0xff in byte j where bit j of i | parity(i) << 7 is
 // set (the reference's ksigns_iq2xs, ggml_min.h:58-67, which stores exactly
 // that byte, expanded to one mask byte per element).
-struct Iq2Signs {
+struct alignas(16) Iq2Signs {
     uint32_t v[128][2];
 };
 constexpr Iq2Signs expand_iq2_signs() {
@@ -934,6 +934,183 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_kernel(const u
     }
 }
 
+// Two-half copies for the GEMVs with one super-block per wave (k == 4096,
+// m = 9..16). A wave copies its super-block of the tile's 16 weight rows and
+// of the m activation rows in 16-byte chunks, each row from the 16-byte
+// boundary at or before its block (rows are 16 blocks long, so that offset
+// depends on the wave only). Half h holds, for each weight row, chunks
+// [wc_h, wc_h + wn_h) of the row's copy, then, for each activation row, chunks
+// [ac_h, ac_h + an_h) (wc_0 = ac_0 = 0). Half 1 starts one chunk before the end
+// of half 0 so that no value straddles the halves, and every row length is an
+// odd number of chunks: rows whose LDS stride is 16 bytes times an odd number
+// put the 16 rows of a tile on 8 different bank groups (2-way conflicts at
+// most, against up to 16-way for strides of 8 chunks). The chunks of both halves
+// are one flat run in LDS, copied 64 per instruction with every lane active:
+// lanes past the last chunk repeat it into a pad, so no lane is predicated (a
+// predicated direct-to-LDS copy may be merged by the compiler into one whose
+// LDS address comes from a single lane). Loads complete in issue order, so a
+// wave multiplies half 0 after waiting for the instructions that wrote it,
+// while half 1 is still in flight.
+struct Q4KRun {  // 144-byte weight blocks (16-byte aligned), 292-byte q8_K blocks
+    static constexpr int wn0 = 5, wc1 = 4, wn1 = 5, an0 = 9, ac1 = 8, an1 = 11;
+    static constexpr uint32_t wrow = 16 * 144, arow = 16 * kQ8KBytes;
+};
+struct Iq2Run {  // 66-byte weight blocks; no bsums needed
+    static constexpr int wn0 = 3, wc1 = 2, wn1 = 3, an0 = 9, ac1 = 8, an1 = 9;
+    static constexpr uint32_t wrow = 16 * kIq2Bytes, arow = 16 * kQ8KBytes;
+};
+
+template <class R> __host__ __device__ constexpr int sb_half0(int m) { return 16 * R::wn0 + m * R::an0; }
+template <class R> __host__ __device__ constexpr int sb_half1(int m) { return 16 * R::wn1 + m * R::an1; }
+template <class R> __host__ __device__ constexpr int sb_copies(int m) { return (sb_half0<R>(m) + sb_half1<R>(m) + 63) / 64; }
+
+// Byte offset of LDS chunk p of a wave's run: from the copy start of the
+// wave's block in the tile's first weight row, or (bit 31 set) in activation
+// row 0. Rows past the last weight row repeat it.
+template <class R, int M>
+__device__ __forceinline__ uint32_t sb_chunk(int p, int rows) {
+    constexpr int kH0 = sb_half0<R>(M), kH1 = sb_half1<R>(M);
+    if (p >= kH0 + kH1) p = kH0 + kH1 - 1;
+    uint32_t off;
+    if (p < 16 * R::wn0) {
+        const int row = p / R::wn0;
+        off = (uint32_t)(row < rows ? row : rows - 1) * R::wrow + 16 * (p - row * R::wn0);
+    } else if (p < kH0) {
+        const int c = p - 16 * R::wn0, row = c / R::an0;
+        off = 0x80000000u | ((uint32_t)row * R::arow + 16 * (c - row * R::an0));
+    } else if (p < kH0 + 16 * R::wn1) {
+        const int c = p - kH0, row = c / R::wn1;
+        off = (uint32_t)(row < rows ? row : rows - 1) * R::wrow + 16 * (R::wc1 + c - row * R::wn1);
+    } else {
+        const int c = p - kH0 - 16 * R::wn1, row = c / R::an1;
+        off = 0x80000000u | ((uint32_t)row * R::arow + 16 * (R::ac1 + c - row * R::an1));
+    }
+    return off;
+}
+
+// Issues a wave's whole run; wsrc / asrc: copy starts of its blocks in the
+// tile's first weight row and in activation row 0.
+template <class R, int M>
+__device__ __forceinline__ void sb_copy(const uint8_t *wsrc, const uint8_t *asrc, uint8_t *base, int lane, int rows) {
+#pragma unroll
+    for (int i = 0; i < sb_copies<R>(M); ++i) {
+        const uint32_t off = sb_chunk<R, M>(64 * i + lane, rows);
+        const uint8_t *src = (off >> 31) ? asrc + (off & 0x7fffffffu) : wsrc + off;
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(base + i * 1024), 16, 0, 0);
+    }
+}
+
+// q4_K: the tile of gemv_q4_K_mfma_kernel with one super-block per wave and
+// two-half copies. The weight blocks are 16-byte aligned; the q8_K block of
+// wave v starts o = 4 (v % 4) bytes past a 16-byte boundary and is copied as
+// 19 chunks from there. Half 0: chunks 0..4 of every weight row (header and
+// the nibbles of sub-blocks 0..3) and 0..8 of every activation row (d and the
+// bytes of sub-blocks 0..3); half 1: weight chunks 4..8 (the nibbles of
+// sub-blocks 4..7) and activation chunks 8..18 (bytes 132..291, bsums
+// included, lie at or past copy byte 128). The min term
+// sum_j m_j * bsum_j is one v_mfma_f32_16x16x16_f16 per super-block: the bsums
+// (|bsum| <= 16 * 127 < 2048) and the 6-bit mins are exact in fp16 and the
+// sums of products exact in fp32, so IM equals the integer sum.
+__host__ __device__ constexpr int q4k_sb_lds_bytes(int m) { return kKqMfWaves * sb_copies<Q4KRun>(m) * 1024; }
+
+template <int M>
+__global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_sb_kernel(const uint8_t *__restrict__ w,
+                                                                            const uint8_t *__restrict__ a,
+                                                                            float *__restrict__ c, int n) {
+    static_assert(M >= 1 && M <= 16, "one 16-row tile of activation rows");
+    constexpr int nsb = kKqMfWaves;  // k == 4096
+    using R = Q4KRun;
+    constexpr int kH0 = sb_half0<R>(M);
+    constexpr int kCopies = sb_copies<R>(M);
+    constexpr int kAfterHalf0 = kCopies - (kH0 + 63) / 64;  // instructions issued after those writing half 0
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int n0 = blockIdx.x * 16;
+    const int o = 4 * (wave & 3);
+    uint8_t *base = lds + wave * kCopies * 1024;
+    sb_copy<R, M>(w + ((size_t)n0 * nsb + wave) * 144, a + wave * kQ8KBytes - o, base, lane, n - n0);
+    const uint8_t *w0 = base, *a0 = w0 + 16 * R::wn0 * 16;  // half 0: weight rows of 80 B, activation rows of 144 B
+    const uint8_t *w1 = base + kH0 * 16, *a1 = w1 + 16 * R::wn1 * 16;  // half 1: 80 B, 176 B
+    const int li = lane & 15, q = lane >> 4;
+    const int arow = li < M ? li : M - 1;
+    int orow[4];  // activation rows of this lane's four results (clamped)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) orow[r] = 4 * q + r < M ? 4 * q + r : M - 1;
+    // activation byte b of row r: half 0 at a0 + 144 r + o + b (b < 144 - o), half 1 at a1 + 176 r + o + b - 128 (b >= 128 - o)
+    const uint8_t *ar0 = a0 + arow * (R::an0 * 16) + o, *ar1 = a1 + arow * (R::an1 * 16) + o - R::ac1 * 16;
+    int is[4] = {0, 0, 0, 0};
+    uint32_t scw[2], mnw[2];
+    auto sub = [&](int j, uint32_t x0, uint32_t x1, uint32_t y0, uint32_t y1) {
+        const uint32_t v0 = (j & 1 ? x0 >> 4 : x0) & 0x0f0f0f0fu;
+        const uint32_t v1 = (j & 1 ? x1 >> 4 : x1) & 0x0f0f0f0fu;
+        const i32x4 sj = mfma_i8_16x16x32((uint64_t)y0 | ((uint64_t)y1 << 32), (uint64_t)v0 | ((uint64_t)v1 << 32),
+                                          (i32x4){0, 0, 0, 0});
+        const int sc = (int)((scw[j / 4] >> (8 * (j % 4))) & 0xffu);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) is[r] += __mul24(sc, sj[r]);
+    };
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfterHalf0) : "memory");  // half 0 has landed
+    // the header as four dwords: a typed read, so the compiler adds no wait for all copies before it
+    const uint32_t *hp = reinterpret_cast<const uint32_t *>(w0 + li * (R::wn0 * 16));
+    const uint4 hd = make_uint4(hp[0], hp[1], hp[2], hp[3]);
+    // scales (bytes 0..3: sub-blocks 0..3, 4..7: 4..7) and mins, as q4_K_scale_min_pair
+    scw[0] = hd.y & 0x3f3f3f3fu;
+    scw[1] = (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u);
+    mnw[0] = hd.z & 0x3f3f3f3fu;
+    mnw[1] = ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u);
+    float ad[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ad[r] = *reinterpret_cast<const float *>(a0 + orow[r] * (R::an0 * 16) + o);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // weight nibbles at block byte 16 + 32 (j / 2) + 4q (+ 16)
+        const uint8_t *wq = w0 + li * (R::wn0 * 16) + 16 + 32 * (j / 2) + 4 * q;
+        const uint8_t *aq = ar0 + 4 + 32 * j + 4 * q;
+        sub(j, *reinterpret_cast<const uint32_t *>(wq), *reinterpret_cast<const uint32_t *>(wq + 16),
+            *reinterpret_cast<const uint32_t *>(aq), *reinterpret_cast<const uint32_t *>(aq + 16));
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int j = 4; j < 8; ++j) {  // weight nibbles at block byte 16 + 32 (j / 2) + 4q (+ 16), half-1 rows from byte 64
+        const uint8_t *wq = w1 + li * (R::wn1 * 16) + 16 + 32 * (j / 2) + 4 * q - 16 * R::wc1;
+        const uint8_t *aq = ar1 + 4 + 32 * j + 4 * q;
+        sub(j, *reinterpret_cast<const uint32_t *>(wq), *reinterpret_cast<const uint32_t *>(wq + 16),
+            *reinterpret_cast<const uint32_t *>(aq), *reinterpret_cast<const uint32_t *>(aq + 16));
+    }
+    // IM: A = bsums 4q..4q+3 of activation row arow, B = m_(2q), m_(2q), m_(2q+1), m_(2q+1) of weight row li
+    const uint32_t *bsp = reinterpret_cast<const uint32_t *>(ar1 + 260 + 8 * q);
+    const uint32_t b01 = bsp[0], b23 = bsp[1];
+    const f16x4 bs = {(_Float16)(short)(b01 & 0xffffu), (_Float16)(short)(b01 >> 16), (_Float16)(short)(b23 & 0xffffu),
+                      (_Float16)(short)(b23 >> 16)};
+    const uint32_t mp = (q & 2 ? mnw[1] : mnw[0]) >> (16 * (q & 1));
+    const _Float16 m0 = (_Float16)(int)(mp & 0xffu), m1 = (_Float16)(int)((mp >> 8) & 0xffu);
+    const f16x4 mm = {m0, m0, m1, m1};
+    const f32x4 im = __builtin_amdgcn_mfma_f32_16x16x16f16(bs, mm, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    const float d = fp16_to_f32(hd.x & 0xffffu), dmin = fp16_to_f32(hd.x >> 16);
+    float acc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = ad[r] * fmaf(-dmin, im[r], d * (float)is[r]);
+    __syncthreads();
+    float *red = reinterpret_cast<float *>(lds);
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[((wave - 1) * 4 + r) * 64 + lane] = acc[r];
+    }
+    __syncthreads();
+    if (wave == 0) {
+        for (int v = 1; v < kKqMfWaves; ++v) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] += red[((v - 1) * 4 + r) * 64 + lane];
+        }
+        const int col = n0 + li;
+        if (col < n) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (4 * q + r < M) c[(size_t)(4 * q + r) * n + col] = acc[r];
+        }
+    }
+}
+
 // iq2_xxs, m = 9..16 at k == 4096: 16x16 int8 MFMA tiles, 16 waves of one
 // super-block each. A 66-byte block starts two bytes into a dword exactly when
 // its index is odd, and with one super-block per wave that parity is the
@@ -1056,6 +1233,115 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_kernel(cons
     }
 }
 
+// iq2_xxs: the tile of gemv_iq2_xxs_mfma_kernel with two-half copies. The
+// 66-byte weight block of wave v starts o2 = 2 (v % 8) bytes past a 16-byte
+// boundary and is copied as 5 chunks from there; its q8_K block as 17 chunks
+// from o = 4 (v % 4) bytes before it (the bsums are not needed). Half 0:
+// weight chunks 0..2 (d and sub-blocks 0..3, block bytes 0..33, all below copy
+// byte 48) and activation chunks 0..8; half 1: weight chunks 2..4 (chunk 2
+// twice, so that sub-blocks 4..7, bytes 34..65, lie in one region) and
+// activation chunks 8..16 (bytes 132..259 lie at or past copy byte 128). The
+// grid and sign tables are copied into LDS by
+// direct loads issued before the run, and published by a barrier that waits
+// for them only, not for the run, which each wave waits for itself.
+typedef uint64_t u64_a4 __attribute__((aligned(4)));  // 8-byte value at a dword-aligned address
+
+__host__ __device__ constexpr int iq2_sb_lds_bytes(int m) {
+    return kIq2TableBytes + kKqMfWaves * sb_copies<Iq2Run>(m) * 1024;
+}
+
+template <int M>
+__global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_sb_kernel(const uint8_t *__restrict__ w,
+                                                                               const uint8_t *__restrict__ a,
+                                                                               float *__restrict__ c, int n) {
+    static_assert(M >= 1 && M <= 16, "one 16-row tile of activation rows");
+    using R = Iq2Run;
+    constexpr int nsb = kKqMfWaves;  // k == 4096: one super-block per wave
+    constexpr int kH0 = sb_half0<R>(M);
+    constexpr int kCopies = sb_copies<R>(M);
+    constexpr int kAfterHalf0 = kCopies - (kH0 + 63) / 64;  // instructions issued after those writing half 0
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint8_t *grid = lds;  // grid magnitudes, then sign masks
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int n0 = blockIdx.x * 16;
+    const int o2 = 2 * (wave & 7), o = 4 * (wave & 3);
+    uint8_t *base = lds + kIq2TableBytes + wave * kCopies * 1024;
+    // the tables by direct loads as well, issued first: waves 0 and 1 copy the
+    // two halves of the grid, wave 2 the sign masks (1 KB each)
+    static_assert(kIq2TableBytes == 3 * 1024, "three 1-KB table pieces");
+    if (wave < 3) {
+        const uint8_t *tsrc = wave < 2 ? reinterpret_cast<const uint8_t *>(&kIq2Grid) + wave * 1024
+                                       : reinterpret_cast<const uint8_t *>(&kIq2Signs);
+        __builtin_amdgcn_global_load_lds(tsrc + 16 * lane, (__attribute__((address_space(3))) void *)(grid + wave * 1024),
+                                         16, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    sb_copy<R, M>(w + ((size_t)n0 * nsb + wave) * kIq2Bytes - o2, a + wave * kQ8KBytes - o, base, lane, n - n0);
+    // the table piece has landed once at most kCopies loads are outstanding
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kCopies) : "memory");
+    const int li = lane & 15, q = lane >> 4;  // q: the sub-block's group of 8 K positions this lane holds
+    const int arow = li < M ? li : M - 1;
+    int orow[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) orow[r] = 4 * q + r < M ? 4 * q + r : M - 1;
+    // weight block byte b sits at copy byte o2 + b: half 0 rows hold copy bytes 0..47, half 1 rows 32..79
+    const uint8_t *w0 = base + li * (R::wn0 * 16), *a0 = base + 16 * R::wn0 * 16;
+    const uint8_t *w1 = base + kH0 * 16 + li * (R::wn1 * 16) - 16 * R::wc1, *a1 = base + kH0 * 16 + 16 * R::wn1 * 16;
+    // activation byte b of row r: half 0 at a0 + 144 r + o + b (b < 144 - o), half 1 at a1 + 144 r + o + b - 128 (b >= 128 - o)
+    const uint8_t *ar0 = a0 + arow * (R::an0 * 16) + o, *ar1 = a1 + arow * (R::an1 * 16) + o - R::ac1 * 16;
+    const uint32_t sh = (uint32_t)(o2 + 2) & 3u;  // bytes of a sub-block into its first dword
+    int is[4] = {0, 0, 0, 0};
+    auto sub = [&](const uint8_t *wr, int j, const uint8_t *ar) {
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(wr + ((o2 + 2 + 8 * j) & ~3));
+        const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
+        const uint32_t gidx = __builtin_amdgcn_alignbyte(d1, d0, sh), ss = __builtin_amdgcn_alignbyte(d2, d1, sh);
+        // group q of the sub-block: its grid entry and sign mask, and its 8
+        // activation bytes (dword-aligned), each read as one typed 8-byte
+        // value so that the compiler adds no wait for the copies before it
+        const uint64_t mag = *reinterpret_cast<const uint64_t *>(grid + ((gidx >> (8 * q)) & 0xffu) * 8);
+        const uint64_t neg = *reinterpret_cast<const uint64_t *>(grid + 256 * 8 + ((ss >> (7 * q)) & 0x7fu) * 8);
+        const uint64_t v = (mag ^ neg) + (neg & 0x0101010101010101ull);  // no carry crosses a byte: |mag| >= 8
+        const uint64_t y = *reinterpret_cast<const u64_a4 *>(ar + 4 + 32 * j + 8 * q);
+        const i32x4 sj = mfma_i8_16x16x32(y, v, (i32x4){0, 0, 0, 0});
+        const int scale = 2 * (int)(ss >> 28) + 1;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) is[r] += __mul24(scale, sj[r]);
+    };
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfterHalf0) : "memory");  // half 0 has landed
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sub(w0, j, ar0);
+    const float t0 = 0.125f * fp16_to_f32(*reinterpret_cast<const uint16_t *>(w0 + o2));
+    float ad[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ad[r] = *reinterpret_cast<const float *>(a0 + orow[r] * (R::an0 * 16) + o);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int j = 4; j < 8; ++j) sub(w1, j, ar1);
+    float acc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = (t0 * ad[r]) * (float)is[r];
+    __syncthreads();
+    float *red = reinterpret_cast<float *>(lds);
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[((wave - 1) * 4 + r) * 64 + lane] = acc[r];
+    }
+    __syncthreads();
+    if (wave == 0) {
+        for (int v = 1; v < kKqMfWaves; ++v) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] += red[((v - 1) * 4 + r) * 64 + lane];
+        }
+        const int col = n0 + li;
+        if (col < n) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (4 * q + r < M) c[(size_t)(4 * q + r) * n + col] = acc[r];
+        }
+    }
+}
+
 bool iq2_mf_fits(int64_t m, int64_t k) {
     return m >= 9 && m <= 16 && k == 4096 && iq2_mf_lds_bytes(m) <= 160 * 1024;
 }
@@ -1074,9 +1360,19 @@ hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int6
     if constexpr (M >= 9) {
         // against the staged kernel at 4096 x 4096 (µs): m = 9 6.66 / 7.30, m = 10
         // 6.70 / 9.34, m = 16 6.92 / 10.01; m = 8 ties (6.66 / 6.64) and stays staged
+        if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && k == 4096) {
+            hipLaunchKernelGGL(gemv_iq2_xxs_mfma_sb_kernel<M>, dim3((unsigned)((n + 15) / 16)), dim3(kKqMfWaves * 64),
+                               (size_t)iq2_sb_lds_bytes(M), stream, wp, ap, c, (int)n);
+            return hipGetLastError();
+        }
         if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && iq2_mf_fits(M, k)) {
             hipLaunchKernelGGL(gemv_iq2_xxs_mfma_kernel<M>, dim3((unsigned)((n + 15) / 16)), dim3(kKqMfWaves * 64),
                                (size_t)iq2_mf_lds_bytes(M), stream, wp, ap, c, (int)n);
+            return hipGetLastError();
+        }
+        if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K && k == 4096) {
+            hipLaunchKernelGGL(gemv_q4_K_mfma_sb_kernel<M>, dim3((unsigned)((n + 15) / 16)), dim3(kKqMfWaves * 64),
+                               (size_t)q4k_sb_lds_bytes(M), stream, wp, ap, c, (int)n);
             return hipGetLastError();
         }
         // measured at 4096 x 4096 against the staged kernel (µs): m = 9 6.57 / 6.96,

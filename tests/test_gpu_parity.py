@@ -465,6 +465,29 @@ def test_gemv_kquant_random_bytes_and_extremes(hip, torch_gpu, oracle, qtype):
         assert np.array_equal(auto, got)
 
 
+@pytest.mark.parametrize("qtype", [1, 2])
+@pytest.mark.parametrize("m", list(range(9, 17)))
+@pytest.mark.parametrize("n", [4096, 37, 1])
+def test_gemv_kquant_one_superblock_per_wave(hip, torch_gpu, oracle, qtype, m, n):
+    """k = 4096, m = 9..16: 16-row MFMA tiles with one super-block per wave,
+    each wave's weight and activation blocks copied in two halves of 16-byte
+    chunks from the 16-byte boundary before them (a different offset for each
+    wave). Every m, a partial last tile and a single weight row; the
+    generator's inputs, then random weight bytes (every scale, min, grid index
+    and sign pattern) against extreme activations."""
+    torch = torch_gpu
+    k = 4096
+    say(f"gemv one super-block per wave type={qtype} m={m} n={n}")
+    act, w = oracle.create_input(qtype, m, n, k, seed=m * 7 + n + qtype)
+    aq = oracle.quantize_q8_K(act)
+    got = run_mul_mat(hip, torch, qtype, w, aq, m, n, k, hip.PATH_GEMV)
+    check_close(oracle, qtype, got, w, aq, m, n, k, label=f"gemv sb type={qtype} m={m} n={n}")
+    wr = random_weight_blocks(oracle, qtype, n, k, seed=59 + m + qtype)
+    ax = extreme_activation(oracle, m, k, seed=m)
+    got = run_mul_mat(hip, torch, qtype, wr, ax, m, n, k, hip.PATH_GEMV)
+    check_close(oracle, qtype, got, wr, ax, m, n, k, label=f"gemv sb random bytes type={qtype} m={m} n={n}")
+
+
 # ------------------------------------------------------ weight quantizers ----
 
 def weight_test_matrix(rows, k, seed):
