@@ -365,8 +365,8 @@ def main():
             act_t = "q8_0" if qt == 0 else "q8_K"
             for dm in (8, 16):
                 # from M = 9 at K = 4096 all three formats run the MFMA tile kernels
-                kname = {(0, 16): "gemv_q4_0_mfma_kernel<16, 16>", (1, 16): "gemv_q4_K_mfma_kernel<16>",
-                         (2, 16): "gemv_iq2_xxs_mfma_kernel<16>"}.get((qt, dm), f"{kern}<{dm}>")
+                kname = {(0, 16): "gemv_q4_0_mfma8_kernel<16>", (1, 16): "gemv_q4_K_mfma_sb_kernel<16>",
+                         (2, 16): "gemv_iq2_xxs_mfma_sb_kernel<16>"}.get((qt, dm), f"{kern}<{dm}>")
                 decode.append(measure(torch, pkg, f"m{dm}_{name}: {name} x {act_t} GEMV M={dm} N=4096 K=4096, "
                                       "32 rotating weight copies", qt, dm, 4096, 4096, side, max(side // 10, 32),
                                       samples, variant, kname, copies=32))

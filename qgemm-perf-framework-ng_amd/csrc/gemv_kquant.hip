@@ -7,9 +7,10 @@
 // (m <= 8) take m == 1 and rows too long to stage; for q4_K at m == 1 the
 // 16-row workgroups copy the activation row into LDS first. The
 // *_staged_kernel variants (m = 2..16) stage the rows in LDS once per 16-row
-// workgroup. From m = 9, q4_K at k % 4096 == 0 and iq2_xxs at k == 4096 run
-// gemv_q4_K_mfma_kernel / gemv_iq2_xxs_mfma_kernel instead: 16x16 int8 MFMA
-// tiles of 16 weight rows, K split over 16 waves.
+// workgroup. From m = 9 at k == 4096 both formats run 16x16 int8 MFMA tiles
+// of 16 weight rows with one super-block per wave (gemv_q4_K_mfma_sb_kernel,
+// gemv_iq2_xxs_mfma_sb_kernel); q4_K at larger k % 4096 == 0 runs
+// gemv_q4_K_mfma_kernel, whose waves take k / 4096 super-blocks each.
 //
 // q4_K: four lanes per super-block, lane e owning sub-blocks 2e and 2e+1 (the
 // 32 nibble bytes qs[32e .. 32e+32): low nibbles of sub-block 2e, high of
@@ -1111,129 +1112,13 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_sb_kernel(cons
     }
 }
 
-// iq2_xxs, m = 9..16 at k == 4096: 16x16 int8 MFMA tiles, 16 waves of one
-// super-block each. A 66-byte block starts two bytes into a dword exactly when
-// its index is odd, and with one super-block per wave that parity is the
-// wave's: each wave copies 17 dwords per weight row from the dword at or just
-// before its block (a direct load writes one dword per lane, so the copy is
-// dword-granular; an odd block's copy ends at its own end, an even block's
-// two bytes into the next block, which exists) into a 68-byte LDS row, the
-// block then sitting 0 or 2 bytes in, and its activation rows with 4-byte
-// direct loads. The grid and sign tables
-// come from constant memory through VGPRs into LDS: their loads go out first,
-// the copies next, and a barrier publishes the tables. Per sub-block a lane
-// decodes the half-groups its K positions need (4q..4q+3: group q / 2;
-// 16+4q..: group 2 + q / 2; half q % 2) with two grid and two sign-mask
-// gathers, one v_mfma_i32_16x16x32_i8 gives S_j, and IS += (2 s_j + 1) * S_j
-// (24-bit multiplies); per super-block acc += (0.125 * d * ad) * IS, as the
-// other iq2_xxs GEMVs form it.
-constexpr int kIq2MfRow = 68;  // LDS bytes per weight row piece (66 + 2)
-
-__host__ __device__ constexpr int64_t iq2_mf_region(int64_t m) {
-    return 16 * kIq2MfRow + (m * 292 + 15) / 16 * 16;  // one wave: weight rows, then activation rows
-}
-__host__ __device__ constexpr int64_t iq2_mf_lds_bytes(int64_t m) {
-    return kIq2TableBytes + kKqMfWaves * iq2_mf_region(m);
-}
-
-template <int M>
-__global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_kernel(const uint8_t *__restrict__ w,
-                                                                            const uint8_t *__restrict__ a,
-                                                                            float *__restrict__ c, int n) {
-    static_assert(M >= 1 && M <= 16, "one 16-row tile of activation rows");
-    constexpr int nsb = kKqMfWaves;  // k == 4096: one super-block per wave
-    extern __shared__ __align__(16) uint8_t lds[];
-    uint8_t *grid = lds;  // grid magnitudes, then sign masks
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int n0 = blockIdx.x * 16;
-    uint8_t *ws = lds + kIq2TableBytes + (size_t)wave * iq2_mf_region(M);
-    uint8_t *as = ws + 16 * kIq2MfRow;
-    // this thread's table entry first (384 entries, one per thread)
-    static_assert(kKqMfWaves * 64 >= 384, "one table entry per thread");
-    const int te = (int)threadIdx.x < 384 ? (int)threadIdx.x : 383;
-    const uint32_t *tsrc = te < 256 ? kIq2Grid.v[te] : kIq2Signs.v[te - 256];
-    uint32_t tab[2] = {tsrc[0], tsrc[1]};
-    __builtin_amdgcn_sched_barrier(0);
-    // weight row pieces: 17 dwords from the dword at or before block (n0 + r, wave)
-    const int boff = (wave & 1) * 2;  // the block's offset within its copy
-#pragma unroll 4
-    for (int r = 0; r < 16; ++r) {
-        if (lane < 17 && n0 + r < n)
-            __builtin_amdgcn_global_load_lds(w + ((size_t)(n0 + r) * nsb + wave) * kIq2Bytes - boff + lane * 4,
-                                             (__attribute__((address_space(3))) void *)(ws + r * kIq2MfRow), 4, 0, 0);
-    }
-    // activation rows: 73 dwords each, contiguous in LDS
-    for (int c0 = 0; c0 < M * 73; c0 += 64) {
-        const int ch = c0 + lane, row = ch / 73, col = ch - row * 73;
-        if (ch < M * 73)
-            __builtin_amdgcn_global_load_lds(a + ((size_t)row * nsb + wave) * kQ8KBytes + col * 4,
-                                             (__attribute__((address_space(3))) void *)(as + c0 * 4), 4, 0, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    use_here(tab);
-    if (threadIdx.x < 384) *reinterpret_cast<uint2 *>(grid + 8 * threadIdx.x) = make_uint2(tab[0], tab[1]);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies
-    __syncthreads();                                   // the tables
-    const int li = lane & 15, q = lane >> 4, h = q & 1;
-    const int g0 = q >> 1, g1 = 2 + (q >> 1);
-    const int arow = li < M ? li : M - 1;
-    int orow[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) orow[r] = 4 * q + r < M ? 4 * q + r : M - 1;
-    const uint8_t *wrow = ws + li * kIq2MfRow + boff;  // block: d at 0, sub-block j's 8 bytes at 2 + 8j
-    const uint32_t sh = 2 - boff;                        // bytes of sub-block j into its first dword
-    const uint8_t *ab = as + arow * kQ8KBytes + 4 + 4 * q;
-    int is[4] = {0, 0, 0, 0};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t *p = reinterpret_cast<const uint32_t *>(ws + li * kIq2MfRow + 8 * j + 4 * (boff >> 1));
-        const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
-        const uint32_t gidx = __builtin_amdgcn_alignbyte(d1, d0, sh), ss = __builtin_amdgcn_alignbyte(d2, d1, sh);
-        auto half = [&](int g) {
-            const uint32_t mag = *reinterpret_cast<const uint32_t *>(grid + ((gidx >> (8 * g)) & 0xffu) * 8 + 4 * h);
-            const uint32_t neg =
-                *reinterpret_cast<const uint32_t *>(grid + 256 * 8 + ((ss >> (7 * g)) & 0x7fu) * 8 + 4 * h);
-            return (mag ^ neg) + (neg & 0x01010101u);
-        };
-        const uint32_t v0 = half(g0), v1 = half(g1);
-        const uint32_t y0 = *reinterpret_cast<const uint32_t *>(ab + 32 * j);
-        const uint32_t y1 = *reinterpret_cast<const uint32_t *>(ab + 32 * j + 16);
-        const i32x4 sj = mfma_i8_16x16x32((uint64_t)y0 | ((uint64_t)y1 << 32), (uint64_t)v0 | ((uint64_t)v1 << 32),
-                                          (i32x4){0, 0, 0, 0});
-        const int scale = 2 * (int)(ss >> 28) + 1;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) is[r] += __mul24(scale, sj[r]);
-    }
-    const float t0 = 0.125f * fp16_to_f32(*reinterpret_cast<const uint16_t *>(wrow));
-    float acc[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const float ad = *reinterpret_cast<const float *>(as + orow[r] * kQ8KBytes);
-        acc[r] = (t0 * ad) * (float)is[r];
-    }
-    __syncthreads();
-    float *red = reinterpret_cast<float *>(lds);
-    if (wave > 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red[((wave - 1) * 4 + r) * 64 + lane] = acc[r];
-    }
-    __syncthreads();
-    if (wave == 0) {
-        for (int v = 1; v < kKqMfWaves; ++v) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] += red[((v - 1) * 4 + r) * 64 + lane];
-        }
-        const int col = n0 + li;
-        if (col < n) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                if (4 * q + r < M) c[(size_t)(4 * q + r) * n + col] = acc[r];
-        }
-    }
-}
-
-// iq2_xxs: the tile of gemv_iq2_xxs_mfma_kernel with two-half copies. The
+// iq2_xxs, m = 9..16 at k == 4096: 16x16 int8 MFMA tiles of 16 weight rows,
+// one super-block per wave, two-half copies. Per sub-block j, lane (row
+// l % 16, q = l / 16) holds K positions 8q..8q+7, i.e. grid group q: one grid
+// entry and one sign mask gathered from LDS (each a typed 8-byte read), the
+// signs applied as (mag ^ neg) + (neg & 1 per byte), one v_mfma_i32_16x16x32_i8
+// gives S_j and IS += (2 s_j + 1) * S_j (24-bit multiplies); per super-block
+// acc = (0.125 * d * ad) * IS, as the other iq2_xxs GEMVs form it. The
 // 66-byte weight block of wave v starts o2 = 2 (v % 8) bytes past a 16-byte
 // boundary and is copied as 5 chunks from there; its q8_K block as 17 chunks
 // from o = 4 (v % 4) bytes before it (the bsums are not needed). Half 0:
@@ -1342,10 +1227,6 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_sb_kernel(c
     }
 }
 
-bool iq2_mf_fits(int64_t m, int64_t k) {
-    return m >= 9 && m <= 16 && k == 4096 && iq2_mf_lds_bytes(m) <= 160 * 1024;
-}
-
 // the q4_K MFMA tile kernel runs from m = 9 at k % 4096 == 0 while its slices fit the LDS
 bool kq_mf_fits(int64_t m, int64_t k) {
     return m >= 9 && m <= 16 && k % 4096 == 0 && kq_mf_lds_bytes(m, k / 256) <= 160 * 1024;
@@ -1358,16 +1239,11 @@ hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int6
     const auto *ap = static_cast<const uint8_t *>(a);
     const int64_t nsb = k / 256;
     if constexpr (M >= 9) {
-        // against the staged kernel at 4096 x 4096 (µs): m = 9 6.66 / 7.30, m = 10
-        // 6.70 / 9.34, m = 16 6.92 / 10.01; m = 8 ties (6.66 / 6.64) and stays staged
+        // k == 4096: one super-block per wave (m = 8 stays on the staged kernel,
+        // which the MFMA tile only tied)
         if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && k == 4096) {
             hipLaunchKernelGGL(gemv_iq2_xxs_mfma_sb_kernel<M>, dim3((unsigned)((n + 15) / 16)), dim3(kKqMfWaves * 64),
                                (size_t)iq2_sb_lds_bytes(M), stream, wp, ap, c, (int)n);
-            return hipGetLastError();
-        }
-        if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && iq2_mf_fits(M, k)) {
-            hipLaunchKernelGGL(gemv_iq2_xxs_mfma_kernel<M>, dim3((unsigned)((n + 15) / 16)), dim3(kKqMfWaves * 64),
-                               (size_t)iq2_mf_lds_bytes(M), stream, wp, ap, c, (int)n);
             return hipGetLastError();
         }
         if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K && k == 4096) {
