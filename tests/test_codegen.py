@@ -1,5 +1,8 @@
 """Instruction-order checks on the gfx950 assembly of kernels whose
-synchronisation depends on it (CPU only: hipcc cross-compiles here).
+synchronisation depends on it (CPU only: hipcc cross-compiles here): the
+M = 1 GEMVs' copy-then-wait order, scalar LDS addresses for every
+direct-to-LDS copy, and the issue order the two-half copies of the M = 9..16
+MFMA tile GEMVs wait on.
 
 gemv_q4_0_m1_kernel<true> and gemv_q4_K_kernel<1, true, false> copy the activation
 row into LDS with direct loads (global_load_lds_*) and then issue the loads
@@ -139,3 +142,63 @@ def test_dma_lds_address_is_scalar(source):
     with open(out) as f:
         lines = [ln.split(";")[0].strip() for ln in f.read().splitlines()]
     assert dma_m0_from_vector(lines) == []
+
+
+def check_half_split(lines: list[str], copies: int, after_half0: int) -> None:
+    """Two-half copies (the M = 9..16 MFMA tile GEMVs): the wave's run of
+    `copies` direct-to-LDS instructions writes consecutive 1-KB pieces of its
+    LDS region in issue order (M0 = base + 0x400 i), and the first wait after
+    the run is vmcnt(after_half0): loads complete in issue order, so it holds
+    the wave until the instructions that wrote half 0 have landed. A run
+    reordered by the compiler would make that wait cover the wrong pieces."""
+    run, m0 = [], None
+    for i, t in enumerate(lines):
+        m = re.match(r"s_mov_b32 m0, (s\d+)$", t)
+        if m:
+            m0 = (m.group(1), 0)
+        m = re.match(r"s_add_i32 m0, (s\d+), (0x[0-9a-f]+|\d+)$", t)
+        if m:
+            m0 = (m.group(1), int(m.group(2), 0))
+        elif t.startswith("s_add_i32 m0,"):
+            m0 = None  # a base plus a register: not part of the run (a table piece)
+        if t.startswith("global_load_lds") and m0 is not None:
+            run.append((i, m0))
+    assert len(run) == copies, f"{len(run)} run copies, expected {copies}"
+    assert len({b for _, (b, _) in run}) == 1, "the run's copies use different LDS bases"
+    offsets = [o for _, (_, o) in run]
+    assert offsets == [0x400 * (offsets[0] // 0x400 + k) for k in range(copies)], f"run out of order: {offsets}"
+    waits = [t for t in lines[run[-1][0]:] if re.match(r"s_waitcnt .*vmcnt\(\d+\)", t)]
+    run_wait = next(t for t in waits if int(re.search(r"vmcnt\((\d+)\)", t).group(1)) < copies)
+    assert f"vmcnt({after_half0})" in run_wait, f"first wait on the run is {run_wait}"
+
+
+def test_half_split_checker():
+    """The checker itself: a swapped pair of copies or a wrong wait fails."""
+    good = ["s_mov_b32 m0, s14", "global_load_lds_dwordx4 v[2:3], off", "s_add_i32 m0, s14, 0x400",
+            "global_load_lds_dwordx4 v[2:3], off", "s_add_i32 m0, s14, 0x800", "global_load_lds_dwordx4 v2, s[4:5]",
+            "s_waitcnt vmcnt(1)", "ds_read_b32 v1, v2", "s_waitcnt vmcnt(0)", "s_endpgm"]
+    check_half_split(good, 3, 1)
+    swapped = good[:2] + good[4:6] + good[2:4] + good[6:]
+    with pytest.raises(AssertionError):
+        check_half_split(swapped, 3, 1)
+    with pytest.raises(AssertionError):
+        check_half_split(good, 3, 2)
+    table = ["s_add_i32 m0, s14, s8", "global_load_lds_dwordx4 v1, s[8:9]"] + good[:6] + ["s_waitcnt vmcnt(3)"] + good[6:]
+    check_half_split(table, 3, 1)
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC) or shutil.which("make") is None, reason="needs hipcc and make")
+@pytest.mark.parametrize("source,kernel,copies,after_half0", [
+    ("gemv.hip", "gemv_q4_0_mfma8_kernelILi16E", 7, 3),
+    ("gemv.hip", "gemv_q4_0_mfma8_kernelILi9E", 6, 3),
+    ("gemv_kquant.hip", "gemv_q4_K_mfma_sb_kernelILi16E", 8, 4),
+    ("gemv_kquant.hip", "gemv_q4_K_mfma_sb_kernelILi9E", 6, 3),
+    ("gemv_kquant.hip", "gemv_iq2_xxs_mfma_sb_kernelILi16E", 6, 3),
+    ("gemv_kquant.hip", "gemv_iq2_xxs_mfma_sb_kernelILi9E", 5, 2),
+])
+def test_half_split_copy_order(source, kernel, copies, after_half0):
+    out = os.path.join(PKG_DIR, "_build", source + ".s")
+    subprocess.run(["make", "-s", "-C", PKG_DIR, out], check=True, capture_output=True, timeout=600)
+    with open(out) as f:
+        asm = f.read()
+    check_half_split(_kernel_lines(asm, kernel), copies, after_half0)
