@@ -19,9 +19,10 @@
 //                              k % 2048 == 0): 16x16 int8 MFMA tiles of 16
 //                              weight rows, K split over the workgroup's waves,
 //                              each wave's slices copied into LDS by direct loads.
-//   gemv_q4_0_mfma8_kernel     the same at k = 4096 (8 blocks per wave): the
-//                              slice copied in two halves, half 0 multiplied
-//                              while half 1 lands, scales on the matrix core.
+//   gemv_q4_0_mfma8_kernel     the same at k = 4096 (8 blocks per wave) from
+//                              m = 7: the slice copied in two halves, half 0
+//                              multiplied while half 1 lands, scales on the
+//                              matrix core.
 //
 // Every lane issues all the loads of a step before any arithmetic, so the
 // weight stream of the grid is in flight at once; weight rows are clamped so
@@ -832,14 +833,17 @@ hipError_t launch_fused_m(const void *w, const float *x, float *c, int64_t n, in
     return hipGetLastError();
 }
 
-// Waves of the MFMA tile kernel for m activation rows and k, 0 where the
+// Waves of the MFMA tile kernels for m activation rows and k, 0 where the
 // pairs kernel runs instead: 16 waves of 8-block slices (k % 4096 == 0) from
-// m = 9, where they measured faster than the pairs kernel (4096 x 4096, µs:
+// m = 9 (from m = 7 at k = 4096, below), where they measured faster than the pairs kernel (4096 x 4096, µs:
 // m = 8 5.93 against 5.98, m = 10 6.15 / 6.95, m = 12 6.11 / 7.86, m = 16
 // 6.21 / 9.54); 8 waves of 8-block slices (k % 2048 == 0) from m = 12 (m = 12
 // 7.14 / 7.86, m = 10 7.18 / 6.95). Both while the slices fit the LDS.
 int mf_gemv_waves(int64_t m, int64_t k) {
     if (m > 16 || mf_gemv_lds_bytes(m, k / 32) > kPairsMaxLds) return 0;
+    // k = 4096 (gemv_q4_0_mfma8_kernel): from m = 7, where it beats the pairs
+    // kernel (4096 x 4096, us: m = 6 5.41 / 5.38, m = 7 5.42 / 5.96, m = 8 5.44 / 5.99)
+    if (m >= 7 && k == 4096) return 16;
     if (m >= 9 && k % 4096 == 0) return 16;
     if (m >= 12 && k % 2048 == 0) return 8;
     return 0;

@@ -7,7 +7,7 @@
 // (m <= 8) take m == 1 and rows too long to stage; for q4_K at m == 1 the
 // 16-row workgroups copy the activation row into LDS first. The
 // *_staged_kernel variants (m = 2..16) stage the rows in LDS once per 16-row
-// workgroup. From m = 9 at k == 4096 both formats run 16x16 int8 MFMA tiles
+// workgroup. From m = 5 at k == 4096 both formats run 16x16 int8 MFMA tiles
 // of 16 weight rows with one super-block per wave (gemv_q4_K_mfma_sb_kernel,
 // gemv_iq2_xxs_mfma_sb_kernel); q4_K at larger k % 4096 == 0 runs
 // gemv_q4_K_mfma_kernel, whose waves take k / 4096 super-blocks each.
@@ -936,7 +936,7 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_kernel(const u
 }
 
 // Two-half copies for the GEMVs with one super-block per wave (k == 4096,
-// m = 9..16). A wave copies its super-block of the tile's 16 weight rows and
+// m = 5..16). A wave copies its super-block of the tile's 16 weight rows and
 // of the m activation rows in 16-byte chunks, each row from the 16-byte
 // boundary at or before its block (rows are 16 blocks long, so that offset
 // depends on the wave only). Half h holds, for each weight row, chunks
@@ -1112,7 +1112,7 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_sb_kernel(cons
     }
 }
 
-// iq2_xxs, m = 9..16 at k == 4096: 16x16 int8 MFMA tiles of 16 weight rows,
+// iq2_xxs, m = 5..16 at k == 4096: 16x16 int8 MFMA tiles of 16 weight rows,
 // one super-block per wave, two-half copies. Per sub-block j, lane (row
 // l % 16, q = l / 16) holds K positions 8q..8q+7, i.e. grid group q: one grid
 // entry and one sign mask gathered from LDS (each a typed 8-byte read), the
@@ -1238,9 +1238,10 @@ hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int6
     const auto *wp = static_cast<const uint8_t *>(w);
     const auto *ap = static_cast<const uint8_t *>(a);
     const int64_t nsb = k / 256;
-    if constexpr (M >= 9) {
-        // k == 4096: one super-block per wave (m = 8 stays on the staged kernel,
-        // which the MFMA tile only tied)
+    if constexpr (M >= 5) {
+        // k == 4096: one super-block per wave, from m = 5 (4096 x 4096 against the
+        // staged kernel, us: q4_K m = 4 5.01 / 4.56, m = 5 5.00 / 5.12, m = 8 5.19 /
+        // 6.21; iq2_xxs m = 4 5.23 / 5.08, m = 5 5.34 / 5.91, m = 8 5.56 / 6.58)
         if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && k == 4096) {
             hipLaunchKernelGGL(gemv_iq2_xxs_mfma_sb_kernel<M>, dim3((unsigned)((n + 15) / 16)), dim3(kKqMfWaves * 64),
                                (size_t)iq2_sb_lds_bytes(M), stream, wp, ap, c, (int)n);
@@ -1251,6 +1252,8 @@ hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int6
                                (size_t)q4k_sb_lds_bytes(M), stream, wp, ap, c, (int)n);
             return hipGetLastError();
         }
+    }
+    if constexpr (M >= 9) {
         // measured at 4096 x 4096 against the staged kernel (µs): m = 9 6.57 / 6.96,
         // m = 12 6.92 / 7.97, m = 16 7.59 / 9.22; m = 8 ties (6.19 / 6.17)
         if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K && kq_mf_fits(M, k)) {

@@ -191,6 +191,9 @@ def test_half_split_checker():
 @pytest.mark.parametrize("source,kernel,copies,after_half0", [
     ("gemv.hip", "gemv_q4_0_mfma8_kernelILi16E", 7, 3),
     ("gemv.hip", "gemv_q4_0_mfma8_kernelILi9E", 6, 3),
+    ("gemv.hip", "gemv_q4_0_mfma8_kernelILi7E", 5, 2),
+    ("gemv_kquant.hip", "gemv_q4_K_mfma_sb_kernelILi5E", 5, 3),
+    ("gemv_kquant.hip", "gemv_iq2_xxs_mfma_sb_kernelILi5E", 3, 1),
     ("gemv_kquant.hip", "gemv_q4_K_mfma_sb_kernelILi16E", 8, 4),
     ("gemv_kquant.hip", "gemv_q4_K_mfma_sb_kernelILi9E", 6, 3),
     ("gemv_kquant.hip", "gemv_iq2_xxs_mfma_sb_kernelILi16E", 6, 3),
