@@ -238,6 +238,36 @@ def measure(torch, pkg, label, qtype, m, n, k, steps, warmup, samples, variant, 
     return item
 
 
+def cpu_description():
+    """The host CPU as /proc/cpuinfo names it, with family / model / stepping
+    (a virtual machine may report only "AMD EPYC"); AMD family 0x1A is Zen 5,
+    0x19 Zen 3/4, 0x17 Zen 1/2."""
+    fields = {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key in ("model name", "cpu family", "model", "stepping", "vendor_id") and key not in fields:
+                fields[key] = val.strip()
+            if key == "flags" and "hypervisor" in val.split():
+                fields["vm"] = "virtual machine"
+            if not line.strip() and fields:
+                break
+    except OSError:
+        return "unknown"
+    desc = fields.get("model name", "unknown")
+    fam = fields.get("cpu family")
+    if fam is not None:
+        desc += f" (family {fam} model {fields.get('model', '?')} stepping {fields.get('stepping', '?')}"
+        zen = {0x17: "Zen 1/2", 0x19: "Zen 3/4", 0x1A: "Zen 5"}.get(int(fam)) if fam.isdigit() else None
+        if fields.get("vendor_id") == "AuthenticAMD" and zen:
+            desc += f": {zen}"
+        if "vm" in fields:
+            desc += ", virtual machine"
+        desc += f", {os.cpu_count()} logical CPUs visible)"
+    return desc
+
+
 def cpu_baseline(budget_s, pkg):
     """Time the reference's compute() on the host (activation quantization
     included) on all usable cores (output columns split, bitwise the same
@@ -288,14 +318,7 @@ def cpu_baseline(budget_s, pkg):
                         "s_per_call": round(per_call, 6),
                         "sample": f"{rows} of {m} rows x {n} x {k}" if rows < m else f"{m} x {n} x {k}"}
             notes.append(f"{key} {rows}/{m} rows x{reps} calls {per_call * 1e3:.1f} ms/call")
-    cpu = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    cpu = cpu_description()
     what = ("llama_reference::compute (oracle/_ref: the reference's llama_reference.cpp, g++ -O3 -ffp-contract=off)"
             if use_ref else "oracle/pfng_oracle.c compute (gcc -O3)")
     return {
