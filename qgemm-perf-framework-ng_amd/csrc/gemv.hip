@@ -930,8 +930,8 @@ bool gemv_supported(int type, int64_t m, int64_t k) {
         return m <= kPairsMaxM && pairs;  // m = 9..16 only in the pair-per-lane kernel
     }
     // q4_K and iq2_xxs (gemv_kquant.hip): m <= 8 for every k % 256 == 0,
-    // m = 9..16 while the staged activations fit in LDS
-    if (m > 8) return kquant_gemv_staged_fits(m, k) &&
+    // m = 9..16 while the staged activations fit in LDS, m = 17..64 at k == 4096
+    if (m > 8) return (kquant_gemv_staged_fits(m, k) || kquant_gemv_chunked_fits(m, k)) &&
                       (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K || type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K);
     return (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K || type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K) && k % 256 == 0;
 }

@@ -1227,6 +1227,259 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_sb_kernel(c
     }
 }
 
+// m = 17..64 at k == 4096: the one-super-block-per-wave tiles above, with the
+// activation rows taken in C chunks of 16. Each wave copies its super-block of
+// the tile's 16 weight rows once, decodes them once into registers, and then
+// streams the chunks: chunk c's activation blocks arrive in two halves (H0:
+// copy chunks 0..8 of each row, d and sub-blocks 0..3; H1: chunks 8..18 or
+// 8..16, sub-blocks 4..7 and the bsums), each half into its own LDS buffer,
+// which is refilled with chunk c + 1 as soon as the wave has read it: the
+// copy of H0(c + 1) runs while H1(c) is multiplied and the copy of H1(c + 1)
+// while H0(c + 1) is. Every wait is for the instructions that wrote one
+// buffer (loads complete in issue order). Activation rows past m repeat row
+// m - 1 (their results are not stored).
+//
+// One flat run of kRows x kCols 16-byte chunks into LDS at dst: chunk
+// (r, j) from src + r * rstride + 16 (col0 + j), 64 chunks per instruction,
+// every lane active (lanes past the end repeat the last chunk into the pad
+// that follows the run); rows at or past rvalid repeat row rvalid - 1.
+template <int kRows, int kCols>
+__device__ __forceinline__ void run_copy(const uint8_t *src, uint32_t rstride, int col0, int rvalid, uint8_t *dst,
+                                         int lane) {
+    constexpr int kN = kRows * kCols;
+#pragma unroll
+    for (int i = 0; i < (kN + 63) / 64; ++i) {
+        int p = 64 * i + lane;
+        if (p > kN - 1) p = kN - 1;
+        int r = p / kCols;
+        const int col = col0 + p - r * kCols;
+        if (r > rvalid - 1) r = rvalid - 1;
+        __builtin_amdgcn_global_load_lds(src + (uint32_t)r * rstride + 16u * (uint32_t)col,
+                                         (__attribute__((address_space(3))) void *)(dst + i * 1024), 16, 0, 0);
+    }
+}
+template <int kRows, int kCols>
+__host__ __device__ constexpr int run_copies() {
+    return (kRows * kCols + 63) / 64;
+}
+
+constexpr int kChunkWaveBytes = 9 * 1024;  // per wave: weight run, H0, H1 (3 KB each)
+
+__host__ __device__ constexpr int q4k_chunk_lds_bytes() { return kKqMfWaves * kChunkWaveBytes; }
+
+template <int C>
+__global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(const uint8_t *__restrict__ w,
+                                                                             const uint8_t *__restrict__ a,
+                                                                             float *__restrict__ c, int m, int n) {
+    static_assert(C >= 2 && C <= 4, "17..64 activation rows");
+    constexpr int nsb = kKqMfWaves;  // k == 4096
+    constexpr uint32_t kARow = nsb * kQ8KBytes;
+    constexpr int kH = run_copies<16, 11>();  // instructions per half (H1: 11 columns, H0: 9)
+    static_assert(run_copies<16, 9>() == kH && run_copies<16, 9>() * 1024 <= 3072, "3 KB per run");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int n0 = blockIdx.x * 16;
+    const int o = 4 * (wave & 3);
+    uint8_t *wl = lds + wave * kChunkWaveBytes, *h0 = wl + 3072, *h1 = wl + 6144;
+    const uint8_t *asrc = a + wave * kQ8KBytes - o;  // copy start of the wave's block in activation row 0
+    auto copy_h0 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, lane); };
+    auto copy_h1 = [&](int ch) { run_copy<16, 11>(asrc + (size_t)ch * 16 * kARow, kARow, 8, m - 16 * ch, h1, lane); };
+    run_copy<16, 9>(w + ((size_t)n0 * nsb + wave) * 144, nsb * 144, 0, n - n0, wl, lane);
+    copy_h0(0);
+    copy_h1(0);
+    const int li = lane & 15, q = lane >> 4;
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // weights and H0(0)
+    // the weight row's decode, once: scales, mins, d, dmin and the nibble operands
+    const uint8_t *wr = wl + li * 144;
+    const uint32_t *hp = reinterpret_cast<const uint32_t *>(wr);
+    const uint4 hd = make_uint4(hp[0], hp[1], hp[2], hp[3]);
+    const uint32_t scw[2] = {hd.y & 0x3f3f3f3fu, (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u)};
+    const uint32_t mnw[2] = {hd.z & 0x3f3f3f3fu, ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u)};
+    uint64_t wv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t x0 = *reinterpret_cast<const uint32_t *>(wr + 16 + 32 * (j / 2) + 4 * q);
+        const uint32_t x1 = *reinterpret_cast<const uint32_t *>(wr + 32 + 32 * (j / 2) + 4 * q);
+        const uint32_t v0 = (j & 1 ? x0 >> 4 : x0) & 0x0f0f0f0fu, v1 = (j & 1 ? x1 >> 4 : x1) & 0x0f0f0f0fu;
+        wv[j] = (uint64_t)v0 | ((uint64_t)v1 << 32);
+    }
+    const uint32_t mp = (q & 2 ? mnw[1] : mnw[0]) >> (16 * (q & 1));
+    const _Float16 m0 = (_Float16)(int)(mp & 0xffu), m1 = (_Float16)(int)((mp >> 8) & 0xffu);
+    const f16x4 mm = {m0, m0, m1, m1};
+    const float d = fp16_to_f32(hd.x & 0xffffu), dmin = fp16_to_f32(hd.x >> 16);
+    // activation byte b of chunk row r: H0 at h0 + 144 r + o + b, H1 at h1 + 176 r + o + b - 128
+    const uint8_t *a0 = h0 + li * 144 + o + 4 + 4 * q, *a1 = h1 + li * 176 + o - 128 + 4 + 4 * q;
+    float acc[C][4];
+#pragma unroll
+    for (int ch = 0; ch < C; ++ch) {
+        if (ch > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H0(ch)
+        int is[4] = {0, 0, 0, 0};
+        auto sub = [&](int j, const uint8_t *ay) {
+            const uint32_t y0 = *reinterpret_cast<const uint32_t *>(ay + 32 * j);
+            const uint32_t y1 = *reinterpret_cast<const uint32_t *>(ay + 32 * j + 16);
+            const i32x4 sj = mfma_i8_16x16x32((uint64_t)y0 | ((uint64_t)y1 << 32), wv[j], (i32x4){0, 0, 0, 0});
+            const int sc = (int)((scw[j / 4] >> (8 * (j % 4))) & 0xffu);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) is[r] += __mul24(sc, sj[r]);
+        };
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sub(j, a0);
+        float ad[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ad[r] = *reinterpret_cast<const float *>(h0 + (4 * q + r) * 144 + o);
+        if (ch + 1 < C) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H0 read: refill it
+            copy_h0(ch + 1);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H1(ch)
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+#pragma unroll
+        for (int j = 4; j < 8; ++j) sub(j, a1);
+        // IM: A = bsums 4q..4q+3 of the lane's activation row, B = the mins (mm)
+        const uint32_t b01 = *reinterpret_cast<const uint32_t *>(a1 - 4 - 4 * q + 260 + 8 * q);
+        const uint32_t b23 = *reinterpret_cast<const uint32_t *>(a1 - 4 - 4 * q + 264 + 8 * q);
+        const f16x4 bs = {(_Float16)(short)(b01 & 0xffffu), (_Float16)(short)(b01 >> 16),
+                          (_Float16)(short)(b23 & 0xffffu), (_Float16)(short)(b23 >> 16)};
+        const f32x4 im = __builtin_amdgcn_mfma_f32_16x16x16f16(bs, mm, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[ch][r] = ad[r] * fmaf(-dmin, im[r], d * (float)is[r]);
+        if (ch + 1 < C) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H1 read: refill it
+            copy_h1(ch + 1);
+        }
+    }
+    // wave partials through LDS ([wave][group g = 4 chunk + r][lane]); wave w
+    // adds groups w, w + 16, ... over the waves in wave order and stores them
+    __syncthreads();
+    float *red = reinterpret_cast<float *>(lds);
+#pragma unroll
+    for (int ch = 0; ch < C; ++ch)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[((wave * C + ch) * 4 + r) * 64 + lane] = acc[ch][r];
+    __syncthreads();
+    const int col = n0 + li;
+    for (int g = wave; g < 4 * C; g += kKqMfWaves) {
+        float s = red[g * 64 + lane];
+        for (int v = 1; v < kKqMfWaves; ++v) s += red[(v * 4 * C + g) * 64 + lane];
+        const int row = 16 * (g / 4) + 4 * q + g % 4;
+        if (col < n && row < m) c[(size_t)row * n + col] = s;
+    }
+}
+
+// iq2_xxs, m = 17..64 at k == 4096: as gemv_q4_K_mfma_chunk_kernel, with the
+// weight decode of gemv_iq2_xxs_mfma_sb_kernel done once per wave (5 weight
+// columns per row, H1 = activation chunks 8..16) and the grid and sign tables
+// copied by waves 0..2 before everything else.
+constexpr int kIq2ChunkWaveBytes = 8 * 1024;  // weight run 2 KB, H0 and H1 3 KB each
+
+__host__ __device__ constexpr int iq2_chunk_lds_bytes() { return kIq2TableBytes + kKqMfWaves * kIq2ChunkWaveBytes; }
+
+template <int C>
+__global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kernel(const uint8_t *__restrict__ w,
+                                                                                const uint8_t *__restrict__ a,
+                                                                                float *__restrict__ c, int m, int n) {
+    static_assert(C >= 2 && C <= 4, "17..64 activation rows");
+    constexpr int nsb = kKqMfWaves;  // k == 4096
+    constexpr uint32_t kARow = nsb * kQ8KBytes;
+    constexpr int kH = run_copies<16, 9>();
+    constexpr int kW = run_copies<16, 5>();
+    static_assert(kH * 1024 <= 3072 && kW * 1024 <= 2048, "run sizes");
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint8_t *grid = lds;  // grid magnitudes, then sign masks
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int n0 = blockIdx.x * 16;
+    const int o2 = 2 * (wave & 7), o = 4 * (wave & 3);
+    uint8_t *wl = lds + kIq2TableBytes + wave * kIq2ChunkWaveBytes, *h0 = wl + 2048, *h1 = wl + 5120;
+    static_assert(kIq2TableBytes == 3 * 1024, "three 1-KB table pieces");
+    if (wave < 3) {
+        const uint8_t *tsrc = wave < 2 ? reinterpret_cast<const uint8_t *>(&kIq2Grid) + wave * 1024
+                                       : reinterpret_cast<const uint8_t *>(&kIq2Signs);
+        __builtin_amdgcn_global_load_lds(tsrc + 16 * lane, (__attribute__((address_space(3))) void *)(grid + wave * 1024),
+                                         16, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t *asrc = a + wave * kQ8KBytes - o;
+    auto copy_h0 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, lane); };
+    auto copy_h1 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 8, m - 16 * ch, h1, lane); };
+    run_copy<16, 5>(w + ((size_t)n0 * nsb + wave) * kIq2Bytes - o2, nsb * kIq2Bytes, 0, n - n0, wl, lane);
+    copy_h0(0);
+    copy_h1(0);
+    // the table piece has landed once at most (weights + H0 + H1) loads are outstanding
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kW + 2 * kH) : "memory");
+    const int li = lane & 15, q = lane >> 4;
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // weights and H0(0)
+    // the weight row's decode, once: group q of every sub-block, its scale, d
+    const uint8_t *wr = wl + li * 80;  // weight block byte b at copy byte o2 + b
+    const uint32_t sh = (uint32_t)(o2 + 2) & 3u;
+    uint64_t wv[8];
+    int scale[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(wr + ((o2 + 2 + 8 * j) & ~3));
+        const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
+        const uint32_t gidx = __builtin_amdgcn_alignbyte(d1, d0, sh), ss = __builtin_amdgcn_alignbyte(d2, d1, sh);
+        const uint64_t mag = *reinterpret_cast<const uint64_t *>(grid + ((gidx >> (8 * q)) & 0xffu) * 8);
+        const uint64_t neg = *reinterpret_cast<const uint64_t *>(grid + 256 * 8 + ((ss >> (7 * q)) & 0x7fu) * 8);
+        wv[j] = (mag ^ neg) + (neg & 0x0101010101010101ull);  // no carry crosses a byte: |mag| >= 8
+        scale[j] = 2 * (int)(ss >> 28) + 1;
+    }
+    const float t0 = 0.125f * fp16_to_f32(*reinterpret_cast<const uint16_t *>(wr + o2));
+    // activation bytes 4 + 32 j + 8q (+ 4) of chunk row li: H0 at h0 + 144 li + o + b, H1 at h1 + 144 li + o + b - 128
+    const uint8_t *a0 = h0 + li * 144 + o + 4 + 8 * q, *a1 = h1 + li * 144 + o - 128 + 4 + 8 * q;
+    float acc[C][4];
+#pragma unroll
+    for (int ch = 0; ch < C; ++ch) {
+        if (ch > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H0(ch)
+        int is[4] = {0, 0, 0, 0};
+        auto sub = [&](int j, const uint8_t *ay) {
+            // one typed 8-byte read: the compiler then adds no wait for every outstanding copy before it
+            const uint64_t y = *reinterpret_cast<const u64_a4 *>(ay + 32 * j);
+            const i32x4 sj = mfma_i8_16x16x32(y, wv[j], (i32x4){0, 0, 0, 0});
+#pragma unroll
+            for (int r = 0; r < 4; ++r) is[r] += __mul24(scale[j], sj[r]);
+        };
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sub(j, a0);
+        float ad[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ad[r] = *reinterpret_cast<const float *>(h0 + (4 * q + r) * 144 + o);
+        if (ch + 1 < C) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H0 read: refill it
+            copy_h0(ch + 1);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H1(ch)
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+#pragma unroll
+        for (int j = 4; j < 8; ++j) sub(j, a1);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[ch][r] = (t0 * ad[r]) * (float)is[r];
+        if (ch + 1 < C) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H1 read: refill it
+            copy_h1(ch + 1);
+        }
+    }
+    // wave partials through LDS ([wave][group g = 4 chunk + r][lane]); wave w
+    // adds groups w, w + 16, ... over the waves in wave order and stores them
+    __syncthreads();
+    float *red = reinterpret_cast<float *>(lds);
+#pragma unroll
+    for (int ch = 0; ch < C; ++ch)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[((wave * C + ch) * 4 + r) * 64 + lane] = acc[ch][r];
+    __syncthreads();
+    const int col = n0 + li;
+    for (int g = wave; g < 4 * C; g += kKqMfWaves) {
+        float s = red[g * 64 + lane];
+        for (int v = 1; v < kKqMfWaves; ++v) s += red[(v * 4 * C + g) * 64 + lane];
+        const int row = 16 * (g / 4) + 4 * q + g % 4;
+        if (col < n && row < m) c[(size_t)row * n + col] = s;
+    }
+}
+
 // the q4_K MFMA tile kernel runs from m = 9 at k % 4096 == 0 while its slices fit the LDS
 bool kq_mf_fits(int64_t m, int64_t k) {
     return m >= 9 && m <= 16 && k % 4096 == 0 && kq_mf_lds_bytes(m, k / 256) <= 160 * 1024;
@@ -1338,6 +1591,8 @@ bool kquant_gemv_staged_fits(int64_t m, int64_t k) {
     return m >= 2 && m <= 16 && k % 256 == 0 && kq_staged_lds_bytes(m, k / 256) <= 160 * 1024;
 }
 
+bool kquant_gemv_chunked_fits(int64_t m, int64_t k) { return m >= 17 && m <= 64 && k == 4096; }
+
 hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                               hipStream_t stream) {
     if (type != PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K && type != PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K)
@@ -1359,8 +1614,29 @@ hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, 
     case 14: return launch_kq_gemv<14>(type, w, a, c, n, k, stream);
     case 15: return launch_kq_gemv<15>(type, w, a, c, n, k, stream);
     case 16: return launch_kq_gemv<16>(type, w, a, c, n, k, stream);
+    default: break;
+    }
+    if (!kquant_gemv_chunked_fits(m, k)) return hipErrorInvalidValue;
+    const auto *wp = static_cast<const uint8_t *>(w);
+    const auto *ap = static_cast<const uint8_t *>(a);
+    const dim3 grid((unsigned)((n + 15) / 16)), block(kKqMfWaves * 64);
+    const bool q4k = type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K;
+    const size_t lds = q4k ? (size_t)q4k_chunk_lds_bytes() : (size_t)iq2_chunk_lds_bytes();
+#define PFNG_CHUNK_CASE(C)                                                                                      \
+    case C:                                                                                                    \
+        if (q4k)                                                                                               \
+            hipLaunchKernelGGL(gemv_q4_K_mfma_chunk_kernel<C>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n); \
+        else                                                                                                   \
+            hipLaunchKernelGGL(gemv_iq2_xxs_mfma_chunk_kernel<C>, grid, block, lds, stream, wp, ap, c, (int)m,     \
+                               (int)n);                                                                        \
+        return hipGetLastError();
+    switch ((m + 15) / 16) {
+        PFNG_CHUNK_CASE(2)
+        PFNG_CHUNK_CASE(3)
+        PFNG_CHUNK_CASE(4)
     default: return hipErrorInvalidValue;
     }
+#undef PFNG_CHUNK_CASE
 }
 
 }  // namespace pfng

@@ -33,6 +33,8 @@ hipError_t launch_kquant_fused_gemv(int type, const void *w, const float *x, flo
                                     hipStream_t stream);
 // q4_K / iq2_xxs GEMV rows m = 9..16 run only with the activations staged in LDS
 bool kquant_gemv_staged_fits(int64_t m, int64_t k);
+// m = 17..64 at k == 4096: MFMA tiles of 16 weight rows over chunks of 16 activation rows
+bool kquant_gemv_chunked_fits(int64_t m, int64_t k);
 hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                               hipStream_t stream);
 

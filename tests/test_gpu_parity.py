@@ -466,10 +466,12 @@ def test_gemv_kquant_random_bytes_and_extremes(hip, torch_gpu, oracle, qtype):
 
 
 @pytest.mark.parametrize("qtype", [1, 2])
-@pytest.mark.parametrize("m", list(range(5, 17)))
+@pytest.mark.parametrize("m", list(range(5, 17)) + [17, 20, 31, 32, 33, 47, 48, 49, 63, 64])
 @pytest.mark.parametrize("n", [4096, 37, 1])
 def test_gemv_kquant_one_superblock_per_wave(hip, torch_gpu, oracle, qtype, m, n):
-    """k = 4096, m = 5..16: 16-row MFMA tiles with one super-block per wave,
+    """k = 4096, m = 5..64: 16-row MFMA tiles with one super-block per wave
+    (from m = 17 over chunks of 16 activation rows, each chunk's halves
+    refilled while the other half is multiplied),
     each wave's weight and activation blocks copied in two halves of 16-byte
     chunks from the 16-byte boundary before them (a different offset for each
     wave). Every m, a partial last tile and a single weight row; the
