@@ -300,4 +300,32 @@ __device__ __forceinline__ float fp16_product(uint32_t a, uint32_t b) {
     return __builtin_fmaf((float)ha, (float)hb, 0.0f);
 }
 
+// One flat run of kRows x kCols 16-byte chunks into LDS at dst with direct
+// loads: chunk (r, j) from src + r * rstride + 16 (col0 + j), 64 chunks per
+// instruction (1 KB at dst + 1024 i), every lane active: lanes past the end
+// repeat the last chunk into the pad that follows the run, and rows at or past
+// rvalid repeat row rvalid - 1. (A copy whose lanes are predicated may be
+// merged by the compiler into one whose LDS address comes from a single lane.)
+template <int kRows, int kCols>
+__device__ __forceinline__ void run_copy(const uint8_t *src, uint32_t rstride, int col0, int rvalid, uint8_t *dst,
+                                         int lane) {
+    constexpr int kN = kRows * kCols;
+#pragma unroll
+    for (int i = 0; i < (kN + 63) / 64; ++i) {
+        int p = 64 * i + lane;
+        if (p > kN - 1) p = kN - 1;
+        int r = p / kCols;
+        const int col = col0 + p - r * kCols;
+        if (r > rvalid - 1) r = rvalid - 1;
+        const uint32_t off = (uint32_t)r * rstride + 16u * (uint32_t)col;  // one 32-bit offset from a uniform base
+        __builtin_amdgcn_global_load_lds(src + off, (__attribute__((address_space(3))) void *)(dst + i * 1024), 16,
+                                         0, 0);
+    }
+}
+// instructions (1-KB pieces) of a run_copy run
+template <int kRows, int kCols>
+__host__ __device__ constexpr int run_copies() {
+    return (kRows * kCols + 63) / 64;
+}
+
 }  // namespace pfng

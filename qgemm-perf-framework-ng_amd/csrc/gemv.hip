@@ -724,6 +724,119 @@ __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma8_kernel(const u
     }
 }
 
+// m = 17..64 at k = 4096: the tile of gemv_q4_0_mfma8_kernel over C chunks of
+// 16 activation rows. Each wave copies its 8-block slice of the 16 weight rows
+// once (144 bytes a row) and widens it once into registers (the nibbles as
+// 16 (q - 8) int8 operands, the fp16 scales); chunk c's activation slice
+// (272 bytes a row) arrives in two halves, H0 = slice bytes 0..143 (blocks
+// 0..3) and H1 = bytes 128..271 (blocks 4..7), each into its own LDS buffer,
+// refilled with chunk c + 1 as soon as the wave has read it (the copy of
+// H0(c + 1) runs while H1(c) is multiplied, H1(c + 1)'s while H0(c + 1) is).
+// Every wait is for the instructions that wrote one buffer (loads complete in
+// issue order). Activation rows past m repeat row m - 1 (not stored).
+constexpr int kQ40ChunkWaveBytes = 9 * 1024;  // weight run, H0, H1: 3 KB each
+
+template <int C>
+__global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(const uint8_t *__restrict__ w,
+                                                                              const uint8_t *__restrict__ a,
+                                                                              float *__restrict__ c, int m, int n) {
+    static_assert(C >= 2 && C <= 4, "17..64 activation rows");
+    constexpr int nb = kMf8Waves * kMf8Blocks;  // k == 4096
+    constexpr uint32_t kARow = nb * 34;
+    constexpr int kH = run_copies<16, 9>();
+    static_assert(kH * 1024 <= 3072, "3 KB per run");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int n0 = blockIdx.x * 16;
+    uint8_t *wl = lds + wave * kQ40ChunkWaveBytes, *h0 = wl + 3072, *h1 = wl + 6144;
+    const uint8_t *asrc = a + wave * kMf8Blocks * 34;  // the wave's slice of activation row 0
+    auto copy_h0 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, lane); };
+    auto copy_h1 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 8, m - 16 * ch, h1, lane); };
+    run_copy<16, 9>(w + ((size_t)n0 * nb + wave * kMf8Blocks) * 18, nb * 18, 0, n - n0, wl, lane);
+    copy_h0(0);
+    copy_h1(0);
+    const int li = lane & 15, q = lane >> 4;
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // weights and H0(0)
+    // the weight slice, once: block j's 8 int8 operands of this lane and its scale
+    const uint8_t *wr = wl + li * 144;
+    uint64_t bop[kMf8Blocks];
+    uint32_t dw[kMf8Blocks];
+#pragma unroll
+    for (int j = 0; j < kMf8Blocks; ++j) {
+        uint32_t wq;
+        if ((j & 1) == 0) {  // two bytes into its dwords
+            const uint32_t *w0 = reinterpret_cast<const uint32_t *>(wr + j * 18 + 4 * q);
+            wq = shift2(w0[0], w0[1]);
+        } else {
+            wq = *reinterpret_cast<const uint32_t *>(wr + j * 18 + 2 + 4 * q);
+        }
+        bop[j] = (uint64_t)q4_0_lo16(wq) | ((uint64_t)q4_0_hi16(wq) << 32);
+        const uint32_t dw_all = *reinterpret_cast<const uint16_t *>(wr + j * 18);  // every lane reads: no branch
+        dw[j] = q == 0 ? dw_all : 0u;
+    }
+    float acc[C][4];
+#pragma unroll
+    for (int ch = 0; ch < C; ++ch) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[ch][r] = 0.0f;
+        // block j of the chunk row li: slice byte 34 j, in H0 (j < 4) or H1 (from slice byte 128)
+        auto block = [&](int j) {
+            const uint8_t *ar = (j < 4 ? h0 + li * 144 : h1 + li * 144 - 128) + j * 34;
+            uint32_t x0, x1;
+            if ((j & 1) == 0) {
+                const uint32_t *a0 = reinterpret_cast<const uint32_t *>(ar + 4 * q);
+                x0 = shift2(a0[0], a0[1]);
+                x1 = shift2(a0[4], a0[5]);
+            } else {
+                const uint32_t *a1 = reinterpret_cast<const uint32_t *>(ar + 2 + 4 * q);
+                x0 = a1[0];
+                x1 = a1[4];
+            }
+            const i32x4 s16 = mfma_i8_16x16x32((uint64_t)x0 | ((uint64_t)x1 << 32), bop[j], (i32x4){0, 0, 0, 0});
+            const uint32_t da_all = *reinterpret_cast<const uint16_t *>(ar);  // every lane reads: no branch
+            const uint32_t da = q == 0 ? da_all : 0u;
+            const f16x4 pa = __builtin_bit_cast(f16x4, make_uint2(da, 0u));
+            const f16x4 pb = __builtin_bit_cast(f16x4, make_uint2(dw[j], 0u));
+            const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, pb, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[ch][r] = __builtin_fmaf((float)s16[r], p[r], acc[ch][r]);
+        };
+        if (ch > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H0(ch)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) block(j);
+        if (ch + 1 < C) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H0 read: refill it
+            copy_h0(ch + 1);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H1(ch)
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+#pragma unroll
+        for (int j = 4; j < kMf8Blocks; ++j) block(j);
+        if (ch + 1 < C) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H1 read: refill it
+            copy_h1(ch + 1);
+        }
+    }
+    // wave partials through LDS ([wave][group g = 4 chunk + r][lane]); wave w
+    // adds groups w, w + 16, ... over the waves in wave order and stores them
+    __syncthreads();
+    float *red = reinterpret_cast<float *>(lds);
+#pragma unroll
+    for (int ch = 0; ch < C; ++ch)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[((wave * C + ch) * 4 + r) * 64 + lane] = acc[ch][r];
+    __syncthreads();
+    const int col = n0 + li;
+    for (int g = wave; g < 4 * C; g += kMf8Waves) {
+        float s = red[g * 64 + lane];
+        for (int v = 1; v < kMf8Waves; ++v) s += red[(v * 4 * C + g) * 64 + lane];
+        const int row = 16 * (g / 4) + 4 * q + g % 4;
+        if (col < n && row < m) c[(size_t)row * n + col] = s * 0.0625f;
+    }
+}
+
 // Fused activation quantization + GEMV (m <= 2): each workgroup quantizes the
 // m fp32 activation rows into q8_0 blocks in LDS (the same arithmetic as
 // quantize_q8_0_kernel, so the bytes equal the standalone quantizer's), then
@@ -927,6 +1040,7 @@ bool gemv_supported(int type, int64_t m, int64_t k) {
     if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) {
         if (m == 1) return k % 64 == 0;
         if (m <= 8) return k % 256 == 0 || pairs;
+        if (m > 16) return m <= 64 && k == 4096;  // gemv_q4_0_mfma_chunk_kernel
         return m <= kPairsMaxM && pairs;  // m = 9..16 only in the pair-per-lane kernel
     }
     // q4_K and iq2_xxs (gemv_kquant.hip): m <= 8 for every k % 256 == 0,
@@ -969,8 +1083,19 @@ hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t
     case 14: return launch_gemv_q4_0_m<14>(w, a, c, n, k, stream);
     case 15: return launch_gemv_q4_0_m<15>(w, a, c, n, k, stream);
     case 16: return launch_gemv_q4_0_m<16>(w, a, c, n, k, stream);
-    default: return hipErrorInvalidValue;
+    default: break;
     }
+    if (!(m >= 17 && m <= 64 && k == 4096)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((n + 15) / 16)), block(kMf8Waves * 64);
+    const size_t lds = (size_t)kMf8Waves * kQ40ChunkWaveBytes;
+    const auto *wp = static_cast<const uint8_t *>(w);
+    const auto *ap = static_cast<const uint8_t *>(a);
+    switch ((m + 15) / 16) {
+    case 2: hipLaunchKernelGGL(gemv_q4_0_mfma_chunk_kernel<2>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n); break;
+    case 3: hipLaunchKernelGGL(gemv_q4_0_mfma_chunk_kernel<3>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n); break;
+    default: hipLaunchKernelGGL(gemv_q4_0_mfma_chunk_kernel<4>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n); break;
+    }
+    return hipGetLastError();
 }
 
 }  // namespace pfng

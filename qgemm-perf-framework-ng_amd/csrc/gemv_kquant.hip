@@ -1237,32 +1237,8 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_sb_kernel(c
 // copy of H0(c + 1) runs while H1(c) is multiplied and the copy of H1(c + 1)
 // while H0(c + 1) is. Every wait is for the instructions that wrote one
 // buffer (loads complete in issue order). Activation rows past m repeat row
-// m - 1 (their results are not stored).
-//
-// One flat run of kRows x kCols 16-byte chunks into LDS at dst: chunk
-// (r, j) from src + r * rstride + 16 (col0 + j), 64 chunks per instruction,
-// every lane active (lanes past the end repeat the last chunk into the pad
-// that follows the run); rows at or past rvalid repeat row rvalid - 1.
-template <int kRows, int kCols>
-__device__ __forceinline__ void run_copy(const uint8_t *src, uint32_t rstride, int col0, int rvalid, uint8_t *dst,
-                                         int lane) {
-    constexpr int kN = kRows * kCols;
-#pragma unroll
-    for (int i = 0; i < (kN + 63) / 64; ++i) {
-        int p = 64 * i + lane;
-        if (p > kN - 1) p = kN - 1;
-        int r = p / kCols;
-        const int col = col0 + p - r * kCols;
-        if (r > rvalid - 1) r = rvalid - 1;
-        __builtin_amdgcn_global_load_lds(src + (uint32_t)r * rstride + 16u * (uint32_t)col,
-                                         (__attribute__((address_space(3))) void *)(dst + i * 1024), 16, 0, 0);
-    }
-}
-template <int kRows, int kCols>
-__host__ __device__ constexpr int run_copies() {
-    return (kRows * kCols + 63) / 64;
-}
-
+// m - 1 (their results are not stored). The copies are run_copy runs
+// (device_common.h).
 constexpr int kChunkWaveBytes = 9 * 1024;  // per wave: weight run, H0, H1 (3 KB each)
 
 __host__ __device__ constexpr int q4k_chunk_lds_bytes() { return kKqMfWaves * kChunkWaveBytes; }

@@ -205,3 +205,38 @@ def test_half_split_copy_order(source, kernel, copies, after_half0):
     with open(out) as f:
         asm = f.read()
     check_half_split(_kernel_lines(asm, kernel), copies, after_half0)
+
+
+def check_chunk_waits(lines: list[str], chunks: int, table_wait: int | None = None) -> None:
+    """The chunked MFMA tile GEMVs (m = 17..64): no scratch memory (spill
+    loads and stores would count in vmcnt and break the waits' arithmetic), and
+    the vector-memory waits are exactly the designed ones: the table copy
+    (iq2_xxs), then one vmcnt(3) before each half of each chunk but the last,
+    which waits for everything."""
+    assert not any(t.startswith("scratch_") or "buffer_store" in t for t in lines), "register spills"
+    waits = [int(re.search(r"vmcnt\((\d+)\)", t).group(1)) for t in lines if re.match(r"s_waitcnt .*vmcnt", t)]
+    expect = ([table_wait] if table_wait is not None else []) + [3] * (2 * chunks - 1) + [0]
+    assert waits[:len(expect)] == expect, f"waits {waits}, expected to start {expect}"
+
+
+def test_chunk_wait_checker():
+    lines = ["global_load_lds_dwordx4 v[2:3], off", "s_waitcnt vmcnt(3)", "ds_read_b32 v1, v2", "s_waitcnt vmcnt(3)",
+             "s_waitcnt vmcnt(3)", "s_waitcnt vmcnt(0)", "s_barrier"]
+    check_chunk_waits(lines, 2)
+    with pytest.raises(AssertionError):  # an extra full wait inside the chunks
+        check_chunk_waits(lines[:2] + ["s_waitcnt vmcnt(0)"] + lines[2:], 2)
+    with pytest.raises(AssertionError):
+        check_chunk_waits(lines[:2] + ["scratch_store_dword off, v1, off"] + lines[2:], 2)
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC) or shutil.which("make") is None, reason="needs hipcc and make")
+@pytest.mark.parametrize("source,kernel,table_wait", [("gemv.hip", "gemv_q4_0_mfma_chunk_kernel", None),
+                                                      ("gemv_kquant.hip", "gemv_q4_K_mfma_chunk_kernel", None),
+                                                      ("gemv_kquant.hip", "gemv_iq2_xxs_mfma_chunk_kernel", 8)])
+@pytest.mark.parametrize("chunks", [2, 3, 4])
+def test_chunked_gemv_waits(source, kernel, table_wait, chunks):
+    out = os.path.join(PKG_DIR, "_build", source + ".s")
+    subprocess.run(["make", "-s", "-C", PKG_DIR, out], check=True, capture_output=True, timeout=600)
+    with open(out) as f:
+        asm = f.read()
+    check_chunk_waits(_kernel_lines(asm, f"{kernel}ILi{chunks}E"), chunks, table_wait)

@@ -191,6 +191,26 @@ def test_gemv_q4_0(hip, torch_gpu, oracle, m, n, k):
     check_close(oracle, 0, got, w, aq, m, n, k, label=f"gemv m={m} n={n} k={k}")
 
 
+@pytest.mark.parametrize("m", [17, 20, 31, 32, 33, 47, 48, 49, 63, 64])
+@pytest.mark.parametrize("n", [4096, 37, 1])
+def test_gemv_q4_0_chunked(hip, torch_gpu, oracle, m, n):
+    """k = 4096, m = 17..64: the 16-row MFMA tile over chunks of 16 activation
+    rows (each chunk's halves refilled while the other half is multiplied), a
+    partial last chunk and tile; the generator's inputs, then random weight
+    bytes against activations at the int8 limits."""
+    torch = torch_gpu
+    k = 4096
+    say(f"gemv q4_0 chunked m={m} n={n}")
+    act, w = oracle.create_input(0, m, n, k, seed=m * 13 + n)
+    aq = oracle.quantize_q8_0(act)
+    got = run_mul_mat(hip, torch, 0, w, aq, m, n, k, hip.PATH_GEMV)
+    check_close(oracle, 0, got, w, aq, m, n, k, label=f"gemv chunked m={m} n={n}")
+    wr = random_weight_blocks(oracle, 0, n, k, seed=71 + m)
+    ax = oracle.quantize_q8_0(np.where(np.random.default_rng(m).random((m, k)) < 0.5, -1.0, 1.0).astype(np.float32))
+    got = run_mul_mat(hip, torch, 0, wr, ax, m, n, k, hip.PATH_GEMV)
+    check_close(oracle, 0, got, wr, ax, m, n, k, label=f"gemv chunked random bytes m={m} n={n}")
+
+
 # ------------------------------------------------------------------- MFMA ----
 
 @pytest.mark.parametrize("m,n,k", [(32, 32, 128), (100, 77, 256), (480, 1536, 1536), (9, 300, 640), (2048, 4096, 256),
