@@ -322,6 +322,9 @@ __device__ __forceinline__ void run_copy(const uint8_t *src, uint32_t rstride, i
                                          0, 0);
     }
 }
+// chunks of 16 activation rows the chunked MFMA tile GEMVs take (m <= 128)
+constexpr int kMaxGemvChunks = 8;
+
 // instructions (1-KB pieces) of a run_copy run
 template <int kRows, int kCols>
 __host__ __device__ constexpr int run_copies() {

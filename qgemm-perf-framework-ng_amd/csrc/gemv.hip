@@ -740,11 +740,12 @@ template <int C>
 __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(const uint8_t *__restrict__ w,
                                                                               const uint8_t *__restrict__ a,
                                                                               float *__restrict__ c, int m, int n) {
-    static_assert(C >= 2 && C <= 4, "17..64 activation rows");
+    static_assert(C >= 2 && C <= kMaxGemvChunks, "17 or more activation rows, at most kMaxGemvChunks chunks");
     constexpr int nb = kMf8Waves * kMf8Blocks;  // k == 4096
     constexpr uint32_t kARow = nb * 34;
     constexpr int kH = run_copies<16, 9>();
     static_assert(kH * 1024 <= 3072, "3 KB per run");
+    static_assert(kMf8Waves * 4 * C * 64 * 4 <= kMf8Waves * kQ40ChunkWaveBytes, "wave partials fit the LDS");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -1040,7 +1041,7 @@ bool gemv_supported(int type, int64_t m, int64_t k) {
     if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) {
         if (m == 1) return k % 64 == 0;
         if (m <= 8) return k % 256 == 0 || pairs;
-        if (m > 16) return m <= 64 && k == 4096;  // gemv_q4_0_mfma_chunk_kernel
+        if (m > 16) return m <= 16 * kMaxGemvChunks && k == 4096;  // gemv_q4_0_mfma_chunk_kernel
         return m <= kPairsMaxM && pairs;  // m = 9..16 only in the pair-per-lane kernel
     }
     // q4_K and iq2_xxs (gemv_kquant.hip): m <= 8 for every k % 256 == 0,
@@ -1085,16 +1086,26 @@ hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t
     case 16: return launch_gemv_q4_0_m<16>(w, a, c, n, k, stream);
     default: break;
     }
-    if (!(m >= 17 && m <= 64 && k == 4096)) return hipErrorInvalidValue;
+    if (!(m >= 17 && m <= 16 * kMaxGemvChunks && k == 4096)) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((n + 15) / 16)), block(kMf8Waves * 64);
     const size_t lds = (size_t)kMf8Waves * kQ40ChunkWaveBytes;
     const auto *wp = static_cast<const uint8_t *>(w);
     const auto *ap = static_cast<const uint8_t *>(a);
+#define PFNG_Q40_CHUNK_CASE(C)                                                                                      \
+    case C:                                                                                                        \
+        hipLaunchKernelGGL(gemv_q4_0_mfma_chunk_kernel<C>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n); \
+        break;
     switch ((m + 15) / 16) {
-    case 2: hipLaunchKernelGGL(gemv_q4_0_mfma_chunk_kernel<2>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n); break;
-    case 3: hipLaunchKernelGGL(gemv_q4_0_mfma_chunk_kernel<3>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n); break;
-    default: hipLaunchKernelGGL(gemv_q4_0_mfma_chunk_kernel<4>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n); break;
+        PFNG_Q40_CHUNK_CASE(2)
+        PFNG_Q40_CHUNK_CASE(3)
+        PFNG_Q40_CHUNK_CASE(4)
+        PFNG_Q40_CHUNK_CASE(5)
+        PFNG_Q40_CHUNK_CASE(6)
+        PFNG_Q40_CHUNK_CASE(7)
+        PFNG_Q40_CHUNK_CASE(8)
+    default: return hipErrorInvalidValue;
     }
+#undef PFNG_Q40_CHUNK_CASE
     return hipGetLastError();
 }
 

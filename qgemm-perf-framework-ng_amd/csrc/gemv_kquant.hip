@@ -1247,11 +1247,12 @@ template <int C>
 __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(const uint8_t *__restrict__ w,
                                                                              const uint8_t *__restrict__ a,
                                                                              float *__restrict__ c, int m, int n) {
-    static_assert(C >= 2 && C <= 4, "17..64 activation rows");
+    static_assert(C >= 2 && C <= kMaxGemvChunks, "17 or more activation rows, at most kMaxGemvChunks chunks");
     constexpr int nsb = kKqMfWaves;  // k == 4096
     constexpr uint32_t kARow = nsb * kQ8KBytes;
     constexpr int kH = run_copies<16, 11>();  // instructions per half (H1: 11 columns, H0: 9)
     static_assert(run_copies<16, 9>() == kH && run_copies<16, 9>() * 1024 <= 3072, "3 KB per run");
+    static_assert(kKqMfWaves * 4 * C * 64 * 4 <= q4k_chunk_lds_bytes(), "wave partials fit the LDS");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -1356,12 +1357,13 @@ template <int C>
 __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kernel(const uint8_t *__restrict__ w,
                                                                                 const uint8_t *__restrict__ a,
                                                                                 float *__restrict__ c, int m, int n) {
-    static_assert(C >= 2 && C <= 4, "17..64 activation rows");
+    static_assert(C >= 2 && C <= kMaxGemvChunks, "17 or more activation rows, at most kMaxGemvChunks chunks");
     constexpr int nsb = kKqMfWaves;  // k == 4096
     constexpr uint32_t kARow = nsb * kQ8KBytes;
     constexpr int kH = run_copies<16, 9>();
     constexpr int kW = run_copies<16, 5>();
     static_assert(kH * 1024 <= 3072 && kW * 1024 <= 2048, "run sizes");
+    static_assert(kKqMfWaves * 4 * C * 64 * 4 <= iq2_chunk_lds_bytes(), "wave partials fit the LDS");
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t *grid = lds;  // grid magnitudes, then sign masks
     const int lane = threadIdx.x & 63;
@@ -1567,7 +1569,7 @@ bool kquant_gemv_staged_fits(int64_t m, int64_t k) {
     return m >= 2 && m <= 16 && k % 256 == 0 && kq_staged_lds_bytes(m, k / 256) <= 160 * 1024;
 }
 
-bool kquant_gemv_chunked_fits(int64_t m, int64_t k) { return m >= 17 && m <= 64 && k == 4096; }
+bool kquant_gemv_chunked_fits(int64_t m, int64_t k) { return m >= 17 && m <= 16 * kMaxGemvChunks && k == 4096; }
 
 hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                               hipStream_t stream) {
@@ -1610,6 +1612,10 @@ hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, 
         PFNG_CHUNK_CASE(2)
         PFNG_CHUNK_CASE(3)
         PFNG_CHUNK_CASE(4)
+        PFNG_CHUNK_CASE(5)
+        PFNG_CHUNK_CASE(6)
+        PFNG_CHUNK_CASE(7)
+        PFNG_CHUNK_CASE(8)
     default: return hipErrorInvalidValue;
     }
 #undef PFNG_CHUNK_CASE

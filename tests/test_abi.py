@@ -82,11 +82,11 @@ def test_argument_validation(pkg, call, expect):
 
 @pytest.mark.parametrize("qtype,m,n,k,expect", [
     (0, 1, 4096, 4096, 1), (0, 16, 4096, 4096, 1), (0, 17, 4096, 4096, 1), (0, 64, 4096, 4096, 1),
-    (0, 65, 4096, 4096, 2), (0, 17, 4096, 8192, 2), (0, 480, 1536, 1536, 2),
+    (0, 128, 4096, 4096, 1), (0, 129, 4096, 4096, 2), (0, 17, 4096, 8192, 2), (0, 480, 1536, 1536, 2),
     (0, 3, 5, 96, -1), (0, 17, 8, 96, -1), (0, 24, 32, 256, 2), (0, 0, 8, 64, 0),
     (1, 8, 64, 512, 1), (1, 480, 1536, 1536, 2), (2, 512, 4096, 4096, 2), (2, 1, 4096, 4096, 1),
-    # q4_K / iq2_xxs at k = 4096 keep the GEMV path up to m = 64 (chunks of 16 activation rows)
-    (1, 32, 4096, 4096, 1), (2, 64, 4096, 4096, 1), (2, 65, 4096, 4096, 2), (1, 17, 4096, 8192, 2),
+    # q4_K / iq2_xxs at k = 4096 keep the GEMV path up to m = 128 (chunks of 16 activation rows)
+    (1, 32, 4096, 4096, 1), (2, 128, 4096, 4096, 1), (2, 129, 4096, 4096, 2), (1, 17, 4096, 8192, 2),
     (0, 4, 4, 48, -1), (3, 4, 4, 64, -1),
 ])
 def test_auto_path_query(pkg, qtype, m, n, k, expect):

@@ -208,7 +208,7 @@ def test_half_split_copy_order(source, kernel, copies, after_half0):
 
 
 def check_chunk_waits(lines: list[str], chunks: int, table_wait: int | None = None) -> None:
-    """The chunked MFMA tile GEMVs (m = 17..64): no scratch memory (spill
+    """The chunked MFMA tile GEMVs (m = 17..128): no scratch memory (spill
     loads and stores would count in vmcnt and break the waits' arithmetic), and
     the vector-memory waits are exactly the designed ones: the table copy
     (iq2_xxs), then one vmcnt(3) before each half of each chunk but the last,
@@ -233,7 +233,7 @@ def test_chunk_wait_checker():
 @pytest.mark.parametrize("source,kernel,table_wait", [("gemv.hip", "gemv_q4_0_mfma_chunk_kernel", None),
                                                       ("gemv_kquant.hip", "gemv_q4_K_mfma_chunk_kernel", None),
                                                       ("gemv_kquant.hip", "gemv_iq2_xxs_mfma_chunk_kernel", 8)])
-@pytest.mark.parametrize("chunks", [2, 3, 4])
+@pytest.mark.parametrize("chunks", [2, 3, 4, 8])
 def test_chunked_gemv_waits(source, kernel, table_wait, chunks):
     out = os.path.join(PKG_DIR, "_build", source + ".s")
     subprocess.run(["make", "-s", "-C", PKG_DIR, out], check=True, capture_output=True, timeout=600)

@@ -191,10 +191,10 @@ def test_gemv_q4_0(hip, torch_gpu, oracle, m, n, k):
     check_close(oracle, 0, got, w, aq, m, n, k, label=f"gemv m={m} n={n} k={k}")
 
 
-@pytest.mark.parametrize("m", [17, 20, 31, 32, 33, 47, 48, 49, 63, 64])
+@pytest.mark.parametrize("m", [17, 20, 31, 32, 33, 47, 48, 49, 63, 64, 65, 96, 127, 128])
 @pytest.mark.parametrize("n", [4096, 37, 1])
 def test_gemv_q4_0_chunked(hip, torch_gpu, oracle, m, n):
-    """k = 4096, m = 17..64: the 16-row MFMA tile over chunks of 16 activation
+    """k = 4096, m = 17..128: the 16-row MFMA tile over chunks of 16 activation
     rows (each chunk's halves refilled while the other half is multiplied), a
     partial last chunk and tile; the generator's inputs, then random weight
     bytes against activations at the int8 limits."""
@@ -486,10 +486,10 @@ def test_gemv_kquant_random_bytes_and_extremes(hip, torch_gpu, oracle, qtype):
 
 
 @pytest.mark.parametrize("qtype", [1, 2])
-@pytest.mark.parametrize("m", list(range(5, 17)) + [17, 20, 31, 32, 33, 47, 48, 49, 63, 64])
+@pytest.mark.parametrize("m", list(range(5, 17)) + [17, 20, 31, 32, 33, 47, 48, 49, 63, 64, 65, 96, 127, 128])
 @pytest.mark.parametrize("n", [4096, 37, 1])
 def test_gemv_kquant_one_superblock_per_wave(hip, torch_gpu, oracle, qtype, m, n):
-    """k = 4096, m = 5..64: 16-row MFMA tiles with one super-block per wave
+    """k = 4096, m = 5..128: 16-row MFMA tiles with one super-block per wave
     (from m = 17 over chunks of 16 activation rows, each chunk's halves
     refilled while the other half is multiplied),
     each wave's weight and activation blocks copied in two halves of 16-byte
