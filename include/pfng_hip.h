@@ -42,21 +42,28 @@ typedef enum {
 } pfng_status;
 
 /* Matrix-product implementations; PFNG_PATH_AUTO picks per shape (the GEMV
- * where it applies, up to m = 16; then the MFMA tiles) and returns
- * PFNG_ERR_UNSUPPORTED when neither applies (see pfng_hip_auto_path). */
+ * where it applies, up to m = 16, and up to m = 128 at k == 4096; then the
+ * MFMA tiles) and returns PFNG_ERR_UNSUPPORTED when neither applies (see
+ * pfng_hip_auto_path). */
 typedef enum {
     PFNG_PATH_AUTO = 0,
-    PFNG_PATH_GEMV = 1,  /* the decode-batch kernels (wavefront-per-row GEMVs;
-                            from m = 9 16x16 int8-MFMA tiles with K split over
-                            the waves, for q4_0 at k % 4096 == 0 or, from
-                            m = 12, k % 2048 == 0, q4_K at k % 4096 == 0 and
-                            iq2_xxs at k == 4096, while their slices fit LDS):
-                            q4_0 for m <= 16 with k % 64 == 0 for m == 1; for
-                            m = 2..16 when the LDS-staged activations fit,
-                            k % 64 == 0 and m * (k / 64) * 76 + 16 <= 163840,
-                            and for m = 2..8 also every k % 256 == 0; q4_K and
-                            iq2_xxs with k % 256 == 0 for m <= 8, and for
-                            m = 9..16 while m * (k / 256) * 320 + 3072 <= 163840 */
+    PFNG_PATH_GEMV = 1,  /* the decode-batch kernels. Shapes taken:
+                            q4_0: m == 1 with k % 64 == 0; m = 2..8 with
+                            k % 256 == 0, or k % 64 == 0 while
+                            m * (k / 64) * 76 + 16 <= 163840; m = 9..16 with
+                            k % 64 == 0 under that same LDS bound;
+                            m = 17..128 with k == 4096.
+                            q4_K and iq2_xxs: m <= 8 with k % 256 == 0;
+                            m = 9..16 while m * (k / 256) * 320 + 3072 <= 163840;
+                            m = 17..128 with k == 4096.
+                            Kernels: wavefront-per-row GEMVs for short batches;
+                            16x16 int8-MFMA tiles with K split over 16 waves at
+                            k == 4096 from m = 7 (q4_0) and m = 5 (q4_K,
+                            iq2_xxs), and at larger k % 4096 == 0 from m = 9
+                            (q4_0, q4_K; q4_0 also from m = 12 at
+                            k % 2048 == 0); from m = 17 (k == 4096) the same
+                            tiles over chunks of 16 activation rows, the
+                            weights decoded once per wave */
     PFNG_PATH_MFMA = 2,  /* int8-MFMA GEMM, LDS-staged tiles: q4_0 with k % 128 == 0,
                             q4_K and iq2_xxs for every k % 256 == 0 */
     PFNG_PATH_NAIVE = 3  /* one thread per output, the reference's exact fp32 order */
