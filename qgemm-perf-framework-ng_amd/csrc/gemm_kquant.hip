@@ -15,8 +15,9 @@
 // workgroup stages into LDS:
 //   * activation int8 rows as they are, the q8_K scale and (q4_K) the eight
 //     16-element bsums of the half as fp16 (|bsum| <= 2032 is exact in fp16);
-//   * weight values expanded to one int8 per element (q4_K nibble 0..15,
-//     iq2_xxs signed grid value), the sub-block scales and the fp16 scales.
+//   * weight values expanded to int8 (q4_K nibble 0..15 and the sub-block
+//     scale digits; iq2_xxs two planes of the scaled value), and the fp16
+//     scales.
 // q4_K: sc (0..63) = 8*h + l with octal digits h, l. Two int8 weight planes
 // q*l and q*h (both <= 105) are formed per fragment with one packed 16-bit
 // multiply per dword (the byte products cannot carry), and two int8 MFMAs per
@@ -24,9 +25,13 @@
 // S_L with no per-sub-block VALU work. IM is one fp16 MFMA per stage over the
 // bsums and the mins (exact: every product and partial sum is an integer below
 // 2^24).
-// iq2_xxs: the scale times a grid value does not fit int8 in two digits, so
-// S_j comes from one int8 MFMA and IS += S_j * (2 s_j + 1) is an exact 24-bit
-// multiply-add per result.
+// iq2_xxs: the staged value is the grid value times its sub-block scale,
+// w' = sign * mag * (2 s + 1) with |w'| <= 43 * 31 = 1333, split as
+// w' = 128 * hi + lo with lo in 0..127 and hi in -11..10 (both int8). Two
+// int8 MFMAs per sub-block accumulate S_LO and S_HI over the whole
+// super-block, so IS = 128 * S_HI + S_LO exactly, again with no per-sub-block
+// VALU work. The split is a byte lookup (v_perm) into a per-scale table of the
+// six (lo, hi) pairs of +-8, +-25, +-43 times the scale.
 // A diagnostic instantiation writes the int32 super-block sums instead of C.
 #include "device_common.h"
 #include "kernels.h"
@@ -62,15 +67,21 @@ struct KqConfig {
     static constexpr int kAq = 0;                                   // int8 [BM][kRowStride]
     static constexpr int kAd = kAq + BM * kRowStride;               // fp32 [BM] activation scale
     static constexpr int kAb = kAd + BM * 4;                        // q4_K: fp16 [BM][8] bsums of the half
-    static constexpr int kWq = kAb + (kQ4K ? BM * 16 : 0);          // int8 [BN][kRowStride]
-    static constexpr int kWs = kWq + BN * kRowStride;               // q4_K: u32 [BN][4][2] digit pairs; iq2: i32 [BN][4]
-    static constexpr int kWd = kWs + BN * (kQ4K ? 32 : 16);         // fp32 [BN] d (iq2: 0.125 * d)
+    static constexpr int kWq = kAb + (kQ4K ? BM * 16 : 0);          // int8 [BN][kRowStride] (iq2: the lo plane)
+    static constexpr int kWq2 = kWq + BN * kRowStride;              // iq2: int8 [BN][kRowStride] hi plane
+    static constexpr int kWs = kWq2 + (kQ4K ? 0 : BN * kRowStride); // q4_K: u32 [BN][4][2] digit pairs
+    static constexpr int kWd = kWs + (kQ4K ? BN * 32 : 0);          // fp32 [BN] d (iq2: 0.125 * d)
     static constexpr int kWdm = kWd + BN * 4;                       // q4_K: fp32 [BN] dmin
     static constexpr int kWmin = kWdm + (kQ4K ? BN * 4 : 0);        // q4_K: fp16 [BN][8] mins, each twice
     static constexpr int kBufBytes = kWmin + (kQ4K ? BN * 16 : 0);
     static constexpr int kSliceBytes = 2 * kBufBytes;                // a slice's two stage buffers
-    static constexpr int kGrid = WS * kSliceBytes;                   // iq2: 256 x 8-byte grid magnitudes
-    static constexpr int kLdsBytes = kGrid + (kQ4K ? 0 : 256 * 8 + 128 * 8);
+    // iq2 tables after the slices: 256 x 8 grid code bytes (0, 1, 2 for 8, 25,
+    // 43), 128 x 8 sign selector bytes (4 where the value is negative), and
+    // per scale s the (lo, hi) byte pairs of the six signed products
+    static constexpr int kGrid = WS * kSliceBytes;
+    static constexpr int kSigns = kGrid + 256 * 8;
+    static constexpr int kScaleTab = kSigns + 128 * 8;
+    static constexpr int kLdsBytes = kGrid + (kQ4K ? 0 : 256 * 8 + 128 * 8 + 16 * 16);
     static constexpr int kAllThreads = kThreads * WS;
     // global -> register tasks per stage: each activation row in kActE parts
     // (2 or 4) of its 128 int8 and 8 bsums, each weight row per sub-block
@@ -83,7 +94,7 @@ struct KqConfig {
     static_assert(kActE == 2 || kActE == 4, "activation rows split in 2 or 4 parts");
     static_assert(kActPT * kThreads == BM * kActE && kWPT * kThreads == BN * kSub, "tasks must split evenly");
     static_assert(kActPT >= 1 && kWPT >= 1, "every thread takes at least one task of each operand");
-    static_assert(kAd % 16 == 0 && kAb % 16 == 0 && kWq % 16 == 0 && kWs % 16 == 0 && kWd % 16 == 0 &&
+    static_assert(kAd % 16 == 0 && kAb % 16 == 0 && kWq % 16 == 0 && kWq2 % 16 == 0 && kWs % 16 == 0 && kWd % 16 == 0 &&
                       kWdm % 16 == 0 && kWmin % 16 == 0 && kBufBytes % 16 == 0,
                   "LDS regions 16-byte aligned");
     static_assert(kWaveSub * WK == kSub, "the stage's sub-blocks split evenly over the K-waves");
@@ -202,7 +213,8 @@ __device__ __forceinline__ void q4_K_scale_min(const uint32_t hd[4], int j, uint
 
 template <class C>
 __device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int h, int tid, const KqRegs<C> &r) {
-    const uint8_t *signs = grid + 256 * 8;
+    const uint8_t *signs = grid + (C::kSigns - C::kGrid);
+    const uint8_t *scale_tab = grid + (C::kScaleTab - C::kGrid);
 #pragma unroll
     for (int it = 0; it < C::kActPT; ++it) {
         const int task = tid + it * C::kThreads;
@@ -254,24 +266,31 @@ __device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int 
             *reinterpret_cast<float *>(lds + C::kWdm + row * 4) = fp16_to_f32(r.wh[it][0] >> 16);
         } else {
             // iq2_xxs sub-block (kernels/common/iq2_xxs.h:29-41): four groups of
-            // 8 values, magnitudes from the grid, signs from the mask table
-            // (0xff in byte j where bit j of idx | parity(idx) << 7 is set, idx
-            // the 7-bit field g of the last dword), scale 2 * (bits 28..31) + 1
+            // 8 values. A value's selector byte is its grid code (0, 1, 2 for
+            // magnitude 8, 25, 43) plus 4 where it is negative (bit j of
+            // idx | parity(idx) << 7, idx the 7-bit field g of the last dword);
+            // it picks the lo and hi bytes of w' = +-mag * (2 * (bits 28..31) + 1)
+            // from the scale's table (x: lo of the positive products, y: lo of
+            // the negative ones, z / w: the hi bytes)
             const uint32_t gidx = r.wq[it][0], ss = r.wq[it][1];
-            uint32_t out[8];
+            const uint4 tab = *reinterpret_cast<const uint4 *>(scale_tab + 16 * (ss >> 28));
+            uint32_t lo[8], hi[8];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const uint2 mag = *reinterpret_cast<const uint2 *>(grid + ((gidx >> (8 * g)) & 0xffu) * 8);
+                const uint2 code = *reinterpret_cast<const uint2 *>(grid + ((gidx >> (8 * g)) & 0xffu) * 8);
                 const uint2 neg = *reinterpret_cast<const uint2 *>(signs + ((ss >> (7 * g)) & 0x7fu) * 8);
-                // magnitudes are >= 8, so (x ^ 0xff) + 1 negates a byte without
-                // a carry into its neighbour
-                out[2 * g] = (mag.x ^ neg.x) + (neg.x & 0x01010101u);
-                out[2 * g + 1] = (mag.y ^ neg.y) + (neg.y & 0x01010101u);
+                const uint32_t s0 = code.x | neg.x, s1 = code.y | neg.y;
+                lo[2 * g] = __builtin_amdgcn_perm(tab.y, tab.x, s0);
+                lo[2 * g + 1] = __builtin_amdgcn_perm(tab.y, tab.x, s1);
+                hi[2 * g] = __builtin_amdgcn_perm(tab.w, tab.z, s0);
+                hi[2 * g + 1] = __builtin_amdgcn_perm(tab.w, tab.z, s1);
             }
-            uint4 *dst = reinterpret_cast<uint4 *>(wrow + 32 * e);
-            dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
-            dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
-            *reinterpret_cast<int32_t *>(lds + C::kWs + row * 16 + 4 * e) = 2 * (int32_t)(ss >> 28) + 1;
+            uint4 *dlo = reinterpret_cast<uint4 *>(wrow + 32 * e);
+            uint4 *dhi = reinterpret_cast<uint4 *>(lds + C::kWq2 + row * C::kRowStride + 32 * e);
+            dlo[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            dlo[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+            dhi[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            dhi[1] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
             *reinterpret_cast<float *>(lds + C::kWd + row * 4) = 0.125f * fp16_to_f32(r.wh[it][0]);
         }
     }
@@ -281,8 +300,8 @@ __device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int 
 template <class C>
 struct KqAcc {
     f32x16 acc[C::TM][C::TN];  // fp32 output
-    i32x16 s0[C::TM][C::TN];   // q4_K: S_L; iq2_xxs: IS
-    i32x16 s1[C::TM][C::TN];   // q4_K: S_H
+    i32x16 s0[C::TM][C::TN];   // q4_K: S_L; iq2_xxs: S_LO
+    i32x16 s1[C::TM][C::TN];   // q4_K: S_H; iq2_xxs: S_HI
     f32x16 im[C::TM][C::TN];   // q4_K: IM (exact integers)
 };
 
@@ -349,26 +368,27 @@ __device__ __forceinline__ void kq_compute(const uint8_t *buf, KqAcc<C> &A, int 
             for (int tn = 0; tn < C::TN; ++tn)
                 A.im[tm][tn] = mfma_f16_32x32x8(ab[tm], wm[tn], H == 0 ? (f32x16){} : A.im[tm][tn]);
     } else {
+        // S_LO and S_HI over the lo and hi planes of the scaled values
+        const uint8_t *wq2 = wq + (C::kWq2 - C::kWq);
 #pragma unroll
         for (int j = 0; j < C::kWaveSub; ++j) {
             const int t = tb + j;
-            i32x4 av[C::TM], wv[C::TN];
+            i32x4 av[C::TM], wl[C::TN], wh[C::TN];
 #pragma unroll
             for (int tm = 0; tm < C::TM; ++tm)
                 av[tm] = *reinterpret_cast<const i32x4 *>(aq + tm * 32 * C::kRowStride + t * 32);
 #pragma unroll
-            for (int tn = 0; tn < C::TN; ++tn)
-                wv[tn] = *reinterpret_cast<const i32x4 *>(wq + tn * 32 * C::kRowStride + t * 32);
+            for (int tn = 0; tn < C::TN; ++tn) {
+                wl[tn] = *reinterpret_cast<const i32x4 *>(wq + tn * 32 * C::kRowStride + t * 32);
+                wh[tn] = *reinterpret_cast<const i32x4 *>(wq2 + tn * 32 * C::kRowStride + t * 32);
+            }
 #pragma unroll
             for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
                 for (int tn = 0; tn < C::TN; ++tn) {
-                    const i32x16 sb = mfma_i8_32x32x32(av[tm], wv[tn], (i32x16){});
-                    const int scale = *reinterpret_cast<const int32_t *>(buf + C::kWs + (wrow + tn * 32) * 16 + 4 * t);
-#pragma unroll
-                    for (int q = 0; q < 16; ++q)
-                        A.s0[tm][tn][q] = (H == 0 && j == 0) ? __mul24(sb[q], scale)
-                                                             : __mul24(sb[q], scale) + A.s0[tm][tn][q];
+                    const bool first = H == 0 && j == 0;
+                    A.s0[tm][tn] = mfma_i8_32x32x32(av[tm], wl[tn], first ? (i32x16){} : A.s0[tm][tn]);
+                    A.s1[tm][tn] = mfma_i8_32x32x32(av[tm], wh[tn], first ? (i32x16){} : A.s1[tm][tn]);
                 }
         }
     }
@@ -394,7 +414,7 @@ __device__ __forceinline__ void kq_epilogue(const uint8_t *buf, KqAcc<C> &A, int
                             isums[2 * o] = 8 * A.s1[tm][tn][q] + A.s0[tm][tn][q];
                             isums[2 * o + 1] = (int32_t)A.im[tm][tn][q];
                         } else {
-                            isums[o] = A.s0[tm][tn][q];
+                            isums[o] = 128 * A.s1[tm][tn][q] + A.s0[tm][tn][q];
                         }
                     }
                 }
@@ -430,7 +450,7 @@ __device__ __forceinline__ void kq_epilogue(const uint8_t *buf, KqAcc<C> &A, int
                     const f32x16 pr = __builtin_amdgcn_mfma_f32_32x32x2f32(adl, lh ? 0.0f : d, (f32x16){}, 0, 0, 0);
 #pragma unroll
                     for (int q = 0; q < 16; ++q)
-                        A.acc[tm][tn][q] = fmaf(pr[q], (float)A.s0[tm][tn][q], A.acc[tm][tn][q]);
+                        A.acc[tm][tn][q] = fmaf(pr[q], (float)(128 * A.s1[tm][tn][q] + A.s0[tm][tn][q]), A.acc[tm][tn][q]);
                 }
             }
         }
@@ -458,28 +478,38 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
     uint8_t *buf0 = lds + slice * C::kSliceBytes;
     uint8_t *buf1 = buf0 + C::kBufBytes;
     if constexpr (!C::kQ4K) {
-        // grid magnitudes (kernels/iq2_xxs-q8_K-RVV-common/ggml_min.h:69-134):
-        // two bits per byte select 8, 25 or 43
+        // grid codes (kernels/iq2_xxs-q8_K-RVV-common/ggml_min.h:69-134): per
+        // value one byte 0, 1 or 2 for the magnitude 8, 25 or 43
         for (int e = threadIdx.x; e < 256; e += C::kAllThreads) {
             const uint32_t code = kIq2GridCodes[e];
             uint32_t v[2] = {0, 0};
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint32_t c2 = (code >> (2 * j)) & 3u;
-                const uint32_t mag = c2 == 0 ? 8u : (c2 == 1 ? 25u : 43u);
-                v[j / 4] |= mag << (8 * (j % 4));
-            }
-            *reinterpret_cast<uint2 *>(grid + 8 * e) = make_uint2(v[0], v[1]);
+            for (int j = 0; j < 8; ++j) v[j / 4] |= ((code >> (2 * j)) & 3u) << (8 * (j % 4));
+            *reinterpret_cast<uint2 *>(lds + C::kGrid + 8 * e) = make_uint2(v[0], v[1]);
         }
-        // sign masks (the reference's ksigns_iq2xs, ggml_min.h:58-67: byte
-        // idx | parity(idx) << 7), one mask byte per element
+        // signs (the reference's ksigns_iq2xs, ggml_min.h:58-67: byte
+        // idx | parity(idx) << 7): 4 in the byte of each negative value
         for (int e = threadIdx.x; e < 128; e += C::kAllThreads) {
             const uint32_t sgn = (uint32_t)e | ((__builtin_popcount((uint32_t)e) & 1u) << 7);
             uint32_t v[2] = {0, 0};
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if ((sgn >> j) & 1u) v[j / 4] |= 0xffu << (8 * (j % 4));
-            *reinterpret_cast<uint2 *>(grid + 256 * 8 + 8 * e) = make_uint2(v[0], v[1]);
+            for (int j = 0; j < 8; ++j) v[j / 4] |= ((sgn >> j) & 1u) << (8 * (j % 4) + 2);
+            *reinterpret_cast<uint2 *>(lds + C::kSigns + 8 * e) = make_uint2(v[0], v[1]);
+        }
+        // per 4-bit scale s: w' = +-mag * (2 s + 1) = 128 hi + lo, byte c of
+        // the positive and byte c of the negative words for code c
+        for (int e = threadIdx.x; e < 16; e += C::kAllThreads) {
+            const int sc = 2 * e + 1;
+            uint32_t lp = 0, ln = 0, hp = 0, hn = 0;
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                const int p = (c == 0 ? 8 : (c == 1 ? 25 : 43)) * sc, q = -p;
+                lp |= (uint32_t)(p & 127) << (8 * c);
+                hp |= (uint32_t)((p >> 7) & 0xff) << (8 * c);
+                ln |= (uint32_t)(q & 127) << (8 * c);
+                hn |= (uint32_t)((q >> 7) & 0xff) << (8 * c);
+            }
+            *reinterpret_cast<uint4 *>(lds + C::kScaleTab + 16 * e) = make_uint4(lp, ln, hp, hn);
         }
         __syncthreads();
     }
