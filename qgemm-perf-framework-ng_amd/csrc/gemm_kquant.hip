@@ -108,9 +108,11 @@ struct KqRegs {
     uint32_t ab[C::kActPT][C::kBsDw];  // 8 / kActE bsums (q4_K)
     float ad[C::kActPT];
     // q4_K: 16 nibble bytes + the 16-byte header (d, dmin, scales)
-    // iq2_xxs: the 8 bytes of one sub-block + d
+    // iq2_xxs: the two dwords covering the sub-block's 8 bytes as loaded, d,
+    // the trailing half-word and whether the bytes start 2 past a dword (the
+    // realignment waits for the store, so the loads are not waited on early)
     uint32_t wq[C::kWPT][C::kQ4K ? 4 : 2];
-    uint32_t wh[C::kWPT][C::kQ4K ? 4 : 1];
+    uint32_t wh[C::kWPT][C::kQ4K ? 4 : 3];
 };
 
 constexpr int kQ8KBytes = 292, kQ4KBytes = 144, kIq2Bytes = 66;
@@ -187,13 +189,13 @@ __device__ __forceinline__ void kq_load(const uint8_t *__restrict__ a_t, const u
             // 66-byte blocks are only 2-byte aligned: read the covering dwords
             // and a trailing half-word, never past the sub-block's last byte
             const uint8_t *sb = w_st + o.w[it] + 32 * H;  // sub-block e of half H
-            const bool sh = (reinterpret_cast<uintptr_t>(sb) & 3) != 0;
-            const uint32_t *p4 = reinterpret_cast<const uint32_t *>(sb - (sh ? 2 : 0));
-            const uint32_t d0 = p4[0], d1 = p4[1];
-            const uint32_t tail = *reinterpret_cast<const uint16_t *>(sb + 6);
-            r.wq[it][0] = sh ? __builtin_amdgcn_alignbyte(d1, d0, 2) : d0;
-            r.wq[it][1] = sh ? ((d1 >> 16) | (tail << 16)) : d1;
+            const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(sb) & 3);  // 0 or 2
+            const uint32_t *p4 = reinterpret_cast<const uint32_t *>(sb - sh);
+            r.wq[it][0] = p4[0];
+            r.wq[it][1] = p4[1];
             r.wh[it][0] = *reinterpret_cast<const uint16_t *>(sb - 32 * H - 2 - 8 * e);
+            r.wh[it][1] = *reinterpret_cast<const uint16_t *>(sb + 6);
+            r.wh[it][2] = sh;
         }
     }
 }
@@ -272,7 +274,10 @@ __device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int 
             // it picks the lo and hi bytes of w' = +-mag * (2 * (bits 28..31) + 1)
             // from the scale's table (x: lo of the positive products, y: lo of
             // the negative ones, z / w: the hi bytes)
-            const uint32_t gidx = r.wq[it][0], ss = r.wq[it][1];
+            const uint32_t d0 = r.wq[it][0], d1 = r.wq[it][1];
+            const bool sh = r.wh[it][2] != 0;
+            const uint32_t gidx = sh ? __builtin_amdgcn_alignbyte(d1, d0, 2) : d0;
+            const uint32_t ss = sh ? ((d1 >> 16) | (r.wh[it][1] << 16)) : d1;
             const uint4 tab = *reinterpret_cast<const uint4 *>(scale_tab + 16 * (ss >> 28));
             uint32_t lo[8], hi[8];
 #pragma unroll
@@ -525,8 +530,12 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
     // other buffer and the loads of the stage after it are issued. Stores and
     // loads are unconditional (the super-block index is clamped at the end);
     // every slice runs the same number of iterations, and one whose
-    // super-block is past the end skips only the arithmetic. (Loads issued two
-    // stages ahead, from a register set per half, measured no faster on c2/c3.)
+    // super-block is past the end skips only the arithmetic. That check is
+    // only compiled into the one iteration that can need it: a branch around
+    // the arithmetic in every iteration made the compiler copy the just-loaded
+    // registers before the barrier and so wait for the loads there. (Loads
+    // issued two stages ahead, from a register set per half, measured no
+    // faster on c2/c3.)
     KqRegs<C> regs;
     const int last = nb - 1;
     const uint8_t *a_t = a + (size_t)m0 * nb * kQ8KBytes;
@@ -536,10 +545,9 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
     kq_store<C>(buf0, grid, 0, tid, regs);
     kq_load<C, 1>(a_t, w_t, slice < nb ? slice : last, offs, tid, regs);
     __syncthreads();
-    const int iters = (nb + C::kWS - 1) / C::kWS;
-    for (int it = 0; it < iters; ++it) {
+    auto step = [&](int it, bool guard) __attribute__((always_inline)) {
         const int b = it * C::kWS + slice;
-        const bool mine = C::kWS == 1 || b < nb;  // uniform across the slice's waves
+        const bool mine = !guard || b < nb;  // uniform across the slice's waves
         const int bn = b + C::kWS < nb ? b + C::kWS : last;
         __builtin_amdgcn_sched_barrier(0);
         if (mine) kq_compute<C, 0>(buf0, A, tb, lane, wave_m, wave_n);
@@ -559,7 +567,10 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
         kq_load<C, 1>(a_t, w_t, bn, offs, tid, regs);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
-    }
+    };
+    const int full = nb / C::kWS;  // iterations in which every slice has a super-block
+    for (int it = 0; it < full; ++it) step(it, false);
+    if (full * C::kWS < nb) step(full, true);
 
     if constexpr (!kIsums) {
         constexpr int kGroups = C::kWK * C::kWS;  // partial accumulators per output tile
