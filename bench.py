@@ -382,14 +382,16 @@ def main():
             gemv_kq.append(measure(torch, pkg, f"m1_{name}: {name} x q8_K GEMV M=1 N=4096 K=4096, 32 rotating "
                                    "weight copies", qt, 1, 4096, 4096, side, max(side // 10, 32), samples, variant,
                                    f"gemv_{name}_kernel<1>", copies=32))
-        for qt, name, variant, kern in ((0, "q4_0", ref, "gemv_q4_0_mfma8_kernel"),
-                                        (1, "q4_K", ref, "gemv_q4_K_mfma_sb_kernel"),
-                                        (2, "iq2_xxs", base, "gemv_iq2_xxs_mfma_sb_kernel")):
+        # at K = 4096 M = 8 and 16 run the 16x16 MFMA tile GEMVs: one chunk of 16
+        # activation rows of the chunked kernels (q4_0 from M = 6, q4_K from M = 5,
+        # iq2_xxs from M = 9), iq2_xxs at M = 5..8 the two-half-copy kernel
+        kernels = {0: {8: "gemv_q4_0_mfma_chunk_kernel<1>", 16: "gemv_q4_0_mfma_chunk_kernel<1>"},
+                   1: {8: "gemv_q4_K_mfma_chunk_kernel<1>", 16: "gemv_q4_K_mfma_chunk_kernel<1>"},
+                   2: {8: "gemv_iq2_xxs_mfma_sb_kernel<8>", 16: "gemv_iq2_xxs_mfma_chunk_kernel<1>"}}
+        for qt, name, variant in ((0, "q4_0", ref), (1, "q4_K", ref), (2, "iq2_xxs", base)):
             act_t = "q8_0" if qt == 0 else "q8_K"
             for dm in (8, 16):
-                # at K = 4096 M = 8 and 16 both run the MFMA tile GEMVs (q4_0 from M = 7,
-                # q4_K and iq2_xxs from M = 5)
-                kname = f"{kern}<{dm}>"
+                kname = kernels[qt][dm]
                 decode.append(measure(torch, pkg, f"m{dm}_{name}: {name} x {act_t} GEMV M={dm} N=4096 K=4096, "
                                       "32 rotating weight copies", qt, dm, 4096, 4096, side, max(side // 10, 32),
                                       samples, variant, kname, copies=32))

@@ -1,5 +1,6 @@
-// q4_0 x q8_0 GEMV path (m <= 16) for gfx950: the weight stream is the
-// roofline. Six kernels, picked in launch_gemv / launch_fused_gemv:
+// q4_0 x q8_0 GEMV path (m <= 16, and up to 128 at k = 4096) for gfx950: the
+// weight stream is the roofline. Six kernels, picked in launch_gemv /
+// launch_fused_gemv:
 //
 //   gemv_q4_0_m1_kernel        m == 1: one wavefront per weight row, one q4_0
 //                              block pair (36 B) per lane, the activation row
@@ -15,14 +16,15 @@
 //                              bytes, then the 8 fp16 scales).
 //   gemv_q4_0_fused_kernel     pfng_hip_compute for m <= 2: quantizes the fp32
 //                              activation rows into LDS, then as the m1 kernel.
-//   gemv_q4_0_mfma_kernel      m = 9..16 (k % 4096 == 0; from m = 12 also
-//                              k % 2048 == 0): 16x16 int8 MFMA tiles of 16
-//                              weight rows, K split over the workgroup's waves,
-//                              each wave's slices copied into LDS by direct loads.
-//   gemv_q4_0_mfma8_kernel     the same at k = 4096 (8 blocks per wave) from
-//                              m = 7: the slice copied in two halves, half 0
-//                              multiplied while half 1 lands, scales on the
-//                              matrix core.
+//   gemv_q4_0_mfma_kernel      m = 9..16 at k % 4096 == 0 above 4096 (from
+//                              m = 12 also k % 2048 == 0): 16x16 int8 MFMA
+//                              tiles of 16 weight rows, K split over the
+//                              workgroup's waves, each wave's slices copied
+//                              into LDS by direct loads.
+//   gemv_q4_0_mfma_chunk_kernel k = 4096 from m = 6 up to m = 128: the same
+//                              tile with 8 blocks per wave, the weights widened
+//                              into registers once and the activation rows
+//                              streamed through LDS in chunks of 16.
 //
 // Every lane issues all the loads of a step before any arithmetic, so the
 // weight stream of the grid is in flight at once; weight rows are clamped so
@@ -592,140 +594,12 @@ __global__ __launch_bounds__(WV * 64) void gemv_q4_0_mfma_kernel(const uint8_t *
     }
 }
 
-// The same tile GEMV for the common slice of 8 blocks per wave (k = 4096 with
-// 16 waves), in two halves of 4 blocks: each half of the wave's slice (weight
-// bytes [0, 72) / [72, 144) of its 16 rows, activation bytes [0, 136) /
-// [136, 272) of its m rows, widened to whole 16-byte chunks: 5 per weight
-// row, 9 per activation row) has its own LDS region, and the wave multiplies
-// half 0 as soon as its copies have landed while half 1 is still in flight
-// (s_waitcnt vmcnt(N): loads complete in issue order, and N is the number of
-// copy instructions after the last one half 0 needs). The two regions are one
-// run of H = 80 + 9m chunks each, copied by consecutive instructions with all
-// 64 lanes active: a lane past the end of half 0 fetches the half-1 chunk its
-// LDS position belongs to (the same bytes the next instruction writes there),
-// and the lanes past half 1 fill a pad. Lane-predicated copies let the
-// compiler merge two copy sites into one whose LDS address (M0) it took from
-// the first active lane, which misplaced the other path's chunks.
-// Per block the scale product dw * da comes from the matrix core (one-hot
-// v_mfma_f32_16x16x16_f16: lanes of K group 0 supply da of their row and dw of
-// their column, the others zero), then acc += float(16 S_b) * P per result.
-constexpr int kMf8Blocks = 8;           // blocks per wave
-constexpr int kMf8ChunksW = 5;          // 16-byte chunks per weight row and half (72 B used)
-constexpr int kMf8ChunksA = 9;          // per activation row and half (136 B used)
+// k = 4096 (16 waves of 8 blocks) from m = 6: 16-row int8 MFMA tiles over C =
+// ceil(m / 16) chunks of 16 activation rows (m up to 16 * kMaxGemvChunks).
+constexpr int kMf8Blocks = 8;  // blocks per wave
 constexpr int kMf8Waves = 16;
 
-__host__ __device__ constexpr int mf8_half_chunks(int m) { return 16 * kMf8ChunksW + m * kMf8ChunksA; }
-__host__ __device__ constexpr int mf8_copies(int m) { return (2 * mf8_half_chunks(m) + 63) / 64; }
-__host__ __device__ constexpr int mf8_wave_bytes(int m) { return mf8_copies(m) * 64 * 16; }
-
-// Global byte offset, from the wave's first block of row 0, of the chunk at
-// LDS chunk position p of the wave's run (positions past both halves repeat
-// the last chunk).
-template <int M>
-__device__ __forceinline__ size_t mf8_chunk_source(int p, size_t wrow_bytes, size_t arow_bytes, int n0, int n) {
-    constexpr int kH = mf8_half_chunks(M);
-    if (p >= 2 * kH) p = 2 * kH - 1;
-    const int h = p >= kH ? 1 : 0;
-    int c = p - h * kH;
-    if (c < 16 * kMf8ChunksW) {
-        int row = c / kMf8ChunksW;
-        const int col = c - row * kMf8ChunksW;
-        if (n0 + row >= n) row = n - 1 - n0;  // partial tile: repeat the last weight row
-        return (size_t)row * wrow_bytes + 64 * h + 16 * col;
-    }
-    c -= 16 * kMf8ChunksW;
-    const int row = c / kMf8ChunksA, col = c - row * kMf8ChunksA;
-    return (size_t)(1) << 62 | ((size_t)row * arow_bytes + 128 * h + 16 * col);  // bit 62: activation
-}
-
-template <int M>
-__global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma8_kernel(const uint8_t *__restrict__ w,
-                                                                       const uint8_t *__restrict__ a,
-                                                                       float *__restrict__ c, int n, int nb) {
-    static_assert(M >= 1 && M <= 16, "one 16-row tile of activation rows");
-    constexpr int kH = mf8_half_chunks(M);
-    constexpr int kCopies = mf8_copies(M);
-    constexpr int kHalf0Copies = (kH + 63) / 64;        // instructions that write half 0
-    constexpr int kAfterHalf0 = kCopies - kHalf0Copies;  // issued after them
-    constexpr int kRegW = 16 * kMf8ChunksW * 16;         // bytes of one half's weight region
-    extern __shared__ __align__(16) uint8_t lds[];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int n0 = blockIdx.x * 16;
-    const int kb0 = wave * kMf8Blocks;
-    uint8_t *base = lds + wave * mf8_wave_bytes(M);
-    const uint8_t *wsrc = w + ((size_t)n0 * nb + kb0) * 18, *asrc = a + (size_t)kb0 * 34;
-#pragma unroll
-    for (int i = 0; i < kCopies; ++i) {
-        const size_t o = mf8_chunk_source<M>(64 * i + lane, (size_t)nb * 18, (size_t)nb * 34, n0, n);
-        const uint8_t *src = (o >> 62) ? asrc + (o & ~((size_t)1 << 62)) : wsrc + o;
-        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(base + i * 1024), 16, 0, 0);
-    }
-    const int li = lane & 15, q = lane >> 4;
-    const int arow = li < M ? li : M - 1;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    // block j (0..3) of half h: weight bytes at 18 j (+ 8 in half 1: its
-    // region starts at slice byte 64) of the row, activation bytes at 34 j
-    // (+ 8 in half 1: its region starts at slice byte 128)
-    auto half = [&](int h) {
-        const uint8_t *ws = base + h * kH * 16, *as = ws + kRegW;
-        const uint8_t *wr = ws + li * (kMf8ChunksW * 16) + 8 * h;
-        const uint8_t *ar = as + arow * (kMf8ChunksA * 16) + 8 * h;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            uint32_t wq, x0, x1;
-            if ((j & 1) == 0) {  // two bytes into its dwords
-                const uint32_t *w0 = reinterpret_cast<const uint32_t *>(wr + j * 18 + 4 * q);
-                const uint32_t *a0 = reinterpret_cast<const uint32_t *>(ar + j * 34 + 4 * q);
-                wq = shift2(w0[0], w0[1]);
-                x0 = shift2(a0[0], a0[1]);
-                x1 = shift2(a0[4], a0[5]);
-            } else {
-                wq = *reinterpret_cast<const uint32_t *>(wr + j * 18 + 2 + 4 * q);
-                const uint32_t *a1 = reinterpret_cast<const uint32_t *>(ar + j * 34 + 2 + 4 * q);
-                x0 = a1[0];
-                x1 = a1[4];
-            }
-            const uint64_t bop = (uint64_t)q4_0_lo16(wq) | ((uint64_t)q4_0_hi16(wq) << 32);
-            const uint64_t aop = (uint64_t)x0 | ((uint64_t)x1 << 32);
-            const i32x4 s16 = mfma_i8_16x16x32(aop, bop, (i32x4){0, 0, 0, 0});
-            const uint32_t dw = *reinterpret_cast<const uint16_t *>(wr + j * 18);
-            const uint32_t da = *reinterpret_cast<const uint16_t *>(ar + j * 34);
-            const f16x4 pa = __builtin_bit_cast(f16x4, make_uint2(q == 0 ? da : 0u, 0u));
-            const f16x4 pb = __builtin_bit_cast(f16x4, make_uint2(q == 0 ? dw : 0u, 0u));
-            const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, pb, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf((float)s16[r], p[r], acc[r]);
-        }
-    };
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfterHalf0) : "memory");  // half 0 has landed
-    half(0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    half(1);
-    // wave partials through LDS, added in wave order by wave 0
-    __syncthreads();
-    float *red = reinterpret_cast<float *>(lds);
-    if (wave > 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red[((wave - 1) * 4 + r) * 64 + lane] = acc[r];
-    }
-    __syncthreads();
-    if (wave == 0) {
-        for (int v = 1; v < kMf8Waves; ++v) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] += red[((v - 1) * 4 + r) * 64 + lane];
-        }
-        const int col = n0 + li;
-        if (col < n) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                if (4 * q + r < M) c[(size_t)(4 * q + r) * n + col] = acc[r] * 0.0625f;
-        }
-    }
-}
-
-// m = 17..64 at k = 4096: the tile of gemv_q4_0_mfma8_kernel over C chunks of
-// 16 activation rows. Each wave copies its 8-block slice of the 16 weight rows
+// Each wave copies its 8-block slice of the 16 weight rows
 // once (144 bytes a row) and widens it once into registers (the nibbles as
 // 16 (q - 8) int8 operands, the fp16 scales); chunk c's activation slice
 // (272 bytes a row) arrives in two halves, H0 = slice bytes 0..143 (blocks
@@ -733,14 +607,20 @@ __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma8_kernel(const u
 // refilled with chunk c + 1 as soon as the wave has read it (the copy of
 // H0(c + 1) runs while H1(c) is multiplied, H1(c + 1)'s while H0(c + 1) is).
 // Every wait is for the instructions that wrote one buffer (loads complete in
-// issue order). Activation rows past m repeat row m - 1 (not stored).
+// issue order). Activation rows past m repeat row m - 1 (not stored). Per
+// block the scale product dw * da comes from the matrix core (one-hot
+// v_mfma_f32_16x16x16_f16), then acc += float(16 S_b) * P per result.
+// Measured at 4096 x 4096 against the former kernel that copied each chunk's
+// weight and activation slice together in two halves (us): q4_0 m = 6 5.33 /
+// 5.15, m = 8 5.42 / 5.16, m = 16 5.83 / 5.28; below m = 6 the pairs kernel
+// is faster (m = 5 4.93 / 5.15).
 constexpr int kQ40ChunkWaveBytes = 9 * 1024;  // weight run, H0, H1: 3 KB each
 
 template <int C>
 __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(const uint8_t *__restrict__ w,
                                                                               const uint8_t *__restrict__ a,
                                                                               float *__restrict__ c, int m, int n) {
-    static_assert(C >= 2 && C <= kMaxGemvChunks, "17 or more activation rows, at most kMaxGemvChunks chunks");
+    static_assert(C >= 1 && C <= kMaxGemvChunks, "at most kMaxGemvChunks chunks of 16 activation rows");
     constexpr int nb = kMf8Waves * kMf8Blocks;  // k == 4096
     constexpr uint32_t kARow = nb * 34;
     constexpr int kH = run_copies<16, 9>();
@@ -955,9 +835,6 @@ hipError_t launch_fused_m(const void *w, const float *x, float *c, int64_t n, in
 // 7.14 / 7.86, m = 10 7.18 / 6.95). Both while the slices fit the LDS.
 int mf_gemv_waves(int64_t m, int64_t k) {
     if (m > 16 || mf_gemv_lds_bytes(m, k / 32) > kPairsMaxLds) return 0;
-    // k = 4096 (gemv_q4_0_mfma8_kernel): from m = 7, where it beats the pairs
-    // kernel (4096 x 4096, us: m = 6 5.41 / 5.38, m = 7 5.42 / 5.96, m = 8 5.44 / 5.99)
-    if (m >= 7 && k == 4096) return 16;
     if (m >= 9 && k % 4096 == 0) return 16;
     if (m >= 12 && k % 2048 == 0) return 8;
     return 0;
@@ -966,14 +843,14 @@ int mf_gemv_waves(int64_t m, int64_t k) {
 template <int M>
 hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n, int64_t k, hipStream_t stream) {
     const int nb = (int)(k / 32);
+    if (M >= 6 && k == 4096) {  // gemv_q4_0_mfma_chunk_kernel, one chunk
+        hipLaunchKernelGGL(gemv_q4_0_mfma_chunk_kernel<1>, dim3((unsigned)((n + 15) / 16)), dim3(kMf8Waves * 64),
+                           (size_t)kMf8Waves * kQ40ChunkWaveBytes, stream, static_cast<const uint8_t *>(w),
+                           static_cast<const uint8_t *>(a), c, M, (int)n);
+        return hipGetLastError();
+    }
     if (const int wv = mf_gemv_waves(M, k)) {
         const int bw = nb / wv;  // blocks per wave, a multiple of 8
-        if (wv == kMf8Waves && bw == kMf8Blocks) {
-            hipLaunchKernelGGL(gemv_q4_0_mfma8_kernel<M>, dim3((unsigned)((n + 15) / 16)), dim3(kMf8Waves * 64),
-                               (size_t)kMf8Waves * mf8_wave_bytes(M), stream, static_cast<const uint8_t *>(w),
-                               static_cast<const uint8_t *>(a), c, (int)n, nb);
-            return hipGetLastError();
-        }
         MfGemvGeom geo;
         geo.cprw = bw * 18 / 16;
         geo.cpra = bw * 34 / 16;

@@ -1,4 +1,5 @@
-// GEMV path (m <= 16) for the super-block formats against q8_K activations:
+// GEMV path (m <= 16, and up to 128 at k == 4096) for the super-block formats
+// against q8_K activations:
 // q4_K (llama_reference.cpp:113-132) and iq2_xxs (llama_reference.cpp:148-161,
 // kernels/common/iq2_xxs.h:29-41). One wavefront per weight row, the weight
 // stream read with aligned 16-byte (q4_K) or realigned dword (iq2_xxs,
@@ -7,10 +8,13 @@
 // (m <= 8) take m == 1 and rows too long to stage; for q4_K at m == 1 the
 // 16-row workgroups copy the activation row into LDS first. The
 // *_staged_kernel variants (m = 2..16) stage the rows in LDS once per 16-row
-// workgroup. From m = 5 at k == 4096 both formats run 16x16 int8 MFMA tiles
-// of 16 weight rows with one super-block per wave (gemv_q4_K_mfma_sb_kernel,
-// gemv_iq2_xxs_mfma_sb_kernel); q4_K at larger k % 4096 == 0 runs
-// gemv_q4_K_mfma_kernel, whose waves take k / 4096 super-blocks each.
+// workgroup. At k == 4096 both formats run 16x16 int8 MFMA tiles of 16 weight
+// rows with one super-block per wave: iq2_xxs at m = 5..8 with the weight and
+// activation bytes copied together in two halves (gemv_iq2_xxs_mfma_sb_kernel),
+// and from m = 5 (q4_K) or 9 (iq2_xxs) with the weights decoded once per wave
+// and the activation rows streamed in chunks of 16 (*_mfma_chunk_kernel); q4_K
+// at larger k % 4096 == 0 runs gemv_q4_K_mfma_kernel, whose waves take
+// k / 4096 super-blocks each.
 //
 // q4_K: four lanes per super-block, lane e owning sub-blocks 2e and 2e+1 (the
 // 32 nibble bytes qs[32e .. 32e+32): low nibbles of sub-block 2e, high of
@@ -935,8 +939,8 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_kernel(const u
     }
 }
 
-// Two-half copies for the GEMVs with one super-block per wave (k == 4096,
-// m = 5..16). A wave copies its super-block of the tile's 16 weight rows and
+// Two-half copies for the iq2_xxs GEMV with one super-block per wave
+// (k == 4096, m = 5..8). A wave copies its super-block of the tile's 16 weight rows and
 // of the m activation rows in 16-byte chunks, each row from the 16-byte
 // boundary at or before its block (rows are 16 blocks long, so that offset
 // depends on the wave only). Half h holds, for each weight row, chunks
@@ -952,10 +956,6 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_kernel(const u
 // LDS address comes from a single lane). Loads complete in issue order, so a
 // wave multiplies half 0 after waiting for the instructions that wrote it,
 // while half 1 is still in flight.
-struct Q4KRun {  // 144-byte weight blocks (16-byte aligned), 292-byte q8_K blocks
-    static constexpr int wn0 = 5, wc1 = 4, wn1 = 5, an0 = 9, ac1 = 8, an1 = 11;
-    static constexpr uint32_t wrow = 16 * 144, arow = 16 * kQ8KBytes;
-};
 struct Iq2Run {  // 66-byte weight blocks; no bsums needed
     static constexpr int wn0 = 3, wc1 = 2, wn1 = 3, an0 = 9, ac1 = 8, an1 = 9;
     static constexpr uint32_t wrow = 16 * kIq2Bytes, arow = 16 * kQ8KBytes;
@@ -1001,118 +1001,7 @@ __device__ __forceinline__ void sb_copy(const uint8_t *wsrc, const uint8_t *asrc
     }
 }
 
-// q4_K: the tile of gemv_q4_K_mfma_kernel with one super-block per wave and
-// two-half copies. The weight blocks are 16-byte aligned; the q8_K block of
-// wave v starts o = 4 (v % 4) bytes past a 16-byte boundary and is copied as
-// 19 chunks from there. Half 0: chunks 0..4 of every weight row (header and
-// the nibbles of sub-blocks 0..3) and 0..8 of every activation row (d and the
-// bytes of sub-blocks 0..3); half 1: weight chunks 4..8 (the nibbles of
-// sub-blocks 4..7) and activation chunks 8..18 (bytes 132..291, bsums
-// included, lie at or past copy byte 128). The min term
-// sum_j m_j * bsum_j is one v_mfma_f32_16x16x16_f16 per super-block: the bsums
-// (|bsum| <= 16 * 127 < 2048) and the 6-bit mins are exact in fp16 and the
-// sums of products exact in fp32, so IM equals the integer sum.
-__host__ __device__ constexpr int q4k_sb_lds_bytes(int m) { return kKqMfWaves * sb_copies<Q4KRun>(m) * 1024; }
-
-template <int M>
-__global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_sb_kernel(const uint8_t *__restrict__ w,
-                                                                            const uint8_t *__restrict__ a,
-                                                                            float *__restrict__ c, int n) {
-    static_assert(M >= 1 && M <= 16, "one 16-row tile of activation rows");
-    constexpr int nsb = kKqMfWaves;  // k == 4096
-    using R = Q4KRun;
-    constexpr int kH0 = sb_half0<R>(M);
-    constexpr int kCopies = sb_copies<R>(M);
-    constexpr int kAfterHalf0 = kCopies - (kH0 + 63) / 64;  // instructions issued after those writing half 0
-    extern __shared__ __align__(16) uint8_t lds[];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int n0 = blockIdx.x * 16;
-    const int o = 4 * (wave & 3);
-    uint8_t *base = lds + wave * kCopies * 1024;
-    sb_copy<R, M>(w + ((size_t)n0 * nsb + wave) * 144, a + wave * kQ8KBytes - o, base, lane, n - n0);
-    const uint8_t *w0 = base, *a0 = w0 + 16 * R::wn0 * 16;  // half 0: weight rows of 80 B, activation rows of 144 B
-    const uint8_t *w1 = base + kH0 * 16, *a1 = w1 + 16 * R::wn1 * 16;  // half 1: 80 B, 176 B
-    const int li = lane & 15, q = lane >> 4;
-    const int arow = li < M ? li : M - 1;
-    int orow[4];  // activation rows of this lane's four results (clamped)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) orow[r] = 4 * q + r < M ? 4 * q + r : M - 1;
-    // activation byte b of row r: half 0 at a0 + 144 r + o + b (b < 144 - o), half 1 at a1 + 176 r + o + b - 128 (b >= 128 - o)
-    const uint8_t *ar0 = a0 + arow * (R::an0 * 16) + o, *ar1 = a1 + arow * (R::an1 * 16) + o - R::ac1 * 16;
-    int is[4] = {0, 0, 0, 0};
-    uint32_t scw[2], mnw[2];
-    auto sub = [&](int j, uint32_t x0, uint32_t x1, uint32_t y0, uint32_t y1) {
-        const uint32_t v0 = (j & 1 ? x0 >> 4 : x0) & 0x0f0f0f0fu;
-        const uint32_t v1 = (j & 1 ? x1 >> 4 : x1) & 0x0f0f0f0fu;
-        const i32x4 sj = mfma_i8_16x16x32((uint64_t)y0 | ((uint64_t)y1 << 32), (uint64_t)v0 | ((uint64_t)v1 << 32),
-                                          (i32x4){0, 0, 0, 0});
-        const int sc = (int)((scw[j / 4] >> (8 * (j % 4))) & 0xffu);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) is[r] += __mul24(sc, sj[r]);
-    };
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfterHalf0) : "memory");  // half 0 has landed
-    // the header as four dwords: a typed read, so the compiler adds no wait for all copies before it
-    const uint32_t *hp = reinterpret_cast<const uint32_t *>(w0 + li * (R::wn0 * 16));
-    const uint4 hd = make_uint4(hp[0], hp[1], hp[2], hp[3]);
-    // scales (bytes 0..3: sub-blocks 0..3, 4..7: 4..7) and mins, as q4_K_scale_min_pair
-    scw[0] = hd.y & 0x3f3f3f3fu;
-    scw[1] = (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u);
-    mnw[0] = hd.z & 0x3f3f3f3fu;
-    mnw[1] = ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u);
-    float ad[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) ad[r] = *reinterpret_cast<const float *>(a0 + orow[r] * (R::an0 * 16) + o);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {  // weight nibbles at block byte 16 + 32 (j / 2) + 4q (+ 16)
-        const uint8_t *wq = w0 + li * (R::wn0 * 16) + 16 + 32 * (j / 2) + 4 * q;
-        const uint8_t *aq = ar0 + 4 + 32 * j + 4 * q;
-        sub(j, *reinterpret_cast<const uint32_t *>(wq), *reinterpret_cast<const uint32_t *>(wq + 16),
-            *reinterpret_cast<const uint32_t *>(aq), *reinterpret_cast<const uint32_t *>(aq + 16));
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-    for (int j = 4; j < 8; ++j) {  // weight nibbles at block byte 16 + 32 (j / 2) + 4q (+ 16), half-1 rows from byte 64
-        const uint8_t *wq = w1 + li * (R::wn1 * 16) + 16 + 32 * (j / 2) + 4 * q - 16 * R::wc1;
-        const uint8_t *aq = ar1 + 4 + 32 * j + 4 * q;
-        sub(j, *reinterpret_cast<const uint32_t *>(wq), *reinterpret_cast<const uint32_t *>(wq + 16),
-            *reinterpret_cast<const uint32_t *>(aq), *reinterpret_cast<const uint32_t *>(aq + 16));
-    }
-    // IM: A = bsums 4q..4q+3 of activation row arow, B = m_(2q), m_(2q), m_(2q+1), m_(2q+1) of weight row li
-    const uint32_t *bsp = reinterpret_cast<const uint32_t *>(ar1 + 260 + 8 * q);
-    const uint32_t b01 = bsp[0], b23 = bsp[1];
-    const f16x4 bs = {(_Float16)(short)(b01 & 0xffffu), (_Float16)(short)(b01 >> 16), (_Float16)(short)(b23 & 0xffffu),
-                      (_Float16)(short)(b23 >> 16)};
-    const uint32_t mp = (q & 2 ? mnw[1] : mnw[0]) >> (16 * (q & 1));
-    const _Float16 m0 = (_Float16)(int)(mp & 0xffu), m1 = (_Float16)(int)((mp >> 8) & 0xffu);
-    const f16x4 mm = {m0, m0, m1, m1};
-    const f32x4 im = __builtin_amdgcn_mfma_f32_16x16x16f16(bs, mm, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-    const float d = fp16_to_f32(hd.x & 0xffffu), dmin = fp16_to_f32(hd.x >> 16);
-    float acc[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] = ad[r] * fmaf(-dmin, im[r], d * (float)is[r]);
-    __syncthreads();
-    float *red = reinterpret_cast<float *>(lds);
-    if (wave > 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red[((wave - 1) * 4 + r) * 64 + lane] = acc[r];
-    }
-    __syncthreads();
-    if (wave == 0) {
-        for (int v = 1; v < kKqMfWaves; ++v) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] += red[((v - 1) * 4 + r) * 64 + lane];
-        }
-        const int col = n0 + li;
-        if (col < n) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                if (4 * q + r < M) c[(size_t)(4 * q + r) * n + col] = acc[r];
-        }
-    }
-}
-
-// iq2_xxs, m = 5..16 at k == 4096: 16x16 int8 MFMA tiles of 16 weight rows,
+// iq2_xxs, m = 5..8 at k == 4096: 16x16 int8 MFMA tiles of 16 weight rows,
 // one super-block per wave, two-half copies. Per sub-block j, lane (row
 // l % 16, q = l / 16) holds K positions 8q..8q+7, i.e. grid group q: one grid
 // entry and one sign mask gathered from LDS (each a typed 8-byte read), the
@@ -1227,10 +1116,11 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_sb_kernel(c
     }
 }
 
-// m = 17..64 at k == 4096: the one-super-block-per-wave tiles above, with the
-// activation rows taken in C chunks of 16. Each wave copies its super-block of
-// the tile's 16 weight rows once, decodes them once into registers, and then
-// streams the chunks: chunk c's activation blocks arrive in two halves (H0:
+// k == 4096 from m = 5 (q4_K) or m = 9 (iq2_xxs) up to m = 16 * kMaxGemvChunks:
+// 16x16 int8 MFMA tiles of 16 weight rows with one super-block per wave, the
+// activation rows taken in C = ceil(m / 16) chunks of 16. Each wave copies its
+// super-block of the tile's 16 weight rows once, decodes them once into
+// registers, and then streams the chunks: chunk c's activation blocks arrive in two halves (H0:
 // copy chunks 0..8 of each row, d and sub-blocks 0..3; H1: chunks 8..18 or
 // 8..16, sub-blocks 4..7 and the bsums), each half into its own LDS buffer,
 // which is refilled with chunk c + 1 as soon as the wave has read it: the
@@ -1238,7 +1128,14 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_sb_kernel(c
 // while H0(c + 1) is. Every wait is for the instructions that wrote one
 // buffer (loads complete in issue order). Activation rows past m repeat row
 // m - 1 (their results are not stored). The copies are run_copy runs
-// (device_common.h).
+// (device_common.h). q4_K's min term sum_j m_j * bsum_j is one
+// v_mfma_f32_16x16x16_f16 per chunk: the bsums (|bsum| <= 16 * 127 < 2048)
+// and the 6-bit mins are exact in fp16 and the sums of products exact in
+// fp32, so IM equals the integer sum. Measured at 4096 x 4096 against the
+// former one-chunk-per-launch kernels that copied each super-block's weight and
+// activation bytes together in two halves (us): q4_K m = 5 5.01 / 4.66, m = 8
+// 5.20 / 4.66, m = 16 5.71 / 4.88 (m = 4 4.55 against 4.66 for the staged
+// kernel); iq2_xxs m = 8 5.53 / 5.61, m = 9 5.85 / 5.78, m = 16 6.27 / 5.98.
 constexpr int kChunkWaveBytes = 9 * 1024;  // per wave: weight run, H0, H1 (3 KB each)
 
 __host__ __device__ constexpr int q4k_chunk_lds_bytes() { return kKqMfWaves * kChunkWaveBytes; }
@@ -1247,7 +1144,7 @@ template <int C>
 __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(const uint8_t *__restrict__ w,
                                                                              const uint8_t *__restrict__ a,
                                                                              float *__restrict__ c, int m, int n) {
-    static_assert(C >= 2 && C <= kMaxGemvChunks, "17 or more activation rows, at most kMaxGemvChunks chunks");
+    static_assert(C >= 1 && C <= kMaxGemvChunks, "at most kMaxGemvChunks chunks of 16 activation rows");
     constexpr int nsb = kKqMfWaves;  // k == 4096
     constexpr uint32_t kARow = nsb * kQ8KBytes;
     constexpr int kH = run_copies<16, 11>();  // instructions per half (H1: 11 columns, H0: 9)
@@ -1345,7 +1242,7 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
     }
 }
 
-// iq2_xxs, m = 17..64 at k == 4096: as gemv_q4_K_mfma_chunk_kernel, with the
+// iq2_xxs, m = 9..128 at k == 4096: as gemv_q4_K_mfma_chunk_kernel, with the
 // weight decode of gemv_iq2_xxs_mfma_sb_kernel done once per wave (5 weight
 // columns per row, H1 = activation chunks 8..16) and the grid and sign tables
 // copied by waves 0..2 before everything else.
@@ -1357,7 +1254,7 @@ template <int C>
 __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kernel(const uint8_t *__restrict__ w,
                                                                                 const uint8_t *__restrict__ a,
                                                                                 float *__restrict__ c, int m, int n) {
-    static_assert(C >= 2 && C <= kMaxGemvChunks, "17 or more activation rows, at most kMaxGemvChunks chunks");
+    static_assert(C >= 1 && C <= kMaxGemvChunks, "at most kMaxGemvChunks chunks of 16 activation rows");
     constexpr int nsb = kKqMfWaves;  // k == 4096
     constexpr uint32_t kARow = nsb * kQ8KBytes;
     constexpr int kH = run_copies<16, 9>();
@@ -1471,16 +1368,23 @@ hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int6
     const int64_t nsb = k / 256;
     if constexpr (M >= 5) {
         // k == 4096: one super-block per wave, from m = 5 (4096 x 4096 against the
-        // staged kernel, us: q4_K m = 4 5.01 / 4.56, m = 5 5.00 / 5.12, m = 8 5.19 /
-        // 6.21; iq2_xxs m = 4 5.23 / 5.08, m = 5 5.34 / 5.91, m = 8 5.56 / 6.58)
+        // staged kernel, us: iq2_xxs m = 4 5.23 / 5.08, m = 5 5.34 / 5.91, m = 8
+        // 5.56 / 6.58); one chunk of the chunked kernel for q4_K and, from m = 9,
+        // for iq2_xxs
+        const dim3 tiles((unsigned)((n + 15) / 16)), block(kKqMfWaves * 64);
+        if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && k == 4096 && M >= 9) {
+            hipLaunchKernelGGL(gemv_iq2_xxs_mfma_chunk_kernel<1>, tiles, block, (size_t)iq2_chunk_lds_bytes(), stream,
+                               wp, ap, c, M, (int)n);
+            return hipGetLastError();
+        }
         if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && k == 4096) {
-            hipLaunchKernelGGL(gemv_iq2_xxs_mfma_sb_kernel<M>, dim3((unsigned)((n + 15) / 16)), dim3(kKqMfWaves * 64),
-                               (size_t)iq2_sb_lds_bytes(M), stream, wp, ap, c, (int)n);
+            hipLaunchKernelGGL(gemv_iq2_xxs_mfma_sb_kernel<M>, tiles, block, (size_t)iq2_sb_lds_bytes(M), stream, wp,
+                               ap, c, (int)n);
             return hipGetLastError();
         }
         if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K && k == 4096) {
-            hipLaunchKernelGGL(gemv_q4_K_mfma_sb_kernel<M>, dim3((unsigned)((n + 15) / 16)), dim3(kKqMfWaves * 64),
-                               (size_t)q4k_sb_lds_bytes(M), stream, wp, ap, c, (int)n);
+            hipLaunchKernelGGL(gemv_q4_K_mfma_chunk_kernel<1>, tiles, block, (size_t)q4k_chunk_lds_bytes(), stream, wp,
+                               ap, c, M, (int)n);
             return hipGetLastError();
         }
     }

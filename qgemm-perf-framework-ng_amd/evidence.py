@@ -53,19 +53,19 @@ CONFIGS = {
            "gemm_kq_kernel", "mfma"),
     "c4": ("q4_0 x q8_0 GEMM M=2048 N=11008 K=4096", 0, 2048, 11008, 4096, 0, "gemm_q4_0_kernel", "mfma"),
     # decode batches (not baseline configurations): at K = 4096 M = 8 and 16 run the MFMA tile GEMVs
+    # (one chunk of the chunked kernels; iq2_xxs at M = 8 the two-half-copy kernel)
     "m8_q4_0": ("q4_0 x q8_0 GEMV M=8 N=4096 K=4096, 32 rotating weight copies", 0, 8, 4096, 4096, 0,
-                "gemv_q4_0_mfma8_kernel", "hbm"),
+                "gemv_q4_0_mfma_chunk_kernel", "hbm"),
     "m8_q4_K": ("q4_K x q8_K GEMV M=8 N=4096 K=4096, 32 rotating weight copies", 1, 8, 4096, 4096, 0,
-                "gemv_q4_K_mfma_sb_kernel", "hbm"),
+                "gemv_q4_K_mfma_chunk_kernel", "hbm"),
     "m8_iq2_xxs": ("iq2_xxs x q8_K GEMV M=8 N=4096 K=4096, 32 rotating weight copies", 2, 8, 4096, 4096, 1,
                    "gemv_iq2_xxs_mfma_sb_kernel", "hbm"),
-    # the MFMA tile GEMVs (M = 9..16)
     "m16_q4_0": ("q4_0 x q8_0 GEMV M=16 N=4096 K=4096, 32 rotating weight copies", 0, 16, 4096, 4096, 0,
-                 "gemv_q4_0_mfma8_kernel", "hbm"),
+                 "gemv_q4_0_mfma_chunk_kernel", "hbm"),
     "m16_q4_K": ("q4_K x q8_K GEMV M=16 N=4096 K=4096, 32 rotating weight copies", 1, 16, 4096, 4096, 0,
-                 "gemv_q4_K_mfma_sb_kernel", "hbm"),
+                 "gemv_q4_K_mfma_chunk_kernel", "hbm"),
     "m16_iq2_xxs": ("iq2_xxs x q8_K GEMV M=16 N=4096 K=4096, 32 rotating weight copies", 2, 16, 4096, 4096, 1,
-                    "gemv_iq2_xxs_mfma_sb_kernel", "hbm"),
+                    "gemv_iq2_xxs_mfma_chunk_kernel", "hbm"),
     # the M = 1 GEMVs of the other two formats (bench.py's gemv_q4_K / gemv_iq2_xxs lines)
     "m1_q4_K": ("q4_K x q8_K GEMV M=1 N=4096 K=4096, 32 rotating weight copies", 1, 1, 4096, 4096, 0,
                 "gemv_q4_K_kernel", "hbm"),
