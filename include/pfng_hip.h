@@ -57,13 +57,13 @@ typedef enum {
                             m = 9..16 while m * (k / 256) * 320 + 3072 <= 163840;
                             m = 17..128 with k == 4096.
                             Kernels: wavefront-per-row GEMVs for short batches;
-                            16x16 int8-MFMA tiles with K split over 16 waves at
-                            k == 4096 from m = 7 (q4_0) and m = 5 (q4_K,
-                            iq2_xxs), and at larger k % 4096 == 0 from m = 9
-                            (q4_0, q4_K; q4_0 also from m = 12 at
-                            k % 2048 == 0); from m = 17 (k == 4096) the same
-                            tiles over chunks of 16 activation rows, the
-                            weights decoded once per wave */
+                            16x16 int8-MFMA tiles with K split over 16 waves:
+                            at k == 4096 from m = 6 (q4_0), 5 (q4_K) and 9
+                            (iq2_xxs; m = 5..8 a tile with two-half copies),
+                            the weights decoded once per wave and the
+                            activation rows streamed in chunks of 16; at larger
+                            k % 4096 == 0 from m = 9 (q4_0, q4_K; q4_0 also
+                            from m = 12 at k % 2048 == 0) */
     PFNG_PATH_MFMA = 2,  /* int8-MFMA GEMM, LDS-staged tiles: q4_0 with k % 128 == 0,
                             q4_K and iq2_xxs for every k % 256 == 0 */
     PFNG_PATH_NAIVE = 3  /* one thread per output, the reference's exact fp32 order */
