@@ -1,4 +1,4 @@
-// q4_0 x q8_0 GEMV path (m <= 16, and up to 128 at k = 4096) for gfx950: the
+// q4_0 x q8_0 GEMV path (m <= 16, and up to 128 at k % 4096 == 0) for gfx950: the
 // weight stream is the roofline. Six kernels, picked in launch_gemv /
 // launch_fused_gemv:
 //
@@ -16,13 +16,14 @@
 //                              bytes, then the 8 fp16 scales).
 //   gemv_q4_0_fused_kernel     pfng_hip_compute for m <= 2: quantizes the fp32
 //                              activation rows into LDS, then as the m1 kernel.
-//   gemv_q4_0_mfma_kernel      m = 9..16 at k % 4096 == 0 above 4096 (from
-//                              m = 12 also k % 2048 == 0): 16x16 int8 MFMA
-//                              tiles of 16 weight rows, K split over the
-//                              workgroup's waves, each wave's slices copied
-//                              into LDS by direct loads.
-//   gemv_q4_0_mfma_chunk_kernel k = 4096 from m = 6 up to m = 128: the same
-//                              tile with 8 blocks per wave, the weights widened
+//   gemv_q4_0_mfma_kernel      m = 12..16 at k % 2048 == 0 (not a multiple
+//                              of 4096): 16x16 int8 MFMA tiles of 16 weight
+//                              rows, K split over the workgroup's 8 waves,
+//                              each wave's slices copied into LDS by direct
+//                              loads.
+//   gemv_q4_0_mfma_chunk_kernel k % 4096 == 0 from m = 6 up to m = 128: the
+//                              same tile with 8 blocks per wave and round
+//                              (k / 4096 rounds), each round's weights widened
 //                              into registers once and the activation rows
 //                              streamed through LDS in chunks of 16.
 //
@@ -480,8 +481,8 @@ __global__ __launch_bounds__(kPairsThreads) void gemv_q4_0_pairs_kernel(const ui
     }
 }
 
-// m = 9..16 with k % 4096 == 0 (16 waves), m = 12..16 with k % 2048 == 0 (8
-// waves): 16x16 int8 MFMA tiles. A workgroup takes 16 weight rows (output
+// m = 12..16 with k % 2048 == 0 (8 waves; k % 4096 == 0 runs the chunk kernel
+// below): 16x16 int8 MFMA tiles. A workgroup takes 16 weight rows (output
 // columns) and all m activation rows; its WV waves split K into equal slices
 // of a multiple of 8 blocks, and each wave copies just its own slice of the 16 weight
 // rows and of the m activation rows into its own LDS region with direct loads
@@ -594,7 +595,9 @@ __global__ __launch_bounds__(WV * 64) void gemv_q4_0_mfma_kernel(const uint8_t *
     }
 }
 
-// k = 4096 (16 waves of 8 blocks) from m = 6: 16-row int8 MFMA tiles over C =
+// k % 4096 == 0 (16 waves of 8 blocks per round; round r takes blocks
+// 8 (16 r + wave) .. + 8 of every row, the partial sums staying in registers
+// across the k / 4096 rounds) from m = 6: 16-row int8 MFMA tiles over C =
 // ceil(m / 16) chunks of 16 activation rows (m up to 16 * kMaxGemvChunks).
 constexpr int kMf8Blocks = 8;  // blocks per wave
 constexpr int kMf8Waves = 16;
@@ -619,10 +622,11 @@ constexpr int kQ40ChunkWaveBytes = 9 * 1024;  // weight run, H0, H1: 3 KB each
 template <int C>
 __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(const uint8_t *__restrict__ w,
                                                                               const uint8_t *__restrict__ a,
-                                                                              float *__restrict__ c, int m, int n) {
+                                                                              float *__restrict__ c, int m, int n,
+                                                                              int rounds) {
     static_assert(C >= 1 && C <= kMaxGemvChunks, "at most kMaxGemvChunks chunks of 16 activation rows");
-    constexpr int nb = kMf8Waves * kMf8Blocks;  // k == 4096
-    constexpr uint32_t kARow = nb * 34;
+    const int nb = kMf8Waves * kMf8Blocks * rounds;  // k == 4096 * rounds
+    const uint32_t kARow = (uint32_t)nb * 34;
     constexpr int kH = run_copies<16, 9>();
     static_assert(kH * 1024 <= 3072, "3 KB per run");
     static_assert(kMf8Waves * 4 * C * 64 * 4 <= kMf8Waves * kQ40ChunkWaveBytes, "wave partials fit the LDS");
@@ -631,78 +635,92 @@ __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(co
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int n0 = blockIdx.x * 16;
     uint8_t *wl = lds + wave * kQ40ChunkWaveBytes, *h0 = wl + 3072, *h1 = wl + 6144;
-    const uint8_t *asrc = a + wave * kMf8Blocks * 34;  // the wave's slice of activation row 0
-    auto copy_h0 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, lane); };
-    auto copy_h1 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 8, m - 16 * ch, h1, lane); };
-    run_copy<16, 9>(w + ((size_t)n0 * nb + wave * kMf8Blocks) * 18, nb * 18, 0, n - n0, wl, lane);
-    copy_h0(0);
-    copy_h1(0);
-    const int li = lane & 15, q = lane >> 4;
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // weights and H0(0)
-    // the weight slice, once: block j's 8 int8 operands of this lane and its scale
-    const uint8_t *wr = wl + li * 144;
-    uint64_t bop[kMf8Blocks];
-    uint32_t dw[kMf8Blocks];
-#pragma unroll
-    for (int j = 0; j < kMf8Blocks; ++j) {
-        uint32_t wq;
-        if ((j & 1) == 0) {  // two bytes into its dwords
-            const uint32_t *w0 = reinterpret_cast<const uint32_t *>(wr + j * 18 + 4 * q);
-            wq = shift2(w0[0], w0[1]);
-        } else {
-            wq = *reinterpret_cast<const uint32_t *>(wr + j * 18 + 2 + 4 * q);
-        }
-        bop[j] = (uint64_t)q4_0_lo16(wq) | ((uint64_t)q4_0_hi16(wq) << 32);
-        const uint32_t dw_all = *reinterpret_cast<const uint16_t *>(wr + j * 18);  // every lane reads: no branch
-        dw[j] = q == 0 ? dw_all : 0u;
-    }
     float acc[C][4];
 #pragma unroll
-    for (int ch = 0; ch < C; ++ch) {
+    for (int ch = 0; ch < C; ++ch)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[ch][r] = 0.0f;
-        // block j of the chunk row li: slice byte 34 j, in H0 (j < 4) or H1 (from slice byte 128)
-        auto block = [&](int j) {
-            const uint8_t *ar = (j < 4 ? h0 + li * 144 : h1 + li * 144 - 128) + j * 34;
-            uint32_t x0, x1;
-            if ((j & 1) == 0) {
-                const uint32_t *a0 = reinterpret_cast<const uint32_t *>(ar + 4 * q);
-                x0 = shift2(a0[0], a0[1]);
-                x1 = shift2(a0[4], a0[5]);
+    // round rnd takes the wave's K slice 16 rnd + wave of every row; the next
+    // round's copies start once the last round's buffers have been read
+    for (int rnd = 0; rnd < rounds; ++rnd) {
+        // a lane index the compiler cannot carry across rounds: the per-lane
+        // copy offsets and LDS addresses are recomputed per round instead of
+        // held in registers for the whole loop
+        int cl = lane;
+        asm volatile("" : "+v"(cl));
+        const int li = cl & 15, q = cl >> 4;
+        if (rnd > 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const int kb0 = (kMf8Waves * rnd + wave) * kMf8Blocks;  // the wave's first block
+        const uint8_t *asrc = a + kb0 * 34;  // the wave's slice of activation row 0
+        auto copy_h0 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, cl); };
+        auto copy_h1 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 8, m - 16 * ch, h1, cl); };
+        run_copy<16, 9>(w + ((size_t)n0 * nb + kb0) * 18, nb * 18, 0, n - n0, wl, cl);
+        copy_h0(0);
+        copy_h1(0);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // weights and H0(0)
+        // the weight slice, once: block j's 8 int8 operands of this lane and its scale
+        const uint8_t *wr = wl + li * 144;
+        uint64_t bop[kMf8Blocks];
+        uint32_t dw[kMf8Blocks];
+    #pragma unroll
+        for (int j = 0; j < kMf8Blocks; ++j) {
+            uint32_t wq;
+            if ((j & 1) == 0) {  // two bytes into its dwords
+                const uint32_t *w0 = reinterpret_cast<const uint32_t *>(wr + j * 18 + 4 * q);
+                wq = shift2(w0[0], w0[1]);
             } else {
-                const uint32_t *a1 = reinterpret_cast<const uint32_t *>(ar + 2 + 4 * q);
-                x0 = a1[0];
-                x1 = a1[4];
+                wq = *reinterpret_cast<const uint32_t *>(wr + j * 18 + 2 + 4 * q);
             }
-            const i32x4 s16 = mfma_i8_16x16x32((uint64_t)x0 | ((uint64_t)x1 << 32), bop[j], (i32x4){0, 0, 0, 0});
-            const uint32_t da_all = *reinterpret_cast<const uint16_t *>(ar);  // every lane reads: no branch
-            const uint32_t da = q == 0 ? da_all : 0u;
-            const f16x4 pa = __builtin_bit_cast(f16x4, make_uint2(da, 0u));
-            const f16x4 pb = __builtin_bit_cast(f16x4, make_uint2(dw[j], 0u));
-            const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, pb, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[ch][r] = __builtin_fmaf((float)s16[r], p[r], acc[ch][r]);
-        };
-        if (ch > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H0(ch)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) block(j);
-        if (ch + 1 < C) {
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H0 read: refill it
-            copy_h0(ch + 1);
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H1(ch)
-        } else {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            bop[j] = (uint64_t)q4_0_lo16(wq) | ((uint64_t)q4_0_hi16(wq) << 32);
+            const uint32_t dw_all = *reinterpret_cast<const uint16_t *>(wr + j * 18);  // every lane reads: no branch
+            dw[j] = q == 0 ? dw_all : 0u;
         }
-#pragma unroll
-        for (int j = 4; j < kMf8Blocks; ++j) block(j);
-        if (ch + 1 < C) {
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H1 read: refill it
-            copy_h1(ch + 1);
+    #pragma unroll
+        for (int ch = 0; ch < C; ++ch) {
+            // block j of the chunk row li: slice byte 34 j, in H0 (j < 4) or H1 (from slice byte 128)
+            auto block = [&](int j) {
+                const uint8_t *ar = (j < 4 ? h0 + li * 144 : h1 + li * 144 - 128) + j * 34;
+                uint32_t x0, x1;
+                if ((j & 1) == 0) {
+                    const uint32_t *a0 = reinterpret_cast<const uint32_t *>(ar + 4 * q);
+                    x0 = shift2(a0[0], a0[1]);
+                    x1 = shift2(a0[4], a0[5]);
+                } else {
+                    const uint32_t *a1 = reinterpret_cast<const uint32_t *>(ar + 2 + 4 * q);
+                    x0 = a1[0];
+                    x1 = a1[4];
+                }
+                const i32x4 s16 = mfma_i8_16x16x32((uint64_t)x0 | ((uint64_t)x1 << 32), bop[j], (i32x4){0, 0, 0, 0});
+                const uint32_t da_all = *reinterpret_cast<const uint16_t *>(ar);  // every lane reads: no branch
+                const uint32_t da = q == 0 ? da_all : 0u;
+                const f16x4 pa = __builtin_bit_cast(f16x4, make_uint2(da, 0u));
+                const f16x4 pb = __builtin_bit_cast(f16x4, make_uint2(dw[j], 0u));
+                const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, pb, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    #pragma unroll
+                for (int r = 0; r < 4; ++r) acc[ch][r] = __builtin_fmaf((float)s16[r], p[r], acc[ch][r]);
+            };
+            if (ch > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H0(ch)
+    #pragma unroll
+            for (int j = 0; j < 4; ++j) block(j);
+            if (ch + 1 < C) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H0 read: refill it
+                copy_h0(ch + 1);
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H1(ch)
+            } else {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+    #pragma unroll
+            for (int j = 4; j < kMf8Blocks; ++j) block(j);
+            if (ch + 1 < C) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H1 read: refill it
+                copy_h1(ch + 1);
+            }
         }
     }
     // wave partials through LDS ([wave][group g = 4 chunk + r][lane]); wave w
     // adds groups w, w + 16, ... over the waves in wave order and stores them
     __syncthreads();
+    const int li = lane & 15, q = lane >> 4;
     float *red = reinterpret_cast<float *>(lds);
 #pragma unroll
     for (int ch = 0; ch < C; ++ch)
@@ -827,44 +845,37 @@ hipError_t launch_fused_m(const void *w, const float *x, float *c, int64_t n, in
     return hipGetLastError();
 }
 
-// Waves of the MFMA tile kernels for m activation rows and k, 0 where the
-// pairs kernel runs instead: 16 waves of 8-block slices (k % 4096 == 0) from
-// m = 9 (from m = 7 at k = 4096, below), where they measured faster than the pairs kernel (4096 x 4096, µs:
-// m = 8 5.93 against 5.98, m = 10 6.15 / 6.95, m = 12 6.11 / 7.86, m = 16
-// 6.21 / 9.54); 8 waves of 8-block slices (k % 2048 == 0) from m = 12 (m = 12
-// 7.14 / 7.86, m = 10 7.18 / 6.95). Both while the slices fit the LDS.
-int mf_gemv_waves(int64_t m, int64_t k) {
-    if (m > 16 || mf_gemv_lds_bytes(m, k / 32) > kPairsMaxLds) return 0;
-    if (m >= 9 && k % 4096 == 0) return 16;
-    if (m >= 12 && k % 2048 == 0) return 8;
-    return 0;
+// The 8-wave MFMA tile kernel (8-block slices, k % 2048 == 0) from m = 12
+// while its slices fit the LDS, where it measured faster than the pairs
+// kernel (k = 4096, us: m = 12 7.14 / 7.86, m = 10 7.18 / 6.95); at
+// k % 4096 == 0 the chunk kernel runs instead.
+bool mf_gemv_fits(int64_t m, int64_t k) {
+    return m >= 12 && m <= 16 && k % 2048 == 0 && mf_gemv_lds_bytes(m, k / 32) <= kPairsMaxLds;
 }
 
 template <int M>
 hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n, int64_t k, hipStream_t stream) {
     const int nb = (int)(k / 32);
-    if (M >= 6 && k == 4096) {  // gemv_q4_0_mfma_chunk_kernel, one chunk
+    // gemv_q4_0_mfma_chunk_kernel, one chunk: from m = 6 at k = 4096, from m = 5
+    // above (m = 5, n = 4096, against the kernels it replaced, us: k = 4096
+    // 5.15 / 4.93, k = 8192 7.91 / 8.13-8.58, k = 12288 10.65 / 11.07-11.76)
+    if ((M >= 6 || (M == 5 && k > 4096)) && k % 4096 == 0) {
         hipLaunchKernelGGL(gemv_q4_0_mfma_chunk_kernel<1>, dim3((unsigned)((n + 15) / 16)), dim3(kMf8Waves * 64),
                            (size_t)kMf8Waves * kQ40ChunkWaveBytes, stream, static_cast<const uint8_t *>(w),
-                           static_cast<const uint8_t *>(a), c, M, (int)n);
+                           static_cast<const uint8_t *>(a), c, M, (int)n, (int)(k / 4096));
         return hipGetLastError();
     }
-    if (const int wv = mf_gemv_waves(M, k)) {
+    if (mf_gemv_fits(M, k)) {
+        constexpr int wv = 8;
         const int bw = nb / wv;  // blocks per wave, a multiple of 8
         MfGemvGeom geo;
         geo.cprw = bw * 18 / 16;
         geo.cpra = bw * 34 / 16;
         geo.magw = (uint32_t)((((uint64_t)1 << 32) + geo.cprw - 1) / geo.cprw);
         geo.maga = (uint32_t)((((uint64_t)1 << 32) + geo.cpra - 1) / geo.cpra);
-        const dim3 grid((unsigned)((n + 15) / 16));
-        const size_t lds = (size_t)mf_gemv_lds_bytes(M, nb);
-        const uint8_t *wp = static_cast<const uint8_t *>(w), *ap = static_cast<const uint8_t *>(a);
-        if (wv == 16)
-            hipLaunchKernelGGL((gemv_q4_0_mfma_kernel<M, 16>), grid, dim3(16 * 64), lds, stream, wp, ap, c, (int)n, nb,
-                               geo);
-        else
-            hipLaunchKernelGGL((gemv_q4_0_mfma_kernel<M, 8>), grid, dim3(8 * 64), lds, stream, wp, ap, c, (int)n, nb,
-                               geo);
+        hipLaunchKernelGGL((gemv_q4_0_mfma_kernel<M, wv>), dim3((unsigned)((n + 15) / 16)), dim3(wv * 64),
+                           (size_t)mf_gemv_lds_bytes(M, nb), stream, static_cast<const uint8_t *>(w),
+                           static_cast<const uint8_t *>(a), c, (int)n, nb, geo);
         return hipGetLastError();
     }
     if (k % 64 == 0 && pairs_lds_bytes(M, nb) <= kPairsMaxLds) {
@@ -918,11 +929,13 @@ bool gemv_supported(int type, int64_t m, int64_t k) {
     if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) {
         if (m == 1) return k % 64 == 0;
         if (m <= 8) return k % 256 == 0 || pairs;
-        if (m > 16) return m <= 16 * kMaxGemvChunks && k == 4096;  // gemv_q4_0_mfma_chunk_kernel
-        return m <= kPairsMaxM && pairs;  // m = 9..16 only in the pair-per-lane kernel
+        // m = 9..128 at k % 4096 == 0: gemv_q4_0_mfma_chunk_kernel; otherwise m = 9..16
+        // in the pair-per-lane kernel (or the 8-wave tile, whose slices need more LDS)
+        if (m <= 16 * kMaxGemvChunks && k % 4096 == 0) return true;
+        return m <= kPairsMaxM && pairs;
     }
     // q4_K and iq2_xxs (gemv_kquant.hip): m <= 8 for every k % 256 == 0,
-    // m = 9..16 while the staged activations fit in LDS, m = 17..64 at k == 4096
+    // m = 9..16 while the staged activations fit in LDS, m = 9..128 at k % 4096 == 0
     if (m > 8) return (kquant_gemv_staged_fits(m, k) || kquant_gemv_chunked_fits(m, k)) &&
                       (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K || type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K);
     return (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K || type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K) && k % 256 == 0;
@@ -963,14 +976,16 @@ hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t
     case 16: return launch_gemv_q4_0_m<16>(w, a, c, n, k, stream);
     default: break;
     }
-    if (!(m >= 17 && m <= 16 * kMaxGemvChunks && k == 4096)) return hipErrorInvalidValue;
+    if (!(m >= 17 && m <= 16 * kMaxGemvChunks && k % 4096 == 0)) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((n + 15) / 16)), block(kMf8Waves * 64);
     const size_t lds = (size_t)kMf8Waves * kQ40ChunkWaveBytes;
+    const int rounds = (int)(k / 4096);
     const auto *wp = static_cast<const uint8_t *>(w);
     const auto *ap = static_cast<const uint8_t *>(a);
 #define PFNG_Q40_CHUNK_CASE(C)                                                                                      \
     case C:                                                                                                        \
-        hipLaunchKernelGGL(gemv_q4_0_mfma_chunk_kernel<C>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n); \
+        hipLaunchKernelGGL(gemv_q4_0_mfma_chunk_kernel<C>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n,     \
+                           rounds);                                                                            \
         break;
     switch ((m + 15) / 16) {
         PFNG_Q40_CHUNK_CASE(2)

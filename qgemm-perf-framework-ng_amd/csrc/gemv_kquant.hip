@@ -1,4 +1,4 @@
-// GEMV path (m <= 16, and up to 128 at k == 4096) for the super-block formats
+// GEMV path (m <= 16, and up to 128 at k % 4096 == 0) for the super-block formats
 // against q8_K activations:
 // q4_K (llama_reference.cpp:113-132) and iq2_xxs (llama_reference.cpp:148-161,
 // kernels/common/iq2_xxs.h:29-41). One wavefront per weight row, the weight
@@ -8,13 +8,13 @@
 // (m <= 8) take m == 1 and rows too long to stage; for q4_K at m == 1 the
 // 16-row workgroups copy the activation row into LDS first. The
 // *_staged_kernel variants (m = 2..16) stage the rows in LDS once per 16-row
-// workgroup. At k == 4096 both formats run 16x16 int8 MFMA tiles of 16 weight
-// rows with one super-block per wave: iq2_xxs at m = 5..8 with the weight and
-// activation bytes copied together in two halves (gemv_iq2_xxs_mfma_sb_kernel),
-// and from m = 5 (q4_K) or 9 (iq2_xxs) with the weights decoded once per wave
-// and the activation rows streamed in chunks of 16 (*_mfma_chunk_kernel); q4_K
-// at larger k % 4096 == 0 runs gemv_q4_K_mfma_kernel, whose waves take
-// k / 4096 super-blocks each.
+// workgroup. At k % 4096 == 0 both formats run 16x16 int8 MFMA tiles of 16
+// weight rows with one super-block per wave: iq2_xxs at m = 5..8 and k == 4096
+// with the weight and activation bytes copied together in two halves
+// (gemv_iq2_xxs_mfma_sb_kernel), and from m = 5 (q4_K) or 9 (iq2_xxs) with the
+// weights decoded once per wave and the activation rows streamed in chunks of
+// 16 (*_mfma_chunk_kernel; at k = 4096 r each wave takes r super-blocks, one
+// per round).
 //
 // q4_K: four lanes per super-block, lane e owning sub-blocks 2e and 2e+1 (the
 // 32 nibble bytes qs[32e .. 32e+32): low nibbles of sub-block 2e, high of
@@ -814,130 +814,8 @@ __global__ __launch_bounds__(kStagedThreads) void gemv_iq2_xxs_staged_kernel(con
     }
 }
 
-// q4_K, m = 9..16 with k % 4096 == 0: 16x16 int8 MFMA tiles, as
-// gemv_q4_0_mfma_kernel. A workgroup takes 16 weight rows; each of its 16
-// waves takes nsb / 16 super-blocks of the 16 weight rows and the m
-// activation rows, copies them into its own LDS region with direct loads
-// (16 bytes per lane for the weights; 4 for the activations, whose 292-byte
-// blocks are only dword-aligned) and waits for its own copies. Per 32-element
-// sub-block j: one v_mfma_i32_16x16x32_i8 of the unsigned nibbles (q4_K has
-// no offset) with the activation bytes (lane l: K positions 4q..4q+3 and
-// 16+4q..16+4q+3, q = l / 16) gives S_j, and IS += sc_j * S_j for the lane's
-// four results (24-bit multiplies; sc_j of the lane's weight row). Per
-// super-block: IM = sum_j m_j * (bsums[2j] + bsums[2j+1]) with one
-// v_dot2_i32_i16 per sub-block, and acc += d_a * (d * IS - dmin * IM) as the
-// reference forms it (llama_reference.cpp:107-131). The wave partials are
-// added in wave order at the end.
+// the MFMA tile GEMVs below run 16 waves per workgroup
 constexpr int kKqMfWaves = 16;
-
-__host__ __device__ constexpr int64_t kq_mf_region(int64_t m, int64_t s) {
-    return 16 * 144 * s + (m * 292 * s + 15) / 16 * 16;  // one wave: weight rows, then activation rows
-}
-__host__ __device__ constexpr int64_t kq_mf_lds_bytes(int64_t m, int64_t nsb) {
-    return kKqMfWaves * kq_mf_region(m, nsb / kKqMfWaves);
-}
-
-struct KqMfGeom {
-    int cprw, cpra;       // 16-byte chunks per weight row slice, dwords per activation row slice
-    uint32_t magw, maga;  // ceil(2^32 / cpr): index -> row by one v_mul_hi_u32
-};
-
-template <int M>
-__global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_kernel(const uint8_t *__restrict__ w,
-                                                                         const uint8_t *__restrict__ a,
-                                                                         float *__restrict__ c, int n, int nsb,
-                                                                         KqMfGeom geo) {
-    static_assert(M >= 1 && M <= 16, "one 16-row tile of activation rows");
-    extern __shared__ __align__(16) uint8_t lds[];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int n0 = blockIdx.x * 16;
-    const int s = nsb / kKqMfWaves;  // super-blocks per wave
-    const int sb0 = wave * s;
-    const int rw = s * 144, ra = s * 292;
-    uint8_t *ws = lds + (size_t)wave * kq_mf_region(M, s);
-    uint8_t *as = ws + 16 * rw;
-    const int nw = 16 * geo.cprw, na = M * geo.cpra;
-    for (int c0 = 0; c0 < nw; c0 += 64) {
-        const uint32_t ch = (uint32_t)(c0 + lane);
-        const int row = (int)__umulhi(ch, geo.magw);
-        const int col = (int)ch - row * geo.cprw;
-        if ((int)ch < nw && n0 + row < n)
-            __builtin_amdgcn_global_load_lds(w + ((size_t)(n0 + row) * nsb + sb0) * 144 + col * 16,
-                                             (__attribute__((address_space(3))) void *)(ws + c0 * 16), 16, 0, 0);
-    }
-    for (int c0 = 0; c0 < na; c0 += 64) {
-        const uint32_t ch = (uint32_t)(c0 + lane);
-        const int row = (int)__umulhi(ch, geo.maga);
-        const int col = (int)ch - row * geo.cpra;
-        if ((int)ch < na)
-            __builtin_amdgcn_global_load_lds(a + ((size_t)row * nsb + sb0) * kQ8KBytes + col * 4,
-                                             (__attribute__((address_space(3))) void *)(as + c0 * 4), 4, 0, 0);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave reads only what it copied
-    const int li = lane & 15, q = lane >> 4;
-    const int arow = li < M ? li : M - 1;
-    int orow[4];  // activation rows of this lane's four results (clamped)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) orow[r] = 4 * q + r < M ? 4 * q + r : M - 1;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int t = 0; t < s; ++t) {
-        const uint8_t *wb = ws + li * rw + t * 144;  // weight row li, super-block t
-        const uint4 hd = *reinterpret_cast<const uint4 *>(wb);
-        // scales (bytes 0..3: sub-blocks 0..3, 4..7: 4..7) and mins, as q4_K_scale_min_pair
-        const uint32_t scw[2] = {hd.y & 0x3f3f3f3fu, (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u)};
-        const uint32_t mnw[2] = {hd.z & 0x3f3f3f3fu, ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u)};
-        const uint8_t *ab = as + arow * ra + t * kQ8KBytes + 4 + 4 * q;
-        int is[4] = {0, 0, 0, 0}, im[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            // sub-block j: nibbles of bytes 32 (j / 2) + {4q.., 16 + 4q..}, low for even j
-            const uint32_t x0 = *reinterpret_cast<const uint32_t *>(wb + 16 + 32 * (j / 2) + 4 * q);
-            const uint32_t x1 = *reinterpret_cast<const uint32_t *>(wb + 32 + 32 * (j / 2) + 4 * q);
-            const uint32_t w0 = (j & 1 ? x0 >> 4 : x0) & 0x0f0f0f0fu;
-            const uint32_t w1 = (j & 1 ? x1 >> 4 : x1) & 0x0f0f0f0fu;
-            const uint32_t y0 = *reinterpret_cast<const uint32_t *>(ab + 32 * j);
-            const uint32_t y1 = *reinterpret_cast<const uint32_t *>(ab + 32 * j + 16);
-            const i32x4 sj = mfma_i8_16x16x32((uint64_t)y0 | ((uint64_t)y1 << 32), (uint64_t)w0 | ((uint64_t)w1 << 32),
-                                              (i32x4){0, 0, 0, 0});
-            const int sc = (int)((scw[j / 4] >> (8 * (j % 4))) & 0xffu);
-            const int mn = (int)((mnw[j / 4] >> (8 * (j % 4))) & 0xffu);
-            typedef short s16x2 __attribute__((ext_vector_type(2)));
-            const s16x2 mm = {(short)mn, (short)mn};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                is[r] += __mul24(sc, sj[r]);
-                const uint32_t bs = *reinterpret_cast<const uint32_t *>(as + orow[r] * ra + t * kQ8KBytes + 260 + 4 * j);
-                im[r] = __builtin_amdgcn_sdot2(__builtin_bit_cast(s16x2, bs), mm, im[r], false);
-            }
-        }
-        const float d = fp16_to_f32(hd.x & 0xffffu), dmin = fp16_to_f32(hd.x >> 16);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float ad = *reinterpret_cast<const float *>(as + orow[r] * ra + t * kQ8KBytes);
-            acc[r] += ad * fmaf(-dmin, (float)im[r], d * (float)is[r]);
-        }
-    }
-    __syncthreads();
-    float *red = reinterpret_cast<float *>(lds);
-    if (wave > 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red[((wave - 1) * 4 + r) * 64 + lane] = acc[r];
-    }
-    __syncthreads();
-    if (wave == 0) {
-        for (int v = 1; v < kKqMfWaves; ++v) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] += red[((v - 1) * 4 + r) * 64 + lane];
-        }
-        const int col = n0 + li;
-        if (col < n) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                if (4 * q + r < M) c[(size_t)(4 * q + r) * n + col] = acc[r];
-        }
-    }
-}
 
 // Two-half copies for the iq2_xxs GEMV with one super-block per wave
 // (k == 4096, m = 5..8). A wave copies its super-block of the tile's 16 weight rows and
@@ -1116,9 +994,11 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_sb_kernel(c
     }
 }
 
-// k == 4096 from m = 5 (q4_K) or m = 9 (iq2_xxs) up to m = 16 * kMaxGemvChunks:
-// 16x16 int8 MFMA tiles of 16 weight rows with one super-block per wave, the
-// activation rows taken in C = ceil(m / 16) chunks of 16. Each wave copies its
+// k % 4096 == 0 from m = 5 (q4_K) or m = 9 (iq2_xxs) up to m = 16 * kMaxGemvChunks:
+// 16x16 int8 MFMA tiles of 16 weight rows with one super-block per wave and
+// round (round r takes super-block 16 r + wave of every row; the partial sums
+// stay in registers across the k / 4096 rounds), the activation rows taken in
+// C = ceil(m / 16) chunks of 16. Each wave copies its
 // super-block of the tile's 16 weight rows once, decodes them once into
 // registers, and then streams the chunks: chunk c's activation blocks arrive in two halves (H0:
 // copy chunks 0..8 of each row, d and sub-blocks 0..3; H1: chunks 8..18 or
@@ -1143,10 +1023,11 @@ __host__ __device__ constexpr int q4k_chunk_lds_bytes() { return kKqMfWaves * kC
 template <int C>
 __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(const uint8_t *__restrict__ w,
                                                                              const uint8_t *__restrict__ a,
-                                                                             float *__restrict__ c, int m, int n) {
+                                                                             float *__restrict__ c, int m, int n,
+                                                                             int rounds) {
     static_assert(C >= 1 && C <= kMaxGemvChunks, "at most kMaxGemvChunks chunks of 16 activation rows");
-    constexpr int nsb = kKqMfWaves;  // k == 4096
-    constexpr uint32_t kARow = nsb * kQ8KBytes;
+    const int nsb = kKqMfWaves * rounds;  // k == 4096 * rounds
+    const uint32_t kARow = (uint32_t)nsb * kQ8KBytes;
     constexpr int kH = run_copies<16, 11>();  // instructions per half (H1: 11 columns, H0: 9)
     static_assert(run_copies<16, 9>() == kH && run_copies<16, 9>() * 1024 <= 3072, "3 KB per run");
     static_assert(kKqMfWaves * 4 * C * 64 * 4 <= q4k_chunk_lds_bytes(), "wave partials fit the LDS");
@@ -1156,77 +1037,93 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
     const int n0 = blockIdx.x * 16;
     const int o = 4 * (wave & 3);
     uint8_t *wl = lds + wave * kChunkWaveBytes, *h0 = wl + 3072, *h1 = wl + 6144;
-    const uint8_t *asrc = a + wave * kQ8KBytes - o;  // copy start of the wave's block in activation row 0
-    auto copy_h0 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, lane); };
-    auto copy_h1 = [&](int ch) { run_copy<16, 11>(asrc + (size_t)ch * 16 * kARow, kARow, 8, m - 16 * ch, h1, lane); };
-    run_copy<16, 9>(w + ((size_t)n0 * nsb + wave) * 144, nsb * 144, 0, n - n0, wl, lane);
-    copy_h0(0);
-    copy_h1(0);
-    const int li = lane & 15, q = lane >> 4;
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // weights and H0(0)
-    // the weight row's decode, once: scales, mins, d, dmin and the nibble operands
-    const uint8_t *wr = wl + li * 144;
-    const uint32_t *hp = reinterpret_cast<const uint32_t *>(wr);
-    const uint4 hd = make_uint4(hp[0], hp[1], hp[2], hp[3]);
-    const uint32_t scw[2] = {hd.y & 0x3f3f3f3fu, (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u)};
-    const uint32_t mnw[2] = {hd.z & 0x3f3f3f3fu, ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u)};
-    uint64_t wv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t x0 = *reinterpret_cast<const uint32_t *>(wr + 16 + 32 * (j / 2) + 4 * q);
-        const uint32_t x1 = *reinterpret_cast<const uint32_t *>(wr + 32 + 32 * (j / 2) + 4 * q);
-        const uint32_t v0 = (j & 1 ? x0 >> 4 : x0) & 0x0f0f0f0fu, v1 = (j & 1 ? x1 >> 4 : x1) & 0x0f0f0f0fu;
-        wv[j] = (uint64_t)v0 | ((uint64_t)v1 << 32);
-    }
-    const uint32_t mp = (q & 2 ? mnw[1] : mnw[0]) >> (16 * (q & 1));
-    const _Float16 m0 = (_Float16)(int)(mp & 0xffu), m1 = (_Float16)(int)((mp >> 8) & 0xffu);
-    const f16x4 mm = {m0, m0, m1, m1};
-    const float d = fp16_to_f32(hd.x & 0xffffu), dmin = fp16_to_f32(hd.x >> 16);
-    // activation byte b of chunk row r: H0 at h0 + 144 r + o + b, H1 at h1 + 176 r + o + b - 128
-    const uint8_t *a0 = h0 + li * 144 + o + 4 + 4 * q, *a1 = h1 + li * 176 + o - 128 + 4 + 4 * q;
     float acc[C][4];
 #pragma unroll
-    for (int ch = 0; ch < C; ++ch) {
-        if (ch > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H0(ch)
-        int is[4] = {0, 0, 0, 0};
-        auto sub = [&](int j, const uint8_t *ay) {
-            const uint32_t y0 = *reinterpret_cast<const uint32_t *>(ay + 32 * j);
-            const uint32_t y1 = *reinterpret_cast<const uint32_t *>(ay + 32 * j + 16);
-            const i32x4 sj = mfma_i8_16x16x32((uint64_t)y0 | ((uint64_t)y1 << 32), wv[j], (i32x4){0, 0, 0, 0});
-            const int sc = (int)((scw[j / 4] >> (8 * (j % 4))) & 0xffu);
+    for (int ch = 0; ch < C; ++ch)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) is[r] += __mul24(sc, sj[r]);
-        };
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sub(j, a0);
-        float ad[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) ad[r] = *reinterpret_cast<const float *>(h0 + (4 * q + r) * 144 + o);
-        if (ch + 1 < C) {
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H0 read: refill it
-            copy_h0(ch + 1);
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H1(ch)
-        } else {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        for (int r = 0; r < 4; ++r) acc[ch][r] = 0.0f;
+    // round rnd takes the wave's K slice 16 rnd + wave of every row; the next
+    // round's copies start once the last round's buffers have been read
+    for (int rnd = 0; rnd < rounds; ++rnd) {
+        // a lane index the compiler cannot carry across rounds: the per-lane
+        // copy offsets and LDS addresses are recomputed per round instead of
+        // held in registers for the whole loop
+        int cl = lane;
+        asm volatile("" : "+v"(cl));
+        const int li = cl & 15, q = cl >> 4;
+        if (rnd > 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const int sb = kKqMfWaves * rnd + wave;
+        const uint8_t *asrc = a + sb * kQ8KBytes - o;  // copy start of the wave's block in activation row 0
+        auto copy_h0 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, cl); };
+        auto copy_h1 = [&](int ch) { run_copy<16, 11>(asrc + (size_t)ch * 16 * kARow, kARow, 8, m - 16 * ch, h1, cl); };
+        run_copy<16, 9>(w + ((size_t)n0 * nsb + sb) * 144, nsb * 144, 0, n - n0, wl, cl);
+        copy_h0(0);
+        copy_h1(0);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // weights and H0(0)
+        // the weight row's decode, once: scales, mins, d, dmin and the nibble operands
+        const uint8_t *wr = wl + li * 144;
+        const uint32_t *hp = reinterpret_cast<const uint32_t *>(wr);
+        const uint4 hd = make_uint4(hp[0], hp[1], hp[2], hp[3]);
+        const uint32_t scw[2] = {hd.y & 0x3f3f3f3fu, (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u)};
+        const uint32_t mnw[2] = {hd.z & 0x3f3f3f3fu, ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u)};
+        uint64_t wv[8];
+    #pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t x0 = *reinterpret_cast<const uint32_t *>(wr + 16 + 32 * (j / 2) + 4 * q);
+            const uint32_t x1 = *reinterpret_cast<const uint32_t *>(wr + 32 + 32 * (j / 2) + 4 * q);
+            const uint32_t v0 = (j & 1 ? x0 >> 4 : x0) & 0x0f0f0f0fu, v1 = (j & 1 ? x1 >> 4 : x1) & 0x0f0f0f0fu;
+            wv[j] = (uint64_t)v0 | ((uint64_t)v1 << 32);
         }
-#pragma unroll
-        for (int j = 4; j < 8; ++j) sub(j, a1);
-        // IM: A = bsums 4q..4q+3 of the lane's activation row, B = the mins (mm)
-        const uint32_t b01 = *reinterpret_cast<const uint32_t *>(a1 - 4 - 4 * q + 260 + 8 * q);
-        const uint32_t b23 = *reinterpret_cast<const uint32_t *>(a1 - 4 - 4 * q + 264 + 8 * q);
-        const f16x4 bs = {(_Float16)(short)(b01 & 0xffffu), (_Float16)(short)(b01 >> 16),
-                          (_Float16)(short)(b23 & 0xffffu), (_Float16)(short)(b23 >> 16)};
-        const f32x4 im = __builtin_amdgcn_mfma_f32_16x16x16f16(bs, mm, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[ch][r] = ad[r] * fmaf(-dmin, im[r], d * (float)is[r]);
-        if (ch + 1 < C) {
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H1 read: refill it
-            copy_h1(ch + 1);
+        const uint32_t mp = (q & 2 ? mnw[1] : mnw[0]) >> (16 * (q & 1));
+        const _Float16 m0 = (_Float16)(int)(mp & 0xffu), m1 = (_Float16)(int)((mp >> 8) & 0xffu);
+        const f16x4 mm = {m0, m0, m1, m1};
+        const float d = fp16_to_f32(hd.x & 0xffffu), dmin = fp16_to_f32(hd.x >> 16);
+        // activation byte b of chunk row r: H0 at h0 + 144 r + o + b, H1 at h1 + 176 r + o + b - 128
+        const uint8_t *a0 = h0 + li * 144 + o + 4 + 4 * q, *a1 = h1 + li * 176 + o - 128 + 4 + 4 * q;
+    #pragma unroll
+        for (int ch = 0; ch < C; ++ch) {
+            if (ch > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H0(ch)
+            int is[4] = {0, 0, 0, 0};
+            auto sub = [&](int j, const uint8_t *ay) {
+                const uint32_t y0 = *reinterpret_cast<const uint32_t *>(ay + 32 * j);
+                const uint32_t y1 = *reinterpret_cast<const uint32_t *>(ay + 32 * j + 16);
+                const i32x4 sj = mfma_i8_16x16x32((uint64_t)y0 | ((uint64_t)y1 << 32), wv[j], (i32x4){0, 0, 0, 0});
+                const int sc = (int)((scw[j / 4] >> (8 * (j % 4))) & 0xffu);
+    #pragma unroll
+                for (int r = 0; r < 4; ++r) is[r] += __mul24(sc, sj[r]);
+            };
+    #pragma unroll
+            for (int j = 0; j < 4; ++j) sub(j, a0);
+            float ad[4];
+    #pragma unroll
+            for (int r = 0; r < 4; ++r) ad[r] = *reinterpret_cast<const float *>(h0 + (4 * q + r) * 144 + o);
+            if (ch + 1 < C) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H0 read: refill it
+                copy_h0(ch + 1);
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H1(ch)
+            } else {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+    #pragma unroll
+            for (int j = 4; j < 8; ++j) sub(j, a1);
+            // IM: A = bsums 4q..4q+3 of the lane's activation row, B = the mins (mm)
+            const uint32_t b01 = *reinterpret_cast<const uint32_t *>(a1 - 4 - 4 * q + 260 + 8 * q);
+            const uint32_t b23 = *reinterpret_cast<const uint32_t *>(a1 - 4 - 4 * q + 264 + 8 * q);
+            const f16x4 bs = {(_Float16)(short)(b01 & 0xffffu), (_Float16)(short)(b01 >> 16),
+                              (_Float16)(short)(b23 & 0xffffu), (_Float16)(short)(b23 >> 16)};
+            const f32x4 im = __builtin_amdgcn_mfma_f32_16x16x16f16(bs, mm, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    #pragma unroll
+            for (int r = 0; r < 4; ++r) acc[ch][r] += ad[r] * fmaf(-dmin, im[r], d * (float)is[r]);
+            if (ch + 1 < C) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H1 read: refill it
+                copy_h1(ch + 1);
+            }
         }
     }
     // wave partials through LDS ([wave][group g = 4 chunk + r][lane]); wave w
     // adds groups w, w + 16, ... over the waves in wave order and stores them
     __syncthreads();
+    const int li = lane & 15, q = lane >> 4;
     float *red = reinterpret_cast<float *>(lds);
 #pragma unroll
     for (int ch = 0; ch < C; ++ch)
@@ -1242,7 +1139,7 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
     }
 }
 
-// iq2_xxs, m = 9..128 at k == 4096: as gemv_q4_K_mfma_chunk_kernel, with the
+// iq2_xxs, m = 9..128 at k % 4096 == 0: as gemv_q4_K_mfma_chunk_kernel, with the
 // weight decode of gemv_iq2_xxs_mfma_sb_kernel done once per wave (5 weight
 // columns per row, H1 = activation chunks 8..16) and the grid and sign tables
 // copied by waves 0..2 before everything else.
@@ -1253,10 +1150,11 @@ __host__ __device__ constexpr int iq2_chunk_lds_bytes() { return kIq2TableBytes 
 template <int C>
 __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kernel(const uint8_t *__restrict__ w,
                                                                                 const uint8_t *__restrict__ a,
-                                                                                float *__restrict__ c, int m, int n) {
+                                                                                float *__restrict__ c, int m, int n,
+                                                                                int rounds) {
     static_assert(C >= 1 && C <= kMaxGemvChunks, "at most kMaxGemvChunks chunks of 16 activation rows");
-    constexpr int nsb = kKqMfWaves;  // k == 4096
-    constexpr uint32_t kARow = nsb * kQ8KBytes;
+    const int nsb = kKqMfWaves * rounds;  // k == 4096 * rounds
+    const uint32_t kARow = (uint32_t)nsb * kQ8KBytes;
     constexpr int kH = run_copies<16, 9>();
     constexpr int kW = run_copies<16, 5>();
     static_assert(kH * 1024 <= 3072 && kW * 1024 <= 2048, "run sizes");
@@ -1276,70 +1174,88 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
                                          16, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    const uint8_t *asrc = a + wave * kQ8KBytes - o;
-    auto copy_h0 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, lane); };
-    auto copy_h1 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 8, m - 16 * ch, h1, lane); };
-    run_copy<16, 5>(w + ((size_t)n0 * nsb + wave) * kIq2Bytes - o2, nsb * kIq2Bytes, 0, n - n0, wl, lane);
-    copy_h0(0);
-    copy_h1(0);
-    // the table piece has landed once at most (weights + H0 + H1) loads are outstanding
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kW + 2 * kH) : "memory");
-    const int li = lane & 15, q = lane >> 4;
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // weights and H0(0)
-    // the weight row's decode, once: group q of every sub-block, its scale, d
-    const uint8_t *wr = wl + li * 80;  // weight block byte b at copy byte o2 + b
-    const uint32_t sh = (uint32_t)(o2 + 2) & 3u;
-    uint64_t wv[8];
-    int scale[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t *p = reinterpret_cast<const uint32_t *>(wr + ((o2 + 2 + 8 * j) & ~3));
-        const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
-        const uint32_t gidx = __builtin_amdgcn_alignbyte(d1, d0, sh), ss = __builtin_amdgcn_alignbyte(d2, d1, sh);
-        const uint64_t mag = *reinterpret_cast<const uint64_t *>(grid + ((gidx >> (8 * q)) & 0xffu) * 8);
-        const uint64_t neg = *reinterpret_cast<const uint64_t *>(grid + 256 * 8 + ((ss >> (7 * q)) & 0x7fu) * 8);
-        wv[j] = (mag ^ neg) + (neg & 0x0101010101010101ull);  // no carry crosses a byte: |mag| >= 8
-        scale[j] = 2 * (int)(ss >> 28) + 1;
-    }
-    const float t0 = 0.125f * fp16_to_f32(*reinterpret_cast<const uint16_t *>(wr + o2));
-    // activation bytes 4 + 32 j + 8q (+ 4) of chunk row li: H0 at h0 + 144 li + o + b, H1 at h1 + 144 li + o + b - 128
-    const uint8_t *a0 = h0 + li * 144 + o + 4 + 8 * q, *a1 = h1 + li * 144 + o - 128 + 4 + 8 * q;
     float acc[C][4];
 #pragma unroll
-    for (int ch = 0; ch < C; ++ch) {
-        if (ch > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H0(ch)
-        int is[4] = {0, 0, 0, 0};
-        auto sub = [&](int j, const uint8_t *ay) {
-            // one typed 8-byte read: the compiler then adds no wait for every outstanding copy before it
-            const uint64_t y = *reinterpret_cast<const u64_a4 *>(ay + 32 * j);
-            const i32x4 sj = mfma_i8_16x16x32(y, wv[j], (i32x4){0, 0, 0, 0});
+    for (int ch = 0; ch < C; ++ch)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) is[r] += __mul24(scale[j], sj[r]);
-        };
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sub(j, a0);
-        float ad[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) ad[r] = *reinterpret_cast<const float *>(h0 + (4 * q + r) * 144 + o);
-        if (ch + 1 < C) {
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H0 read: refill it
-            copy_h0(ch + 1);
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H1(ch)
-        } else {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        for (int r = 0; r < 4; ++r) acc[ch][r] = 0.0f;
+    // round rnd takes the wave's K slice 16 rnd + wave of every row; the next
+    // round's copies start once the last round's buffers have been read
+    for (int rnd = 0; rnd < rounds; ++rnd) {
+        // a lane index the compiler cannot carry across rounds: the per-lane
+        // copy offsets and LDS addresses are recomputed per round instead of
+        // held in registers for the whole loop
+        int cl = lane;
+        asm volatile("" : "+v"(cl));
+        const int li = cl & 15, q = cl >> 4;
+        if (rnd > 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const int sb = kKqMfWaves * rnd + wave;
+        const uint8_t *asrc = a + sb * kQ8KBytes - o;
+        auto copy_h0 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, cl); };
+        auto copy_h1 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 8, m - 16 * ch, h1, cl); };
+        run_copy<16, 5>(w + ((size_t)n0 * nsb + sb) * kIq2Bytes - o2, nsb * kIq2Bytes, 0, n - n0, wl, cl);
+        copy_h0(0);
+        copy_h1(0);
+        // the table piece has landed once at most (weights + H0 + H1) loads are
+        // outstanding (in later rounds no other load is: the wait passes, and the
+        // barrier keeps the waits in one straight line of code)
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kW + 2 * kH) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // weights and H0(0)
+        // the weight row's decode, once: group q of every sub-block, its scale, d
+        const uint8_t *wr = wl + li * 80;  // weight block byte b at copy byte o2 + b
+        const uint32_t sh = (uint32_t)(o2 + 2) & 3u;
+        uint64_t wv[8];
+        int scale[8];
+    #pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t *p = reinterpret_cast<const uint32_t *>(wr + ((o2 + 2 + 8 * j) & ~3));
+            const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
+            const uint32_t gidx = __builtin_amdgcn_alignbyte(d1, d0, sh), ss = __builtin_amdgcn_alignbyte(d2, d1, sh);
+            const uint64_t mag = *reinterpret_cast<const uint64_t *>(grid + ((gidx >> (8 * q)) & 0xffu) * 8);
+            const uint64_t neg = *reinterpret_cast<const uint64_t *>(grid + 256 * 8 + ((ss >> (7 * q)) & 0x7fu) * 8);
+            wv[j] = (mag ^ neg) + (neg & 0x0101010101010101ull);  // no carry crosses a byte: |mag| >= 8
+            scale[j] = 2 * (int)(ss >> 28) + 1;
         }
-#pragma unroll
-        for (int j = 4; j < 8; ++j) sub(j, a1);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[ch][r] = (t0 * ad[r]) * (float)is[r];
-        if (ch + 1 < C) {
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H1 read: refill it
-            copy_h1(ch + 1);
+        const float t0 = 0.125f * fp16_to_f32(*reinterpret_cast<const uint16_t *>(wr + o2));
+        // activation bytes 4 + 32 j + 8q (+ 4) of chunk row li: H0 at h0 + 144 li + o + b, H1 at h1 + 144 li + o + b - 128
+        const uint8_t *a0 = h0 + li * 144 + o + 4 + 8 * q, *a1 = h1 + li * 144 + o - 128 + 4 + 8 * q;
+    #pragma unroll
+        for (int ch = 0; ch < C; ++ch) {
+            if (ch > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H0(ch)
+            int is[4] = {0, 0, 0, 0};
+            auto sub = [&](int j, const uint8_t *ay) {
+                // one typed 8-byte read: the compiler then adds no wait for every outstanding copy before it
+                const uint64_t y = *reinterpret_cast<const u64_a4 *>(ay + 32 * j);
+                const i32x4 sj = mfma_i8_16x16x32(y, wv[j], (i32x4){0, 0, 0, 0});
+    #pragma unroll
+                for (int r = 0; r < 4; ++r) is[r] += __mul24(scale[j], sj[r]);
+            };
+    #pragma unroll
+            for (int j = 0; j < 4; ++j) sub(j, a0);
+            float ad[4];
+    #pragma unroll
+            for (int r = 0; r < 4; ++r) ad[r] = *reinterpret_cast<const float *>(h0 + (4 * q + r) * 144 + o);
+            if (ch + 1 < C) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H0 read: refill it
+                copy_h0(ch + 1);
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // H1(ch)
+            } else {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+    #pragma unroll
+            for (int j = 4; j < 8; ++j) sub(j, a1);
+    #pragma unroll
+            for (int r = 0; r < 4; ++r) acc[ch][r] += (t0 * ad[r]) * (float)is[r];
+            if (ch + 1 < C) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // H1 read: refill it
+                copy_h1(ch + 1);
+            }
         }
     }
     // wave partials through LDS ([wave][group g = 4 chunk + r][lane]); wave w
     // adds groups w, w + 16, ... over the waves in wave order and stores them
     __syncthreads();
+    const int li = lane & 15, q = lane >> 4;
     float *red = reinterpret_cast<float *>(lds);
 #pragma unroll
     for (int ch = 0; ch < C; ++ch)
@@ -1355,11 +1271,6 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
     }
 }
 
-// the q4_K MFMA tile kernel runs from m = 9 at k % 4096 == 0 while its slices fit the LDS
-bool kq_mf_fits(int64_t m, int64_t k) {
-    return m >= 9 && m <= 16 && k % 4096 == 0 && kq_mf_lds_bytes(m, k / 256) <= 160 * 1024;
-}
-
 template <int M>
 hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int64_t n, int64_t k,
                           hipStream_t stream) {
@@ -1367,14 +1278,17 @@ hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int6
     const auto *ap = static_cast<const uint8_t *>(a);
     const int64_t nsb = k / 256;
     if constexpr (M >= 5) {
-        // k == 4096: one super-block per wave, from m = 5 (4096 x 4096 against the
-        // staged kernel, us: iq2_xxs m = 4 5.23 / 5.08, m = 5 5.34 / 5.91, m = 8
-        // 5.56 / 6.58); one chunk of the chunked kernel for q4_K and, from m = 9,
-        // for iq2_xxs
+        // one super-block per wave (and round), from m = 5 (4096 x 4096 against
+        // the staged kernel, us: iq2_xxs m = 4 5.23 / 5.08, m = 5 5.34 / 5.91,
+        // m = 8 5.56 / 6.58): one chunk of the chunked kernel at k % 4096 == 0
+        // for q4_K and for iq2_xxs (at k = 4096 from m = 9, m = 5..8 taking the
+        // two-half-copy kernel; n = 4096, k = 8192 against the staged kernel,
+        // us: q4_K m = 8 8.06 / 11.12, m = 12 8.67 / 14.64; iq2_xxs m = 12
+        // 8.87 / 16.72)
         const dim3 tiles((unsigned)((n + 15) / 16)), block(kKqMfWaves * 64);
-        if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && k == 4096 && M >= 9) {
+        if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && k % 4096 == 0 && (M >= 9 || k > 4096)) {
             hipLaunchKernelGGL(gemv_iq2_xxs_mfma_chunk_kernel<1>, tiles, block, (size_t)iq2_chunk_lds_bytes(), stream,
-                               wp, ap, c, M, (int)n);
+                               wp, ap, c, M, (int)n, (int)(k / 4096));
             return hipGetLastError();
         }
         if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && k == 4096) {
@@ -1382,24 +1296,9 @@ hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int6
                                ap, c, (int)n);
             return hipGetLastError();
         }
-        if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K && k == 4096) {
+        if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K && k % 4096 == 0) {
             hipLaunchKernelGGL(gemv_q4_K_mfma_chunk_kernel<1>, tiles, block, (size_t)q4k_chunk_lds_bytes(), stream, wp,
-                               ap, c, M, (int)n);
-            return hipGetLastError();
-        }
-    }
-    if constexpr (M >= 9) {
-        // measured at 4096 x 4096 against the staged kernel (µs): m = 9 6.57 / 6.96,
-        // m = 12 6.92 / 7.97, m = 16 7.59 / 9.22; m = 8 ties (6.19 / 6.17)
-        if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K && kq_mf_fits(M, k)) {
-            const int sw = (int)(nsb / kKqMfWaves);
-            KqMfGeom geo;
-            geo.cprw = sw * 144 / 16;
-            geo.cpra = sw * kQ8KBytes / 4;
-            geo.magw = (uint32_t)((((uint64_t)1 << 32) + geo.cprw - 1) / geo.cprw);
-            geo.maga = (uint32_t)((((uint64_t)1 << 32) + geo.cpra - 1) / geo.cpra);
-            hipLaunchKernelGGL(gemv_q4_K_mfma_kernel<M>, dim3((unsigned)((n + 15) / 16)), dim3(kKqMfWaves * 64),
-                               (size_t)kq_mf_lds_bytes(M, nsb), stream, wp, ap, c, (int)n, (int)nsb, geo);
+                               ap, c, M, (int)n, (int)(k / 4096));
             return hipGetLastError();
         }
     }
@@ -1473,7 +1372,9 @@ bool kquant_gemv_staged_fits(int64_t m, int64_t k) {
     return m >= 2 && m <= 16 && k % 256 == 0 && kq_staged_lds_bytes(m, k / 256) <= 160 * 1024;
 }
 
-bool kquant_gemv_chunked_fits(int64_t m, int64_t k) { return m >= 17 && m <= 16 * kMaxGemvChunks && k == 4096; }
+bool kquant_gemv_chunked_fits(int64_t m, int64_t k) {
+    return m >= 9 && m <= 16 * kMaxGemvChunks && k % 4096 == 0 && k > 0;
+}
 
 hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                               hipStream_t stream) {
@@ -1504,13 +1405,15 @@ hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, 
     const dim3 grid((unsigned)((n + 15) / 16)), block(kKqMfWaves * 64);
     const bool q4k = type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K;
     const size_t lds = q4k ? (size_t)q4k_chunk_lds_bytes() : (size_t)iq2_chunk_lds_bytes();
+    const int rounds = (int)(k / 4096);
 #define PFNG_CHUNK_CASE(C)                                                                                      \
     case C:                                                                                                    \
         if (q4k)                                                                                               \
-            hipLaunchKernelGGL(gemv_q4_K_mfma_chunk_kernel<C>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n); \
+            hipLaunchKernelGGL(gemv_q4_K_mfma_chunk_kernel<C>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n, \
+                               rounds);                                                                        \
         else                                                                                                   \
             hipLaunchKernelGGL(gemv_iq2_xxs_mfma_chunk_kernel<C>, grid, block, lds, stream, wp, ap, c, (int)m,     \
-                               (int)n);                                                                        \
+                               (int)n, rounds);                                                                \
         return hipGetLastError();
     switch ((m + 15) / 16) {
         PFNG_CHUNK_CASE(2)

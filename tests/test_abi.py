@@ -59,10 +59,12 @@ def test_version_string(pkg):
     (lambda L: L.pfng_hip_mul_mat(0, None, None, None, 4, 4, 64, 0, None), 1),
     (lambda L: L.pfng_hip_mul_mat(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 4, 4, 64, 9, None), 1),
     (lambda L: L.pfng_hip_mul_mat(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 64, 4, 96, 2, None), 2),
-    # the GEMV takes up to m = 16 (m > 8 only while the activations fit in LDS)
+    # the GEMV takes up to m = 16 (m > 8 only while the activations fit in LDS),
+    # up to m = 128 at k % 4096 == 0; k = 20736 is 81 super-blocks
     (lambda L: L.pfng_hip_mul_mat(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 17, 4, 256, 1, None), 2),
     (lambda L: L.pfng_hip_mul_mat(1, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 17, 4, 256, 1, None), 2),
-    (lambda L: L.pfng_hip_mul_mat(2, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 9, 4, 20480, 1, None), 2),
+    (lambda L: L.pfng_hip_mul_mat(2, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 9, 4, 20736, 1, None), 2),
+    (lambda L: L.pfng_hip_mul_mat(2, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 129, 4, 8192, 1, None), 2),
     # the automatic path declines what no tiled path takes instead of falling
     # back to the one-thread-per-output kernel
     (lambda L: L.pfng_hip_mul_mat(0, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 17, 4, 96, 0, None), 2),
@@ -82,11 +84,14 @@ def test_argument_validation(pkg, call, expect):
 
 @pytest.mark.parametrize("qtype,m,n,k,expect", [
     (0, 1, 4096, 4096, 1), (0, 16, 4096, 4096, 1), (0, 17, 4096, 4096, 1), (0, 64, 4096, 4096, 1),
-    (0, 128, 4096, 4096, 1), (0, 129, 4096, 4096, 2), (0, 17, 4096, 8192, 2), (0, 480, 1536, 1536, 2),
+    (0, 128, 4096, 4096, 1), (0, 129, 4096, 4096, 2), (0, 480, 1536, 1536, 2),
     (0, 3, 5, 96, -1), (0, 17, 8, 96, -1), (0, 24, 32, 256, 2), (0, 0, 8, 64, 0),
     (1, 8, 64, 512, 1), (1, 480, 1536, 1536, 2), (2, 512, 4096, 4096, 2), (2, 1, 4096, 4096, 1),
-    # q4_K / iq2_xxs at k = 4096 keep the GEMV path up to m = 128 (chunks of 16 activation rows)
-    (1, 32, 4096, 4096, 1), (2, 128, 4096, 4096, 1), (2, 129, 4096, 4096, 2), (1, 17, 4096, 8192, 2),
+    # at k % 4096 == 0 the GEMV path runs up to m = 128 (MFMA tiles over chunks of 16
+    # activation rows, k / 4096 rounds); other k take the GEMM from m = 17
+    (1, 32, 4096, 4096, 1), (2, 128, 4096, 4096, 1), (2, 129, 4096, 4096, 2), (1, 17, 4096, 8192, 1),
+    (0, 17, 4096, 8192, 1), (0, 64, 4096, 12288, 1), (2, 16, 4096, 8192, 1), (1, 12, 4096, 12288, 1),
+    (1, 129, 4096, 8192, 2), (0, 17, 4096, 6144, 2), (2, 17, 4096, 6144, 2), (0, 12, 4096, 14336, 2),
     (0, 4, 4, 48, -1), (3, 4, 4, 64, -1),
 ])
 def test_auto_path_query(pkg, qtype, m, n, k, expect):

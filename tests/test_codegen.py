@@ -201,7 +201,7 @@ def test_half_split_copy_order(source, kernel, copies, after_half0):
 
 
 def check_chunk_waits(lines: list[str], chunks: int, table_wait: int | None = None) -> None:
-    """The chunked MFMA tile GEMVs (k = 4096, up to m = 128): no scratch memory (spill
+    """The chunked MFMA tile GEMVs (k % 4096 == 0, up to m = 128): no scratch memory (spill
     loads and stores would count in vmcnt and break the waits' arithmetic), and
     the vector-memory waits are exactly the designed ones: the table copy
     (iq2_xxs), then one vmcnt(3) before each half of each chunk but the last,
