@@ -1,4 +1,4 @@
-// q4_0 x q8_0 GEMV path (m <= 16, and up to 128 at k % 4096 == 0) for gfx950: the
+// q4_0 x q8_0 GEMV path (m <= 16, and up to 128 from k = 4096 at k % 256 == 0) for gfx950: the
 // weight stream is the roofline. Six kernels, picked in launch_gemv /
 // launch_fused_gemv:
 //
@@ -16,16 +16,17 @@
 //                              bytes, then the 8 fp16 scales).
 //   gemv_q4_0_fused_kernel     pfng_hip_compute for m <= 2: quantizes the fp32
 //                              activation rows into LDS, then as the m1 kernel.
-//   gemv_q4_0_mfma_kernel      m = 12..16 at k % 2048 == 0 (not a multiple
-//                              of 4096): 16x16 int8 MFMA tiles of 16 weight
-//                              rows, K split over the workgroup's 8 waves,
-//                              each wave's slices copied into LDS by direct
-//                              loads.
-//   gemv_q4_0_mfma_chunk_kernel k % 4096 == 0 from m = 6 up to m = 128: the
-//                              same tile with 8 blocks per wave and round
-//                              (k / 4096 rounds), each round's weights widened
-//                              into registers once and the activation rows
-//                              streamed through LDS in chunks of 16.
+//   gemv_q4_0_mfma_kernel      m = 12..16 at k = 2048: 16x16 int8 MFMA tiles
+//                              of 16 weight rows, K split over the
+//                              workgroup's 8 waves, each wave's slices copied
+//                              into LDS by direct loads.
+//   gemv_q4_0_mfma_chunk_kernel k % 256 == 0 from k = 4096, from m = 6 (m = 5
+//                              above k = 4096) up to m = 128: the same tile
+//                              with 8 blocks per wave and round (wave w takes
+//                              the 8-block groups w, w + 16, ...), each round's
+//                              weights widened into registers once and the
+//                              activation rows streamed through LDS in chunks
+//                              of 16.
 //
 // Every lane issues all the loads of a step before any arithmetic, so the
 // weight stream of the grid is in flight at once; weight rows are clamped so
@@ -481,8 +482,8 @@ __global__ __launch_bounds__(kPairsThreads) void gemv_q4_0_pairs_kernel(const ui
     }
 }
 
-// m = 12..16 with k % 2048 == 0 (8 waves; k % 4096 == 0 runs the chunk kernel
-// below): 16x16 int8 MFMA tiles. A workgroup takes 16 weight rows (output
+// m = 12..16 at k = 2048 (8 waves; from k = 4096 the chunk kernel below
+// runs): 16x16 int8 MFMA tiles. A workgroup takes 16 weight rows (output
 // columns) and all m activation rows; its WV waves split K into equal slices
 // of a multiple of 8 blocks, and each wave copies just its own slice of the 16 weight
 // rows and of the m activation rows into its own LDS region with direct loads
@@ -595,10 +596,11 @@ __global__ __launch_bounds__(WV * 64) void gemv_q4_0_mfma_kernel(const uint8_t *
     }
 }
 
-// k % 4096 == 0 (16 waves of 8 blocks per round; round r takes blocks
-// 8 (16 r + wave) .. + 8 of every row, the partial sums staying in registers
-// across the k / 4096 rounds) from m = 6: 16-row int8 MFMA tiles over C =
-// ceil(m / 16) chunks of 16 activation rows (m up to 16 * kMaxGemvChunks).
+// k % 256 == 0 from k = 4096 (16 waves of 8 blocks per round; round r takes
+// blocks 8 (16 r + wave) .. + 8 of every row while they exist, so waves can run
+// different numbers of rounds, the partial sums staying in registers) from
+// m = 6 (m = 5 above k = 4096): 16-row int8 MFMA tiles over C = ceil(m / 16)
+// chunks of 16 activation rows (m up to 16 * kMaxGemvChunks).
 constexpr int kMf8Blocks = 8;  // blocks per wave
 constexpr int kMf8Waves = 16;
 
@@ -623,9 +625,9 @@ template <int C>
 __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(const uint8_t *__restrict__ w,
                                                                               const uint8_t *__restrict__ a,
                                                                               float *__restrict__ c, int m, int n,
-                                                                              int rounds) {
+                                                                              int ng) {
     static_assert(C >= 1 && C <= kMaxGemvChunks, "at most kMaxGemvChunks chunks of 16 activation rows");
-    const int nb = kMf8Waves * kMf8Blocks * rounds;  // k == 4096 * rounds
+    const int nb = kMf8Blocks * ng;  // k == 256 * ng, ng >= kMf8Waves
     const uint32_t kARow = (uint32_t)nb * 34;
     constexpr int kH = run_copies<16, 9>();
     static_assert(kH * 1024 <= 3072, "3 KB per run");
@@ -642,7 +644,9 @@ __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(co
         for (int r = 0; r < 4; ++r) acc[ch][r] = 0.0f;
     // round rnd takes the wave's K slice 16 rnd + wave of every row; the next
     // round's copies start once the last round's buffers have been read
-    for (int rnd = 0; rnd < rounds; ++rnd) {
+    // this wave's rounds: its 8-block groups wave, wave + 16, ... below ng
+    const int my_rounds = (ng - wave + kMf8Waves - 1) / kMf8Waves;
+    for (int rnd = 0; rnd < my_rounds; ++rnd) {
         // a lane index the compiler cannot carry across rounds: the per-lane
         // copy offsets and LDS addresses are recomputed per round instead of
         // held in registers for the whole loop
@@ -845,10 +849,15 @@ hipError_t launch_fused_m(const void *w, const float *x, float *c, int64_t n, in
     return hipGetLastError();
 }
 
+// k the chunked MFMA tile kernel takes: groups of 8 blocks (256 elements), at
+// least one per wave (the slices and rows stay 16-byte aligned at every k % 256)
+bool q4_0_tiles_take_k(int64_t k) { return k % 256 == 0 && k >= 256 * kMf8Waves; }
+
 // The 8-wave MFMA tile kernel (8-block slices, k % 2048 == 0) from m = 12
 // while its slices fit the LDS, where it measured faster than the pairs
-// kernel (k = 4096, us: m = 12 7.14 / 7.86, m = 10 7.18 / 6.95); at
-// k % 4096 == 0 the chunk kernel runs instead.
+// kernel (k = 4096, us: m = 12 7.14 / 7.86, m = 10 7.18 / 6.95); from
+// k = 4096 the chunk kernel runs instead (k = 6144, m = 12: 7.03 against
+// 8.26 us), which leaves it k = 2048.
 bool mf_gemv_fits(int64_t m, int64_t k) {
     return m >= 12 && m <= 16 && k % 2048 == 0 && mf_gemv_lds_bytes(m, k / 32) <= kPairsMaxLds;
 }
@@ -858,11 +867,12 @@ hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n,
     const int nb = (int)(k / 32);
     // gemv_q4_0_mfma_chunk_kernel, one chunk: from m = 6 at k = 4096, from m = 5
     // above (m = 5, n = 4096, against the kernels it replaced, us: k = 4096
-    // 5.15 / 4.93, k = 8192 7.91 / 8.13-8.58, k = 12288 10.65 / 11.07-11.76)
-    if ((M >= 6 || (M == 5 && k > 4096)) && k % 4096 == 0) {
+    // 5.15 / 4.93, k = 8192 7.91 / 8.13-8.58, k = 12288 10.65 / 11.07-11.76,
+    // k = 11008 9.65 / 13.07)
+    if ((M >= 6 || (M == 5 && k > 4096)) && q4_0_tiles_take_k(k)) {
         hipLaunchKernelGGL(gemv_q4_0_mfma_chunk_kernel<1>, dim3((unsigned)((n + 15) / 16)), dim3(kMf8Waves * 64),
                            (size_t)kMf8Waves * kQ40ChunkWaveBytes, stream, static_cast<const uint8_t *>(w),
-                           static_cast<const uint8_t *>(a), c, M, (int)n, (int)(k / 4096));
+                           static_cast<const uint8_t *>(a), c, M, (int)n, (int)(k / 256));
         return hipGetLastError();
     }
     if (mf_gemv_fits(M, k)) {
@@ -929,14 +939,15 @@ bool gemv_supported(int type, int64_t m, int64_t k) {
     if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) {
         if (m == 1) return k % 64 == 0;
         if (m <= 8) return k % 256 == 0 || pairs;
-        // m = 9..128 at k % 4096 == 0: gemv_q4_0_mfma_chunk_kernel; otherwise m = 9..16
+        // m = 9..128 from k = 4096: gemv_q4_0_mfma_chunk_kernel; otherwise m = 9..16
         // in the pair-per-lane kernel (or the 8-wave tile, whose slices need more LDS)
-        if (m <= 16 * kMaxGemvChunks && k % 4096 == 0) return true;
+        if (m <= 16 * kMaxGemvChunks && q4_0_tiles_take_k(k)) return true;
         return m <= kPairsMaxM && pairs;
     }
     // q4_K and iq2_xxs (gemv_kquant.hip): m <= 8 for every k % 256 == 0,
-    // m = 9..16 while the staged activations fit in LDS, m = 9..128 at k % 4096 == 0
-    if (m > 8) return (kquant_gemv_staged_fits(m, k) || kquant_gemv_chunked_fits(m, k)) &&
+    // m = 9..16 while the staged activations fit in LDS, m = 9..128 from k = 4096
+    // (q4_K k % 1024 == 0, iq2_xxs k % 2048 == 0)
+    if (m > 8) return (kquant_gemv_staged_fits(m, k) || kquant_gemv_chunked_fits(type, m, k)) &&
                       (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K || type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K);
     return (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K || type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K) && k % 256 == 0;
 }
@@ -976,16 +987,16 @@ hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t
     case 16: return launch_gemv_q4_0_m<16>(w, a, c, n, k, stream);
     default: break;
     }
-    if (!(m >= 17 && m <= 16 * kMaxGemvChunks && k % 4096 == 0)) return hipErrorInvalidValue;
+    if (!(m >= 17 && m <= 16 * kMaxGemvChunks && q4_0_tiles_take_k(k))) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((n + 15) / 16)), block(kMf8Waves * 64);
     const size_t lds = (size_t)kMf8Waves * kQ40ChunkWaveBytes;
-    const int rounds = (int)(k / 4096);
+    const int ng = (int)(k / 256);
     const auto *wp = static_cast<const uint8_t *>(w);
     const auto *ap = static_cast<const uint8_t *>(a);
 #define PFNG_Q40_CHUNK_CASE(C)                                                                                      \
     case C:                                                                                                        \
         hipLaunchKernelGGL(gemv_q4_0_mfma_chunk_kernel<C>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n,     \
-                           rounds);                                                                            \
+                           ng);                                                                                \
         break;
     switch ((m + 15) / 16) {
         PFNG_Q40_CHUNK_CASE(2)

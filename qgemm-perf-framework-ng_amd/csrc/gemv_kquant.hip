@@ -1,4 +1,4 @@
-// GEMV path (m <= 16, and up to 128 at k % 4096 == 0) for the super-block formats
+// GEMV path (m <= 16, and up to 128 from k = 4096) for the super-block formats
 // against q8_K activations:
 // q4_K (llama_reference.cpp:113-132) and iq2_xxs (llama_reference.cpp:148-161,
 // kernels/common/iq2_xxs.h:29-41). One wavefront per weight row, the weight
@@ -8,13 +8,14 @@
 // (m <= 8) take m == 1 and rows too long to stage; for q4_K at m == 1 the
 // 16-row workgroups copy the activation row into LDS first. The
 // *_staged_kernel variants (m = 2..16) stage the rows in LDS once per 16-row
-// workgroup. At k % 4096 == 0 both formats run 16x16 int8 MFMA tiles of 16
-// weight rows with one super-block per wave: iq2_xxs at m = 5..8 and k == 4096
-// with the weight and activation bytes copied together in two halves
-// (gemv_iq2_xxs_mfma_sb_kernel), and from m = 5 (q4_K) or 9 (iq2_xxs) with the
-// weights decoded once per wave and the activation rows streamed in chunks of
-// 16 (*_mfma_chunk_kernel; at k = 4096 r each wave takes r super-blocks, one
-// per round).
+// workgroup. From k = 4096 (q4_K at k % 1024 == 0, iq2_xxs at k % 2048 == 0)
+// both formats run 16x16 int8 MFMA tiles of 16 weight rows with one super-block
+// per wave: iq2_xxs at m = 5..8 and k == 4096 with the weight and activation
+// bytes copied together in two halves (gemv_iq2_xxs_mfma_sb_kernel), and from
+// m = 5 (q4_K; iq2_xxs from 9 at k = 4096, from 5 above) with the weights
+// decoded once per wave and the activation rows streamed in chunks of 16
+// (*_mfma_chunk_kernel; wave w takes super-blocks w, w + 16, ..., one per
+// round).
 //
 // q4_K: four lanes per super-block, lane e owning sub-blocks 2e and 2e+1 (the
 // 32 nibble bytes qs[32e .. 32e+32): low nibbles of sub-block 2e, high of
@@ -994,11 +995,12 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_sb_kernel(c
     }
 }
 
-// k % 4096 == 0 from m = 5 (q4_K) or m = 9 (iq2_xxs) up to m = 16 * kMaxGemvChunks:
-// 16x16 int8 MFMA tiles of 16 weight rows with one super-block per wave and
-// round (round r takes super-block 16 r + wave of every row; the partial sums
-// stay in registers across the k / 4096 rounds), the activation rows taken in
-// C = ceil(m / 16) chunks of 16. Each wave copies its
+// From k = 4096 (kq_tiles_take_k) and m = 5 (q4_K; iq2_xxs m = 9 at k = 4096)
+// up to m = 16 * kMaxGemvChunks: 16x16 int8 MFMA tiles of 16 weight rows with
+// one super-block per wave and round (round r takes super-block 16 r + wave of
+// every row while it exists, so waves can run different numbers of rounds; the
+// partial sums stay in registers), the activation rows taken in C = ceil(m / 16)
+// chunks of 16. Each wave copies its
 // super-block of the tile's 16 weight rows once, decodes them once into
 // registers, and then streams the chunks: chunk c's activation blocks arrive in two halves (H0:
 // copy chunks 0..8 of each row, d and sub-blocks 0..3; H1: chunks 8..18 or
@@ -1024,9 +1026,9 @@ template <int C>
 __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(const uint8_t *__restrict__ w,
                                                                              const uint8_t *__restrict__ a,
                                                                              float *__restrict__ c, int m, int n,
-                                                                             int rounds) {
+                                                                             int ng) {
     static_assert(C >= 1 && C <= kMaxGemvChunks, "at most kMaxGemvChunks chunks of 16 activation rows");
-    const int nsb = kKqMfWaves * rounds;  // k == 4096 * rounds
+    const int nsb = ng;  // k == 256 * ng, ng >= kKqMfWaves and ng % 4 == 0
     const uint32_t kARow = (uint32_t)nsb * kQ8KBytes;
     constexpr int kH = run_copies<16, 11>();  // instructions per half (H1: 11 columns, H0: 9)
     static_assert(run_copies<16, 9>() == kH && run_copies<16, 9>() * 1024 <= 3072, "3 KB per run");
@@ -1044,7 +1046,9 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
         for (int r = 0; r < 4; ++r) acc[ch][r] = 0.0f;
     // round rnd takes the wave's K slice 16 rnd + wave of every row; the next
     // round's copies start once the last round's buffers have been read
-    for (int rnd = 0; rnd < rounds; ++rnd) {
+    // this wave's rounds: its super-blocks wave, wave + 16, ... below nsb
+    const int my_rounds = (nsb - wave + kKqMfWaves - 1) / kKqMfWaves;
+    for (int rnd = 0; rnd < my_rounds; ++rnd) {
         // a lane index the compiler cannot carry across rounds: the per-lane
         // copy offsets and LDS addresses are recomputed per round instead of
         // held in registers for the whole loop
@@ -1139,7 +1143,7 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
     }
 }
 
-// iq2_xxs, m = 9..128 at k % 4096 == 0: as gemv_q4_K_mfma_chunk_kernel, with the
+// iq2_xxs, from k = 4096 at k % 2048 == 0: as gemv_q4_K_mfma_chunk_kernel, with the
 // weight decode of gemv_iq2_xxs_mfma_sb_kernel done once per wave (5 weight
 // columns per row, H1 = activation chunks 8..16) and the grid and sign tables
 // copied by waves 0..2 before everything else.
@@ -1151,9 +1155,9 @@ template <int C>
 __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kernel(const uint8_t *__restrict__ w,
                                                                                 const uint8_t *__restrict__ a,
                                                                                 float *__restrict__ c, int m, int n,
-                                                                                int rounds) {
+                                                                                int ng) {
     static_assert(C >= 1 && C <= kMaxGemvChunks, "at most kMaxGemvChunks chunks of 16 activation rows");
-    const int nsb = kKqMfWaves * rounds;  // k == 4096 * rounds
+    const int nsb = ng;  // k == 256 * ng, ng >= kKqMfWaves and ng % 8 == 0
     const uint32_t kARow = (uint32_t)nsb * kQ8KBytes;
     constexpr int kH = run_copies<16, 9>();
     constexpr int kW = run_copies<16, 5>();
@@ -1181,7 +1185,9 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
         for (int r = 0; r < 4; ++r) acc[ch][r] = 0.0f;
     // round rnd takes the wave's K slice 16 rnd + wave of every row; the next
     // round's copies start once the last round's buffers have been read
-    for (int rnd = 0; rnd < rounds; ++rnd) {
+    // this wave's rounds: its super-blocks wave, wave + 16, ... below nsb
+    const int my_rounds = (nsb - wave + kKqMfWaves - 1) / kKqMfWaves;
+    for (int rnd = 0; rnd < my_rounds; ++rnd) {
         // a lane index the compiler cannot carry across rounds: the per-lane
         // copy offsets and LDS addresses are recomputed per round instead of
         // held in registers for the whole loop
@@ -1197,9 +1203,9 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
         copy_h0(0);
         copy_h1(0);
         // the table piece has landed once at most (weights + H0 + H1) loads are
-        // outstanding (in later rounds no other load is: the wait passes, and the
-        // barrier keeps the waits in one straight line of code)
-        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kW + 2 * kH) : "memory");
+        // outstanding; round 0 only, which every wave runs (waves can differ in
+        // their number of rounds, and the reduction's barrier follows the loop)
+        if (rnd == 0) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kW + 2 * kH) : "memory");
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // weights and H0(0)
         // the weight row's decode, once: group q of every sub-block, its scale, d
         const uint8_t *wr = wl + li * 80;  // weight block byte b at copy byte o2 + b
@@ -1271,6 +1277,16 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
     }
 }
 
+// k the chunked MFMA tile kernels take: at least one super-block per wave, and
+// every row's blocks at the same offset from a 16-byte boundary with the last
+// block's copy ending at the row's end (q4_K: k % 1024 == 0, the q8_K blocks'
+// offset set by the block index mod 4; iq2_xxs: k % 2048 == 0, its 66-byte
+// weight blocks' offset by the index mod 8)
+bool kq_tiles_take_k(int type, int64_t k) {
+    const int64_t unit = type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K ? 1024 : 2048;
+    return k % unit == 0 && k >= 256 * kKqMfWaves;
+}
+
 template <int M>
 hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int64_t n, int64_t k,
                           hipStream_t stream) {
@@ -1280,15 +1296,15 @@ hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int6
     if constexpr (M >= 5) {
         // one super-block per wave (and round), from m = 5 (4096 x 4096 against
         // the staged kernel, us: iq2_xxs m = 4 5.23 / 5.08, m = 5 5.34 / 5.91,
-        // m = 8 5.56 / 6.58): one chunk of the chunked kernel at k % 4096 == 0
-        // for q4_K and for iq2_xxs (at k = 4096 from m = 9, m = 5..8 taking the
-        // two-half-copy kernel; n = 4096, k = 8192 against the staged kernel,
-        // us: q4_K m = 8 8.06 / 11.12, m = 12 8.67 / 14.64; iq2_xxs m = 12
-        // 8.87 / 16.72)
+        // m = 8 5.56 / 6.58): one chunk of the chunked kernel for q4_K and for
+        // iq2_xxs (at k = 4096 from m = 9, m = 5..8 taking the two-half-copy
+        // kernel; n = 4096 against the staged kernel, us: k = 8192 q4_K m = 8
+        // 8.06 / 11.12, m = 12 8.67 / 14.64, iq2_xxs m = 12 8.87 / 16.72;
+        // k = 14336 q4_K m = 5 11.15 / 15.03, iq2_xxs m = 8 12.54 / 18.98)
         const dim3 tiles((unsigned)((n + 15) / 16)), block(kKqMfWaves * 64);
-        if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && k % 4096 == 0 && (M >= 9 || k > 4096)) {
+        if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && kq_tiles_take_k(type, k) && (M >= 9 || k > 4096)) {
             hipLaunchKernelGGL(gemv_iq2_xxs_mfma_chunk_kernel<1>, tiles, block, (size_t)iq2_chunk_lds_bytes(), stream,
-                               wp, ap, c, M, (int)n, (int)(k / 4096));
+                               wp, ap, c, M, (int)n, (int)(k / 256));
             return hipGetLastError();
         }
         if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && k == 4096) {
@@ -1296,9 +1312,9 @@ hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int6
                                ap, c, (int)n);
             return hipGetLastError();
         }
-        if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K && k % 4096 == 0) {
+        if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K && kq_tiles_take_k(type, k)) {
             hipLaunchKernelGGL(gemv_q4_K_mfma_chunk_kernel<1>, tiles, block, (size_t)q4k_chunk_lds_bytes(), stream, wp,
-                               ap, c, M, (int)n, (int)(k / 4096));
+                               ap, c, M, (int)n, (int)(k / 256));
             return hipGetLastError();
         }
     }
@@ -1372,8 +1388,8 @@ bool kquant_gemv_staged_fits(int64_t m, int64_t k) {
     return m >= 2 && m <= 16 && k % 256 == 0 && kq_staged_lds_bytes(m, k / 256) <= 160 * 1024;
 }
 
-bool kquant_gemv_chunked_fits(int64_t m, int64_t k) {
-    return m >= 9 && m <= 16 * kMaxGemvChunks && k % 4096 == 0 && k > 0;
+bool kquant_gemv_chunked_fits(int type, int64_t m, int64_t k) {
+    return m >= 9 && m <= 16 * kMaxGemvChunks && kq_tiles_take_k(type, k);
 }
 
 hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
@@ -1399,21 +1415,21 @@ hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, 
     case 16: return launch_kq_gemv<16>(type, w, a, c, n, k, stream);
     default: break;
     }
-    if (!kquant_gemv_chunked_fits(m, k)) return hipErrorInvalidValue;
+    if (!kquant_gemv_chunked_fits(type, m, k)) return hipErrorInvalidValue;
     const auto *wp = static_cast<const uint8_t *>(w);
     const auto *ap = static_cast<const uint8_t *>(a);
     const dim3 grid((unsigned)((n + 15) / 16)), block(kKqMfWaves * 64);
     const bool q4k = type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K;
     const size_t lds = q4k ? (size_t)q4k_chunk_lds_bytes() : (size_t)iq2_chunk_lds_bytes();
-    const int rounds = (int)(k / 4096);
+    const int ng = (int)(k / 256);
 #define PFNG_CHUNK_CASE(C)                                                                                      \
     case C:                                                                                                    \
         if (q4k)                                                                                               \
             hipLaunchKernelGGL(gemv_q4_K_mfma_chunk_kernel<C>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n, \
-                               rounds);                                                                        \
+                               ng);                                                                            \
         else                                                                                                   \
             hipLaunchKernelGGL(gemv_iq2_xxs_mfma_chunk_kernel<C>, grid, block, lds, stream, wp, ap, c, (int)m,     \
-                               (int)n, rounds);                                                                \
+                               (int)n, ng);                                                                    \
         return hipGetLastError();
     switch ((m + 15) / 16) {
         PFNG_CHUNK_CASE(2)

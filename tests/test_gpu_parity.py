@@ -177,13 +177,14 @@ def test_gemv_q4_0(hip, torch_gpu, oracle, m, n, k):
     rounds of 16 KB up to 64 KB, k = 20480 taking two rounds, a dword tail at
     k = 320 and 64), m = 2..16 with the activations staged in LDS
     (m * (k / 64) * 76 + 16 <= 160 KB), m = 2..8 beyond that (groups of 8
-    blocks per lane); at k % 4096 == 0 from m = 6 the one-chunk 16x16 MFMA tile
-    kernel over k / 4096 rounds (k = 4096 to 65536: 1 to 16 rounds, 100 and 33
-    columns partial tiles), with 8 waves from m = 12 at k = 6144 (37 columns: a
-    partial tile) and 2048."""
+    blocks per lane); from k = 4096 at k % 256 == 0 the one-chunk 16x16 MFMA
+    tile kernel, from m = 6 at k = 4096 and m = 5 above, over one to 16 rounds
+    (k = 6144 and 7680: waves with different numbers of rounds; 100, 33, 37 and
+    129 columns partial tiles), with 8 waves from m = 12 at k = 2048."""
     torch = torch_gpu
-    if m > 8 and k % 4096 and m * (k // 64) * 76 + 16 > 160 * 1024:
-        pytest.skip("m > 8 takes the GEMV off k % 4096 == 0 only while the staged activations fit in LDS")
+    tiles = k % 256 == 0 and k >= 4096
+    if m > 8 and not tiles and m * (k // 64) * 76 + 16 > 160 * 1024:
+        pytest.skip("m > 8 takes the GEMV below the tiles' k only while the staged activations fit in LDS")
     say(f"gemv q4_0 m={m} n={n} k={k}")
     act, w = oracle.create_input(0, m, n, k, seed=m * 31 + n)
     aq = oracle.quantize_q8_0(act)
@@ -459,12 +460,14 @@ def test_gemv_kquant(hip, torch_gpu, oracle, qtype, m, n, k):
     (k <= 57344; k = 65536 takes the global-read kernel), iq2_xxs reads it from
     global memory; m = 2..16 stage the rows in LDS while m * (k / 256) * 320 +
     3072 bytes fit 160 KB (at k = 20480 only m <= 6 do, at k = 65536 none; the
-    others up to m = 8 take the global-read kernel). At k % 4096 == 0 the
-    one-chunk MFMA tile kernel takes q4_K from m = 5 and iq2_xxs from m = 9
-    (iq2_xxs m = 5..8 at k = 4096: the two-half-copy tile), over k / 4096
-    rounds (16 at k = 65536)."""
-    if m > 8 and k % 4096 and m * (k // 256) * 320 + 3072 > 160 * 1024:
-        pytest.skip("m > 8 takes the GEMV off k % 4096 == 0 only while the staged activations fit in LDS")
+    others up to m = 8 take the global-read kernel). From k = 4096 (q4_K at
+    k % 1024 == 0, iq2_xxs at k % 2048 == 0) the one-chunk MFMA tile kernel
+    takes q4_K from m = 5 and iq2_xxs from m = 9 at k = 4096 (m = 5..8 there:
+    the two-half-copy tile) and from m = 5 above, one super-block per wave and
+    round (16 rounds at k = 65536)."""
+    tiles = k >= 4096 and k % (1024 if qtype == 1 else 2048) == 0
+    if m > 8 and not tiles and m * (k // 256) * 320 + 3072 > 160 * 1024:
+        pytest.skip("m > 8 takes the GEMV below the tiles' k only while the staged activations fit in LDS")
     torch = torch_gpu
     say(f"gemv type={qtype} m={m} n={n} k={k}")
     act, w = oracle.create_input(qtype, m, n, k, seed=m * 31 + n + qtype)
@@ -513,15 +516,19 @@ def test_gemv_kquant_one_superblock_per_wave(hip, torch_gpu, oracle, qtype, m, n
     check_close(oracle, qtype, got, wr, ax, m, n, k, label=f"gemv sb random bytes type={qtype} m={m} n={n}")
 
 
-@pytest.mark.parametrize("qtype", [0, 1, 2])
 @pytest.mark.parametrize("m", [5, 6, 9, 16, 17, 33, 64, 128])
-@pytest.mark.parametrize("n,k", [(512, 8192), (37, 12288)])
+@pytest.mark.parametrize("qtype,n,k", [(0, 512, 8192), (0, 37, 12288), (0, 256, 14336), (0, 37, 11008), (0, 64, 4352),
+                                       (1, 512, 8192), (1, 37, 12288), (1, 256, 14336), (1, 37, 5120),
+                                       (2, 512, 8192), (2, 37, 12288), (2, 256, 14336), (2, 37, 6144)])
 def test_gemv_tiles_several_rounds(hip, torch_gpu, oracle, qtype, m, n, k):
-    """k = 8192 and 12288: the one-chunk (m <= 16) and chunked MFMA tile GEMVs
-    run k / 4096 rounds of the 16 waves' K slices, the partial sums carried
-    across rounds in registers (from m = 5 above k = 4096). The automatic path
-    takes the GEMV for every case; the generator's inputs, then random weight
-    bytes against activations at the int8 limits, 37 columns a partial tile."""
+    """Above k = 4096: the one-chunk (m <= 16) and chunked MFMA tile GEMVs give
+    wave w the K groups w, w + 16, ... (q4_0: 8 blocks, K-quants: one
+    super-block), one per round, the partial sums carried across rounds in
+    registers; at k = 4352, 5120, 6144, 11008 and 14336 the waves run different
+    numbers of rounds (k = 4352: wave 0 two, the others one). From m = 5 the
+    automatic path takes the GEMV for every case; the generator's inputs, then
+    random weight bytes against activations at the int8 limits, 37 columns a
+    partial tile."""
     torch = torch_gpu
     say(f"gemv rounds type={qtype} m={m} n={n} k={k}")
     assert hip.auto_path(qtype, m, n, k) == hip.PATH_GEMV
