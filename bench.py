@@ -383,11 +383,12 @@ def main():
                                    "weight copies", qt, 1, 4096, 4096, side, max(side // 10, 32), samples, variant,
                                    f"gemv_{name}_kernel<1>", copies=32))
         # at K = 4096 M = 8 and 16 run the 16x16 MFMA tile GEMVs: one chunk of 16
-        # activation rows of the chunked kernels (q4_0 from M = 6, q4_K from M = 5,
-        # iq2_xxs from M = 9), iq2_xxs at M = 5..8 the two-half-copy kernel
-        kernels = {0: {8: "gemv_q4_0_mfma_chunk_kernel<1>", 16: "gemv_q4_0_mfma_chunk_kernel<1>"},
-                   1: {8: "gemv_q4_K_mfma_chunk_kernel<1>", 16: "gemv_q4_K_mfma_chunk_kernel<1>"},
-                   2: {8: "gemv_iq2_xxs_mfma_sb_kernel<8>", 16: "gemv_iq2_xxs_mfma_chunk_kernel<1>"}}
+        # activation rows of the chunked kernels in their one-round form (16
+        # groups; q4_0 from M = 6, q4_K from M = 5, iq2_xxs from M = 9), iq2_xxs
+        # at M = 5..8 the two-half-copy kernel
+        kernels = {0: {8: "gemv_q4_0_mfma_chunk_kernel<1, 16>", 16: "gemv_q4_0_mfma_chunk_kernel<1, 16>"},
+                   1: {8: "gemv_q4_K_mfma_chunk_kernel<1, 16>", 16: "gemv_q4_K_mfma_chunk_kernel<1, 16>"},
+                   2: {8: "gemv_iq2_xxs_mfma_sb_kernel<8>", 16: "gemv_iq2_xxs_mfma_chunk_kernel<1, 16>"}}
         for qt, name, variant in ((0, "q4_0", ref), (1, "q4_K", ref), (2, "iq2_xxs", base)):
             act_t = "q8_0" if qt == 0 else "q8_K"
             for dm in (8, 16):

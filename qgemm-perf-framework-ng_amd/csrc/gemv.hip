@@ -621,13 +621,16 @@ constexpr int kMf8Waves = 16;
 // is faster (m = 5 4.93 / 5.15).
 constexpr int kQ40ChunkWaveBytes = 9 * 1024;  // weight run, H0, H1: 3 KB each
 
-template <int C>
+template <int C, int kG>
 __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(const uint8_t *__restrict__ w,
                                                                               const uint8_t *__restrict__ a,
                                                                               float *__restrict__ c, int m, int n,
-                                                                              int ng) {
+                                                                              int groups) {
     static_assert(C >= 1 && C <= kMaxGemvChunks, "at most kMaxGemvChunks chunks of 16 activation rows");
-    const int nb = kMf8Blocks * ng;  // k == 256 * ng, ng >= kMf8Waves
+    // 256-element groups of a row (k == 256 ng, ng >= kMf8Waves): kG when it is
+    // fixed at compile time (k = 4096: one round, constant strides), else groups
+    const int ng = kG > 0 ? kG : groups;
+    const int nb = kMf8Blocks * ng;
     const uint32_t kARow = (uint32_t)nb * 34;
     constexpr int kH = run_copies<16, 9>();
     static_assert(kH * 1024 <= 3072, "3 KB per run");
@@ -646,14 +649,18 @@ __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(co
     // round's copies start once the last round's buffers have been read
     // this wave's rounds: its 8-block groups wave, wave + 16, ... below ng
     const int my_rounds = (ng - wave + kMf8Waves - 1) / kMf8Waves;
+#pragma clang loop unroll(disable)
     for (int rnd = 0; rnd < my_rounds; ++rnd) {
         // a lane index the compiler cannot carry across rounds: the per-lane
         // copy offsets and LDS addresses are recomputed per round instead of
-        // held in registers for the whole loop
+        // held in registers for the whole loop (one round with kG: no need)
         int cl = lane;
-        asm volatile("" : "+v"(cl));
+        if constexpr (kG == 0) asm volatile("" : "+v"(cl));
         const int li = cl & 15, q = cl >> 4;
-        if (rnd > 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        // the last round's LDS reads are done before its buffers are refilled (in
+        // round 0 this covers the kernel arguments' scalar loads, needed anyway;
+        // a wait in round 0 only would make the compiler peel that round)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int kb0 = (kMf8Waves * rnd + wave) * kMf8Blocks;  // the wave's first block
         const uint8_t *asrc = a + kb0 * 34;  // the wave's slice of activation row 0
         auto copy_h0 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, cl); };
@@ -738,6 +745,18 @@ __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(co
         const int row = 16 * (g / 4) + 4 * q + g % 4;
         if (col < n && row < m) c[(size_t)row * n + col] = s * 0.0625f;
     }
+}
+
+// One launch of gemv_q4_0_mfma_chunk_kernel with C chunks over ng 256-element
+// groups, the k = 4096 form (16 groups, one round) where it applies.
+template <int C>
+void launch_q4_0_chunk(const uint8_t *w, const uint8_t *a, float *c, int m, int n, int ng, hipStream_t stream) {
+    const dim3 grid((unsigned)((n + 15) / 16)), block(kMf8Waves * 64);
+    const size_t lds = (size_t)kMf8Waves * kQ40ChunkWaveBytes;
+    if (ng == kMf8Waves)
+        hipLaunchKernelGGL((gemv_q4_0_mfma_chunk_kernel<C, kMf8Waves>), grid, block, lds, stream, w, a, c, m, n, ng);
+    else
+        hipLaunchKernelGGL((gemv_q4_0_mfma_chunk_kernel<C, 0>), grid, block, lds, stream, w, a, c, m, n, ng);
 }
 
 // Fused activation quantization + GEMV (m <= 2): each workgroup quantizes the
@@ -870,9 +889,8 @@ hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n,
     // 5.15 / 4.93, k = 8192 7.91 / 8.13-8.58, k = 12288 10.65 / 11.07-11.76,
     // k = 11008 9.65 / 13.07)
     if ((M >= 6 || (M == 5 && k > 4096)) && q4_0_tiles_take_k(k)) {
-        hipLaunchKernelGGL(gemv_q4_0_mfma_chunk_kernel<1>, dim3((unsigned)((n + 15) / 16)), dim3(kMf8Waves * 64),
-                           (size_t)kMf8Waves * kQ40ChunkWaveBytes, stream, static_cast<const uint8_t *>(w),
-                           static_cast<const uint8_t *>(a), c, M, (int)n, (int)(k / 256));
+        launch_q4_0_chunk<1>(static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(a), c, M, (int)n,
+                             (int)(k / 256), stream);
         return hipGetLastError();
     }
     if (mf_gemv_fits(M, k)) {
@@ -988,15 +1006,12 @@ hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t
     default: break;
     }
     if (!(m >= 17 && m <= 16 * kMaxGemvChunks && q4_0_tiles_take_k(k))) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((n + 15) / 16)), block(kMf8Waves * 64);
-    const size_t lds = (size_t)kMf8Waves * kQ40ChunkWaveBytes;
     const int ng = (int)(k / 256);
     const auto *wp = static_cast<const uint8_t *>(w);
     const auto *ap = static_cast<const uint8_t *>(a);
 #define PFNG_Q40_CHUNK_CASE(C)                                                                                      \
     case C:                                                                                                        \
-        hipLaunchKernelGGL(gemv_q4_0_mfma_chunk_kernel<C>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n,     \
-                           ng);                                                                                \
+        launch_q4_0_chunk<C>(wp, ap, c, (int)m, (int)n, ng, stream);                                               \
         break;
     switch ((m + 15) / 16) {
         PFNG_Q40_CHUNK_CASE(2)

@@ -1022,13 +1022,15 @@ constexpr int kChunkWaveBytes = 9 * 1024;  // per wave: weight run, H0, H1 (3 KB
 
 __host__ __device__ constexpr int q4k_chunk_lds_bytes() { return kKqMfWaves * kChunkWaveBytes; }
 
-template <int C>
+template <int C, int kG>
 __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(const uint8_t *__restrict__ w,
                                                                              const uint8_t *__restrict__ a,
                                                                              float *__restrict__ c, int m, int n,
-                                                                             int ng) {
+                                                                             int groups) {
     static_assert(C >= 1 && C <= kMaxGemvChunks, "at most kMaxGemvChunks chunks of 16 activation rows");
-    const int nsb = ng;  // k == 256 * ng, ng >= kKqMfWaves and ng % 4 == 0
+    // super-blocks of a row (k == 256 nsb, nsb >= kKqMfWaves and nsb % 4 == 0): kG when it
+    // is fixed at compile time (k = 4096: one round, constant strides), else groups
+    const int nsb = kG > 0 ? kG : groups;
     const uint32_t kARow = (uint32_t)nsb * kQ8KBytes;
     constexpr int kH = run_copies<16, 11>();  // instructions per half (H1: 11 columns, H0: 9)
     static_assert(run_copies<16, 9>() == kH && run_copies<16, 9>() * 1024 <= 3072, "3 KB per run");
@@ -1048,14 +1050,18 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
     // round's copies start once the last round's buffers have been read
     // this wave's rounds: its super-blocks wave, wave + 16, ... below nsb
     const int my_rounds = (nsb - wave + kKqMfWaves - 1) / kKqMfWaves;
+#pragma clang loop unroll(disable)
     for (int rnd = 0; rnd < my_rounds; ++rnd) {
         // a lane index the compiler cannot carry across rounds: the per-lane
         // copy offsets and LDS addresses are recomputed per round instead of
-        // held in registers for the whole loop
+        // held in registers for the whole loop (one round with kG: no need)
         int cl = lane;
-        asm volatile("" : "+v"(cl));
+        if constexpr (kG == 0) asm volatile("" : "+v"(cl));
         const int li = cl & 15, q = cl >> 4;
-        if (rnd > 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        // the last round's LDS reads are done before its buffers are refilled (in
+        // round 0 this covers the kernel arguments' scalar loads, needed anyway;
+        // a wait in round 0 only would make the compiler peel that round)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int sb = kKqMfWaves * rnd + wave;
         const uint8_t *asrc = a + sb * kQ8KBytes - o;  // copy start of the wave's block in activation row 0
         auto copy_h0 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, cl); };
@@ -1151,13 +1157,15 @@ constexpr int kIq2ChunkWaveBytes = 8 * 1024;  // weight run 2 KB, H0 and H1 3 KB
 
 __host__ __device__ constexpr int iq2_chunk_lds_bytes() { return kIq2TableBytes + kKqMfWaves * kIq2ChunkWaveBytes; }
 
-template <int C>
+template <int C, int kG>
 __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kernel(const uint8_t *__restrict__ w,
                                                                                 const uint8_t *__restrict__ a,
                                                                                 float *__restrict__ c, int m, int n,
-                                                                                int ng) {
+                                                                                int groups) {
     static_assert(C >= 1 && C <= kMaxGemvChunks, "at most kMaxGemvChunks chunks of 16 activation rows");
-    const int nsb = ng;  // k == 256 * ng, ng >= kKqMfWaves and ng % 8 == 0
+    // super-blocks of a row (k == 256 nsb, nsb >= kKqMfWaves and nsb % 8 == 0): kG when it
+    // is fixed at compile time (k = 4096: one round, constant strides), else groups
+    const int nsb = kG > 0 ? kG : groups;
     const uint32_t kARow = (uint32_t)nsb * kQ8KBytes;
     constexpr int kH = run_copies<16, 9>();
     constexpr int kW = run_copies<16, 5>();
@@ -1187,14 +1195,18 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
     // round's copies start once the last round's buffers have been read
     // this wave's rounds: its super-blocks wave, wave + 16, ... below nsb
     const int my_rounds = (nsb - wave + kKqMfWaves - 1) / kKqMfWaves;
+#pragma clang loop unroll(disable)
     for (int rnd = 0; rnd < my_rounds; ++rnd) {
         // a lane index the compiler cannot carry across rounds: the per-lane
         // copy offsets and LDS addresses are recomputed per round instead of
-        // held in registers for the whole loop
+        // held in registers for the whole loop (one round with kG: no need)
         int cl = lane;
-        asm volatile("" : "+v"(cl));
+        if constexpr (kG == 0) asm volatile("" : "+v"(cl));
         const int li = cl & 15, q = cl >> 4;
-        if (rnd > 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        // the last round's LDS reads are done before its buffers are refilled (in
+        // round 0 this covers the kernel arguments' scalar loads, needed anyway;
+        // a wait in round 0 only would make the compiler peel that round)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int sb = kKqMfWaves * rnd + wave;
         const uint8_t *asrc = a + sb * kQ8KBytes - o;
         auto copy_h0 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, cl); };
@@ -1277,6 +1289,24 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
     }
 }
 
+// One launch of the q4_K or iq2_xxs chunk kernel with C chunks over nsb
+// super-blocks, the k = 4096 form (16 super-blocks, one round) where it applies.
+template <int C>
+void launch_kq_chunk(bool q4k, const uint8_t *w, const uint8_t *a, float *c, int m, int n, int nsb,
+                     hipStream_t stream) {
+    const dim3 grid((unsigned)((n + 15) / 16)), block(kKqMfWaves * 64);
+    const size_t lds = q4k ? (size_t)q4k_chunk_lds_bytes() : (size_t)iq2_chunk_lds_bytes();
+    if (q4k && nsb == kKqMfWaves)
+        hipLaunchKernelGGL((gemv_q4_K_mfma_chunk_kernel<C, kKqMfWaves>), grid, block, lds, stream, w, a, c, m, n, nsb);
+    else if (q4k)
+        hipLaunchKernelGGL((gemv_q4_K_mfma_chunk_kernel<C, 0>), grid, block, lds, stream, w, a, c, m, n, nsb);
+    else if (nsb == kKqMfWaves)
+        hipLaunchKernelGGL((gemv_iq2_xxs_mfma_chunk_kernel<C, kKqMfWaves>), grid, block, lds, stream, w, a, c, m, n,
+                           nsb);
+    else
+        hipLaunchKernelGGL((gemv_iq2_xxs_mfma_chunk_kernel<C, 0>), grid, block, lds, stream, w, a, c, m, n, nsb);
+}
+
 // k the chunked MFMA tile kernels take: at least one super-block per wave, and
 // every row's blocks at the same offset from a 16-byte boundary with the last
 // block's copy ending at the row's end (q4_K: k % 1024 == 0, the q8_K blocks'
@@ -1303,8 +1333,7 @@ hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int6
         // k = 14336 q4_K m = 5 11.15 / 15.03, iq2_xxs m = 8 12.54 / 18.98)
         const dim3 tiles((unsigned)((n + 15) / 16)), block(kKqMfWaves * 64);
         if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && kq_tiles_take_k(type, k) && (M >= 9 || k > 4096)) {
-            hipLaunchKernelGGL(gemv_iq2_xxs_mfma_chunk_kernel<1>, tiles, block, (size_t)iq2_chunk_lds_bytes(), stream,
-                               wp, ap, c, M, (int)n, (int)(k / 256));
+            launch_kq_chunk<1>(false, wp, ap, c, M, (int)n, (int)nsb, stream);
             return hipGetLastError();
         }
         if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && k == 4096) {
@@ -1313,8 +1342,7 @@ hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int6
             return hipGetLastError();
         }
         if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K && kq_tiles_take_k(type, k)) {
-            hipLaunchKernelGGL(gemv_q4_K_mfma_chunk_kernel<1>, tiles, block, (size_t)q4k_chunk_lds_bytes(), stream, wp,
-                               ap, c, M, (int)n, (int)(k / 256));
+            launch_kq_chunk<1>(true, wp, ap, c, M, (int)n, (int)nsb, stream);
             return hipGetLastError();
         }
     }
@@ -1418,18 +1446,11 @@ hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, 
     if (!kquant_gemv_chunked_fits(type, m, k)) return hipErrorInvalidValue;
     const auto *wp = static_cast<const uint8_t *>(w);
     const auto *ap = static_cast<const uint8_t *>(a);
-    const dim3 grid((unsigned)((n + 15) / 16)), block(kKqMfWaves * 64);
     const bool q4k = type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K;
-    const size_t lds = q4k ? (size_t)q4k_chunk_lds_bytes() : (size_t)iq2_chunk_lds_bytes();
     const int ng = (int)(k / 256);
 #define PFNG_CHUNK_CASE(C)                                                                                      \
     case C:                                                                                                    \
-        if (q4k)                                                                                               \
-            hipLaunchKernelGGL(gemv_q4_K_mfma_chunk_kernel<C>, grid, block, lds, stream, wp, ap, c, (int)m, (int)n, \
-                               ng);                                                                            \
-        else                                                                                                   \
-            hipLaunchKernelGGL(gemv_iq2_xxs_mfma_chunk_kernel<C>, grid, block, lds, stream, wp, ap, c, (int)m,     \
-                               (int)n, ng);                                                                    \
+        launch_kq_chunk<C>(q4k, wp, ap, c, (int)m, (int)n, ng, stream);                                        \
         return hipGetLastError();
     switch ((m + 15) / 16) {
         PFNG_CHUNK_CASE(2)

@@ -238,9 +238,12 @@ def test_chunk_wait_checker():
                                                       ("gemv_kquant.hip", "gemv_q4_K_mfma_chunk_kernel", None),
                                                       ("gemv_kquant.hip", "gemv_iq2_xxs_mfma_chunk_kernel", 8)])
 @pytest.mark.parametrize("chunks", [1, 2, 3, 4, 8])
-def test_chunked_gemv_waits(source, kernel, table_wait, chunks):
+@pytest.mark.parametrize("groups", [0, 16])
+def test_chunked_gemv_waits(source, kernel, table_wait, chunks, groups):
+    """Both forms: the group count read at run time (0, any number of rounds) and
+    fixed at 16 (k = 4096, one round)."""
     out = os.path.join(PKG_DIR, "_build", source + ".s")
     subprocess.run(["make", "-s", "-C", PKG_DIR, out], check=True, capture_output=True, timeout=600)
     with open(out) as f:
         asm = f.read()
-    check_chunk_waits(_kernel_lines(asm, f"{kernel}ILi{chunks}E"), chunks, table_wait)
+    check_chunk_waits(_kernel_lines(asm, f"{kernel}ILi{chunks}ELi{groups}E"), chunks, table_wait)
