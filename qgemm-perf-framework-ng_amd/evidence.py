@@ -281,8 +281,9 @@ def bench_stats(args):
         base, _, tag = kname.partition("<")
         tag = tag.rstrip(">")
         # K-quant tiles are tagged by type; GEMV instantiations by their row count
-        tag = {"q4_K": "(Kq)0", "iq2_xxs": "(Kq)1"}.get(tag, f"<{tag}>" if tag.isdigit() else "")
-        match = [r for r in stats if base in r["Name"] and tag in short(r["Name"])]
+        # (the first template argument, more may follow)
+        tags = {"q4_K": ["(Kq)0"], "iq2_xxs": ["(Kq)1"]}.get(tag, [f"<{tag}>", f"<{tag},"] if tag.isdigit() else [""])
+        match = [r for r in stats if base in r["Name"] and any(t in short(r["Name"]) for t in tags)]
         # one line per instantiation: the plan picks the tile configuration by shape
         for r in match or [None]:
             prof = (f"{float(r['AverageNs']) / 1e3:.3f} / {median_us(r['Name'])} "
