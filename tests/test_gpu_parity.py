@@ -633,6 +633,26 @@ def test_compute_fused_kquant_gemv(hip, torch_gpu, oracle, qtype, m, n, k):
     assert torch.equal(fused, unfused)
 
 
+@pytest.mark.parametrize("qtype,m,n,k", [(0, 24, 96, 14336), (0, 7, 64, 11008), (1, 40, 64, 14336), (1, 9, 50, 5120),
+                                         (2, 12, 80, 14336), (2, 70, 40, 8192)])
+def test_compute_tiles_several_rounds(hip, torch_gpu, oracle, qtype, m, n, k):
+    """pfng_hip_compute where the product is an MFMA tile GEMV over several
+    rounds (quantize first, m >= 3): within the bound of the oracle's compute,
+    and equal bit for bit to quantize + the GEMV called directly."""
+    torch = torch_gpu
+    say(f"compute rounds type={qtype} m={m} n={n} k={k}")
+    assert hip.auto_path(qtype, m, n, k) == hip.PATH_GEMV
+    act, w = oracle.create_input(qtype, m, n, k, seed=m * 3 + n + k)
+    wt, at = dev(torch, w), dev(torch, act)
+    got = hip.compute(qtype, at, wt, n)
+    quantize = hip.quantize_q8_0 if qtype == 0 else hip.quantize_q8_K
+    direct = hip.mul_mat(qtype, wt, quantize(at), m, n, k, path=hip.PATH_GEMV)
+    torch.cuda.synchronize()
+    aq = oracle.quantize_activation(qtype, act)
+    check_close(oracle, qtype, got.cpu().numpy(), w, aq, m, n, k, label=f"compute rounds type={qtype} m={m} k={k}")
+    assert torch.equal(got, direct)
+
+
 def test_wrappers_reject_short_or_strided_buffers(hip, torch_gpu):
     """The C-ABI takes bare pointers; the Python wrappers check sizes, layout
     and device first and raise before anything is launched."""
