@@ -325,6 +325,11 @@ __device__ __forceinline__ void run_copy(const uint8_t *src, uint32_t rstride, i
 // chunks of 16 activation rows the chunked MFMA tile GEMVs take (m <= 128)
 constexpr int kMaxGemvChunks = 8;
 
+// Largest m the chunked MFMA tile GEMVs take at this k: every chunk count from
+// k = 2048; below it, where the MFMA GEMM tiles are cheaper past four chunks
+// (q4_0 k = 1024, m = 128: 10.44 us against 7.24), m = 64.
+inline int gemv_tiles_max_m(int64_t k) { return k >= 2048 ? 16 * kMaxGemvChunks : 64; }
+
 // instructions (1-KB pieces) of a run_copy run
 template <int kRows, int kCols>
 __host__ __device__ constexpr int run_copies() {

@@ -1,4 +1,4 @@
-// q4_0 x q8_0 GEMV path (m <= 16, and up to 128 from k = 4096 at k % 256 == 0) for gfx950: the
+// q4_0 x q8_0 GEMV path (m <= 16, and up to 64 or 128 at k % 256 == 0) for gfx950: the
 // weight stream is the roofline. Six kernels, picked in launch_gemv /
 // launch_fused_gemv:
 //
@@ -16,17 +16,14 @@
 //                              bytes, then the 8 fp16 scales).
 //   gemv_q4_0_fused_kernel     pfng_hip_compute for m <= 2: quantizes the fp32
 //                              activation rows into LDS, then as the m1 kernel.
-//   gemv_q4_0_mfma_kernel      m = 12..16 at k = 2048: 16x16 int8 MFMA tiles
-//                              of 16 weight rows, K split over the
-//                              workgroup's 8 waves, each wave's slices copied
-//                              into LDS by direct loads.
-//   gemv_q4_0_mfma_chunk_kernel k % 256 == 0 from k = 4096, from m = 6 (m = 5
-//                              above k = 4096) up to m = 128: the same tile
-//                              with 8 blocks per wave and round (wave w takes
-//                              the 8-block groups w, w + 16, ...), each round's
-//                              weights widened into registers once and the
-//                              activation rows streamed through LDS in chunks
-//                              of 16.
+//   gemv_q4_0_mfma_chunk_kernel k % 256 == 0 from k = 512, from m = 3..6 (by
+//                              k) up to m = 64 (k < 2048) or 128: 16x16 int8
+//                              MFMA tiles of 16 weight rows, K split over the
+//                              workgroup's 16 waves in 8-block groups (wave w
+//                              takes groups w, w + 16, ..., one per round),
+//                              each round's weights widened into registers
+//                              once and the activation rows streamed through
+//                              LDS in chunks of 16.
 //
 // Every lane issues all the loads of a step before any arithmetic, so the
 // weight stream of the grid is in flight at once; weight rows are clamped so
@@ -482,125 +479,18 @@ __global__ __launch_bounds__(kPairsThreads) void gemv_q4_0_pairs_kernel(const ui
     }
 }
 
-// m = 12..16 at k = 2048 (8 waves; from k = 4096 the chunk kernel below
-// runs): 16x16 int8 MFMA tiles. A workgroup takes 16 weight rows (output
-// columns) and all m activation rows; its WV waves split K into equal slices
-// of a multiple of 8 blocks, and each wave copies just its own slice of the 16 weight
-// rows and of the m activation rows into its own LDS region with direct loads
-// (global_load_lds_dwordx4), waits for its own copies and needs no barrier
-// until the cross-wave sum at the end. Per block the wave reads its MFMA
-// operands from LDS: lane l takes weight row l % 16 (B) and activation row
-// l % 16 (A, clamped below m) with K positions 4q..4q+3 and 16+4q..16+4q+3,
-// q = l / 16 — one nibble dword as loaded gives both (low nibbles, then high),
-// and the activation's two dwords sit at the same byte offsets. The first
-// block of a pair sits two bytes into its dwords (realigned with
-// v_alignbyte), the second is dword-aligned. Per block and lane: one
-// v_mfma_i32_16x16x32_i8 (16 * S_b), four dw*da products (v_fma_mix), four
-// fp32 fma. The wave partial sums are added in wave order through LDS.
-// Against the pairs kernel this trades its 16 v_dot4 and 17-dword LDS read
-// per activation row and block pair for a few LDS reads and one MFMA per
-// block.
-__host__ __device__ constexpr int64_t mf_gemv_lds_bytes(int64_t m, int64_t nb) {
-    return nb * (16 * 18 + m * 34);  // the waves' slices: 16 weight rows, m activation rows
-}
-
-struct MfGemvGeom {
-    int cprw, cpra;         // 16-byte chunks per weight / activation row slice
-    uint32_t magw, maga;    // ceil(2^32 / cpr): chunk -> row by one v_mul_hi_u32
-};
-
-template <int M, int WV>
-__global__ __launch_bounds__(WV * 64) void gemv_q4_0_mfma_kernel(const uint8_t *__restrict__ w,
-                                                                       const uint8_t *__restrict__ a,
-                                                                       float *__restrict__ c, int n, int nb,
-                                                                       MfGemvGeom geo) {
-    static_assert(M >= 1 && M <= 16, "one 16-row tile of activation rows");
-    extern __shared__ __align__(16) uint8_t lds[];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int n0 = blockIdx.x * 16;
-    const int bw = nb / WV;  // blocks per wave
-    const int kb0 = wave * bw;
-    const int rw = bw * 18, ra = bw * 34;  // slice bytes per row (multiples of 16: bw % 8 == 0)
-    uint8_t *ws = lds + (size_t)wave * (16 * rw + M * ra);
-    uint8_t *as = ws + 16 * rw;
-    // this wave's slices, 16 bytes per lane and load
-    const int nw = 16 * geo.cprw, na = M * geo.cpra;
-    for (int c0 = 0; c0 < nw; c0 += 64) {
-        const uint32_t ch = (uint32_t)(c0 + lane);
-        const int row = (int)__umulhi(ch, geo.magw);
-        const int col = (int)ch - row * geo.cprw;
-        if ((int)ch < nw && n0 + row < n)
-            __builtin_amdgcn_global_load_lds(w + ((size_t)(n0 + row) * nb + kb0) * 18 + col * 16,
-                                             (__attribute__((address_space(3))) void *)(ws + c0 * 16), 16, 0, 0);
-    }
-    for (int c0 = 0; c0 < na; c0 += 64) {
-        const uint32_t ch = (uint32_t)(c0 + lane);
-        const int row = (int)__umulhi(ch, geo.maga);
-        const int col = (int)ch - row * geo.cpra;
-        if ((int)ch < na)
-            __builtin_amdgcn_global_load_lds(a + ((size_t)row * nb + kb0) * 34 + col * 16,
-                                             (__attribute__((address_space(3))) void *)(as + c0 * 16), 16, 0, 0);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave reads only what it copied
-    const int li = lane & 15, q = lane >> 4;
-    const int arow = li < M ? li : M - 1;
-    const uint8_t *wl = ws + li * rw + 2 + 4 * q;          // + 18 j: block j's nibble dword q
-    const uint8_t *al = as + arow * ra + 2 + 4 * q;        // + 34 j: activation dwords q, q + 4
-    const uint8_t *dwp = ws + li * rw;                      // + 18 j: dw of weight row li
-    int orow[4];                                            // output rows of this lane's results
-#pragma unroll
-    for (int r = 0; r < 4; ++r) orow[r] = 4 * q + r < M ? 4 * q + r : M - 1;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto block = [&](int j, uint32_t wq, uint32_t x0, uint32_t x1) {
-        const uint64_t bop = (uint64_t)q4_0_lo16(wq) | ((uint64_t)q4_0_hi16(wq) << 32);
-        const uint64_t aop = (uint64_t)x0 | ((uint64_t)x1 << 32);
-        const i32x4 s16 = mfma_i8_16x16x32(aop, bop, (i32x4){0, 0, 0, 0});
-        const uint32_t dw = *reinterpret_cast<const uint16_t *>(dwp + j * 18);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t da = *reinterpret_cast<const uint16_t *>(as + orow[r] * ra + j * 34);
-            acc[r] = __builtin_fmaf((float)s16[r], fp16_product<false, false>(da, dw), acc[r]);
-        }
-    };
-    for (int j = 0; j < bw; j += 2) {
-        // block j: two bytes into its dwords; block j + 1: dword-aligned
-        const uint32_t *w0 = reinterpret_cast<const uint32_t *>(wl + j * 18 - 2);
-        const uint32_t *a0 = reinterpret_cast<const uint32_t *>(al + j * 34 - 2);
-        const uint32_t wq0 = shift2(w0[0], w0[1]);
-        const uint32_t x00 = shift2(a0[0], a0[1]), x01 = shift2(a0[4], a0[5]);
-        const uint32_t wq1 = *reinterpret_cast<const uint32_t *>(wl + (j + 1) * 18);
-        const uint32_t *a1 = reinterpret_cast<const uint32_t *>(al + (j + 1) * 34);
-        block(j, wq0, x00, x01);
-        block(j + 1, wq1, a1[0], a1[4]);
-    }
-    // wave partials through LDS, added in wave order by wave 0
-    __syncthreads();
-    float *red = reinterpret_cast<float *>(lds);
-    if (wave > 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red[((wave - 1) * 4 + r) * 64 + lane] = acc[r];
-    }
-    __syncthreads();
-    if (wave == 0) {
-        for (int v = 1; v < WV; ++v) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] += red[((v - 1) * 4 + r) * 64 + lane];
-        }
-        const int col = n0 + li;
-        if (col < n) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                if (4 * q + r < M) c[(size_t)(4 * q + r) * n + col] = acc[r] * 0.0625f;
-        }
-    }
-}
-
-// k % 256 == 0 from k = 4096 (16 waves of 8 blocks per round; round r takes
+// k % 256 == 0 from k = 512 (16 waves of 8 blocks per round; round r takes
 // blocks 8 (16 r + wave) .. + 8 of every row while they exist, so waves can run
-// different numbers of rounds, the partial sums staying in registers) from
-// m = 6 (m = 5 above k = 4096): 16-row int8 MFMA tiles over C = ceil(m / 16)
-// chunks of 16 activation rows (m up to 16 * kMaxGemvChunks).
+// different numbers of rounds, or none below k = 4096, the partial sums
+// staying in registers) from m = q4_0_tiles_min_m(k): 16x16 int8 MFMA tiles
+// over C = ceil(m / 16) chunks of 16 activation rows (m up to
+// gemv_tiles_max_m(k)). A workgroup takes 16 weight rows (output columns).
+// Per block lane l takes weight row l % 16 (B) and activation row l % 16 of
+// the chunk (A) with K positions 4q..4q+3 and 16+4q..16+4q+3, q = l / 16: one
+// nibble dword gives both (low nibbles, then high), and the activation's two
+// dwords sit at the same byte offsets; the first block of a pair sits two
+// bytes into its dwords (realigned with v_alignbyte), the second is
+// dword-aligned. One v_mfma_i32_16x16x32_i8 per block gives 16 S_b.
 constexpr int kMf8Blocks = 8;  // blocks per wave
 constexpr int kMf8Waves = 16;
 
@@ -627,8 +517,8 @@ __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(co
                                                                               float *__restrict__ c, int m, int n,
                                                                               int groups) {
     static_assert(C >= 1 && C <= kMaxGemvChunks, "at most kMaxGemvChunks chunks of 16 activation rows");
-    // 256-element groups of a row (k == 256 ng, ng >= kMf8Waves): kG when it is
-    // fixed at compile time (k = 4096: one round, constant strides), else groups
+    // 256-element groups of a row (k == 256 ng, ng >= 2): kG when it is fixed at
+    // compile time (k = 4096: one round, constant strides), else groups
     const int ng = kG > 0 ? kG : groups;
     const int nb = kMf8Blocks * ng;
     const uint32_t kARow = (uint32_t)nb * 34;
@@ -868,42 +758,29 @@ hipError_t launch_fused_m(const void *w, const float *x, float *c, int64_t n, in
     return hipGetLastError();
 }
 
-// k the chunked MFMA tile kernel takes: groups of 8 blocks (256 elements), at
-// least one per wave (the slices and rows stay 16-byte aligned at every k % 256)
-bool q4_0_tiles_take_k(int64_t k) { return k % 256 == 0 && k >= 256 * kMf8Waves; }
+// k the chunked MFMA tile kernel takes: groups of 8 blocks (256 elements; the
+// slices and rows stay 16-byte aligned at every k % 256), from k = 512 (below
+// 4096 the waves past the last group idle)
+bool q4_0_tiles_take_k(int64_t k) { return k % 256 == 0 && k >= 512; }
 
-// The 8-wave MFMA tile kernel (8-block slices, k % 2048 == 0) from m = 12
-// while its slices fit the LDS, where it measured faster than the pairs
-// kernel (k = 4096, us: m = 12 7.14 / 7.86, m = 10 7.18 / 6.95); from
-// k = 4096 the chunk kernel runs instead (k = 6144, m = 12: 7.03 against
-// 8.26 us), which leaves it k = 2048.
-bool mf_gemv_fits(int64_t m, int64_t k) {
-    return m >= 12 && m <= 16 && k % 2048 == 0 && mf_gemv_lds_bytes(m, k / 32) <= kPairsMaxLds;
+// Smallest m from which the tile kernel runs, measured at n = 4096 against the
+// pairs and group kernels (us, tile / other): k = 512 m = 3 2.97 / 3.34;
+// k = 1024 m = 3 3.30 / 3.41; k = 2048 m = 4 3.90 / 4.06 (m = 3 3.89 / 3.57);
+// k = 3072 m = 5 4.33 / 4.63 (m = 4 4.37 / 4.22); k = 4096 m = 6 5.15 / 5.33
+// (m = 5 5.15 / 4.93); above 4096 m = 5 (k = 8192 7.91 / 8.13-8.58, k = 12288
+// 10.65 / 11.07-11.76, k = 11008 9.65 / 13.07).
+int q4_0_tiles_min_m(int64_t k) {
+    if (k <= 1024) return 3;
+    if (k <= 2048) return 4;
+    return k == 4096 ? 6 : 5;
 }
 
 template <int M>
 hipError_t launch_gemv_q4_0_m(const void *w, const void *a, float *c, int64_t n, int64_t k, hipStream_t stream) {
     const int nb = (int)(k / 32);
-    // gemv_q4_0_mfma_chunk_kernel, one chunk: from m = 6 at k = 4096, from m = 5
-    // above (m = 5, n = 4096, against the kernels it replaced, us: k = 4096
-    // 5.15 / 4.93, k = 8192 7.91 / 8.13-8.58, k = 12288 10.65 / 11.07-11.76,
-    // k = 11008 9.65 / 13.07)
-    if ((M >= 6 || (M == 5 && k > 4096)) && q4_0_tiles_take_k(k)) {
+    if (M >= q4_0_tiles_min_m(k) && q4_0_tiles_take_k(k)) {  // gemv_q4_0_mfma_chunk_kernel, one chunk
         launch_q4_0_chunk<1>(static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(a), c, M, (int)n,
                              (int)(k / 256), stream);
-        return hipGetLastError();
-    }
-    if (mf_gemv_fits(M, k)) {
-        constexpr int wv = 8;
-        const int bw = nb / wv;  // blocks per wave, a multiple of 8
-        MfGemvGeom geo;
-        geo.cprw = bw * 18 / 16;
-        geo.cpra = bw * 34 / 16;
-        geo.magw = (uint32_t)((((uint64_t)1 << 32) + geo.cprw - 1) / geo.cprw);
-        geo.maga = (uint32_t)((((uint64_t)1 << 32) + geo.cpra - 1) / geo.cpra);
-        hipLaunchKernelGGL((gemv_q4_0_mfma_kernel<M, wv>), dim3((unsigned)((n + 15) / 16)), dim3(wv * 64),
-                           (size_t)mf_gemv_lds_bytes(M, nb), stream, static_cast<const uint8_t *>(w),
-                           static_cast<const uint8_t *>(a), c, (int)n, nb, geo);
         return hipGetLastError();
     }
     if (k % 64 == 0 && pairs_lds_bytes(M, nb) <= kPairsMaxLds) {
@@ -957,14 +834,14 @@ bool gemv_supported(int type, int64_t m, int64_t k) {
     if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) {
         if (m == 1) return k % 64 == 0;
         if (m <= 8) return k % 256 == 0 || pairs;
-        // m = 9..128 from k = 4096: gemv_q4_0_mfma_chunk_kernel; otherwise m = 9..16
-        // in the pair-per-lane kernel (or the 8-wave tile, whose slices need more LDS)
-        if (m <= 16 * kMaxGemvChunks && q4_0_tiles_take_k(k)) return true;
+        // gemv_q4_0_mfma_chunk_kernel up to gemv_tiles_max_m(k); otherwise m = 9..16
+        // in the pair-per-lane kernel
+        if (m <= gemv_tiles_max_m(k) && q4_0_tiles_take_k(k)) return true;
         return m <= kPairsMaxM && pairs;
     }
     // q4_K and iq2_xxs (gemv_kquant.hip): m <= 8 for every k % 256 == 0,
-    // m = 9..16 while the staged activations fit in LDS, m = 9..128 from k = 4096
-    // (q4_K k % 1024 == 0, iq2_xxs k % 2048 == 0)
+    // m = 9..16 while the staged activations fit in LDS, m = 9..64 or 128 at
+    // q4_K k % 1024 == 0, iq2_xxs k % 2048 == 0
     if (m > 8) return (kquant_gemv_staged_fits(m, k) || kquant_gemv_chunked_fits(type, m, k)) &&
                       (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K || type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K);
     return (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K || type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K) && k % 256 == 0;
@@ -1005,7 +882,7 @@ hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t
     case 16: return launch_gemv_q4_0_m<16>(w, a, c, n, k, stream);
     default: break;
     }
-    if (!(m >= 17 && m <= 16 * kMaxGemvChunks && q4_0_tiles_take_k(k))) return hipErrorInvalidValue;
+    if (!(m >= 17 && m <= gemv_tiles_max_m(k) && q4_0_tiles_take_k(k))) return hipErrorInvalidValue;
     const int ng = (int)(k / 256);
     const auto *wp = static_cast<const uint8_t *>(w);
     const auto *ap = static_cast<const uint8_t *>(a);

@@ -1,4 +1,4 @@
-// GEMV path (m <= 16, and up to 128 from k = 4096) for the super-block formats
+// GEMV path (m <= 16, and up to 64 or 128 for the tiles) for the super-block formats
 // against q8_K activations:
 // q4_K (llama_reference.cpp:113-132) and iq2_xxs (llama_reference.cpp:148-161,
 // kernels/common/iq2_xxs.h:29-41). One wavefront per weight row, the weight
@@ -8,14 +8,13 @@
 // (m <= 8) take m == 1 and rows too long to stage; for q4_K at m == 1 the
 // 16-row workgroups copy the activation row into LDS first. The
 // *_staged_kernel variants (m = 2..16) stage the rows in LDS once per 16-row
-// workgroup. From k = 4096 (q4_K at k % 1024 == 0, iq2_xxs at k % 2048 == 0)
-// both formats run 16x16 int8 MFMA tiles of 16 weight rows with one super-block
-// per wave: iq2_xxs at m = 5..8 and k == 4096 with the weight and activation
-// bytes copied together in two halves (gemv_iq2_xxs_mfma_sb_kernel), and from
-// m = 5 (q4_K; iq2_xxs from 9 at k = 4096, from 5 above) with the weights
-// decoded once per wave and the activation rows streamed in chunks of 16
-// (*_mfma_chunk_kernel; wave w takes super-blocks w, w + 16, ..., one per
-// round).
+// workgroup. At q4_K k % 1024 == 0 and iq2_xxs k % 2048 == 0 both formats run
+// 16x16 int8 MFMA tiles of 16 weight rows with one super-block per wave:
+// iq2_xxs at m = 5..8 and k == 4096 with the weight and activation bytes
+// copied together in two halves (gemv_iq2_xxs_mfma_sb_kernel), and from
+// m = kq_tiles_min_m (3..9 by format and k) with the weights decoded once per
+// wave and the activation rows streamed in chunks of 16 (*_mfma_chunk_kernel;
+// wave w takes super-blocks w, w + 16, ..., one per round).
 //
 // q4_K: four lanes per super-block, lane e owning sub-blocks 2e and 2e+1 (the
 // 32 nibble bytes qs[32e .. 32e+32): low nibbles of sub-block 2e, high of
@@ -995,10 +994,10 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_sb_kernel(c
     }
 }
 
-// From k = 4096 (kq_tiles_take_k) and m = 5 (q4_K; iq2_xxs m = 9 at k = 4096)
-// up to m = 16 * kMaxGemvChunks: 16x16 int8 MFMA tiles of 16 weight rows with
-// one super-block per wave and round (round r takes super-block 16 r + wave of
-// every row while it exists, so waves can run different numbers of rounds; the
+// At kq_tiles_take_k and from m = kq_tiles_min_m up to m = gemv_tiles_max_m:
+// 16x16 int8 MFMA tiles of 16 weight rows with one super-block per wave and
+// round (round r takes super-block 16 r + wave of every row while it exists,
+// so waves can run different numbers of rounds, or none below k = 4096; the
 // partial sums stay in registers), the activation rows taken in C = ceil(m / 16)
 // chunks of 16. Each wave copies its
 // super-block of the tile's 16 weight rows once, decodes them once into
@@ -1028,7 +1027,7 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
                                                                              float *__restrict__ c, int m, int n,
                                                                              int groups) {
     static_assert(C >= 1 && C <= kMaxGemvChunks, "at most kMaxGemvChunks chunks of 16 activation rows");
-    // super-blocks of a row (k == 256 nsb, nsb >= kKqMfWaves and nsb % 4 == 0): kG when it
+    // super-blocks of a row (k == 256 nsb, nsb % 4 == 0): kG when it
     // is fixed at compile time (k = 4096: one round, constant strides), else groups
     const int nsb = kG > 0 ? kG : groups;
     const uint32_t kARow = (uint32_t)nsb * kQ8KBytes;
@@ -1163,7 +1162,7 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
                                                                                 float *__restrict__ c, int m, int n,
                                                                                 int groups) {
     static_assert(C >= 1 && C <= kMaxGemvChunks, "at most kMaxGemvChunks chunks of 16 activation rows");
-    // super-blocks of a row (k == 256 nsb, nsb >= kKqMfWaves and nsb % 8 == 0): kG when it
+    // super-blocks of a row (k == 256 nsb, nsb % 8 == 0): kG when it
     // is fixed at compile time (k = 4096: one round, constant strides), else groups
     const int nsb = kG > 0 ? kG : groups;
     const uint32_t kARow = (uint32_t)nsb * kQ8KBytes;
@@ -1193,8 +1192,11 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
         for (int r = 0; r < 4; ++r) acc[ch][r] = 0.0f;
     // round rnd takes the wave's K slice 16 rnd + wave of every row; the next
     // round's copies start once the last round's buffers have been read
-    // this wave's rounds: its super-blocks wave, wave + 16, ... below nsb
+    // this wave's rounds: its super-blocks wave, wave + 16, ... below nsb; a wave
+    // without any (nsb < 16) still takes round 0's table barrier, so that every
+    // wave reaches the same barriers (waves 0..2, which copy the tables, have one)
     const int my_rounds = (nsb - wave + kKqMfWaves - 1) / kKqMfWaves;
+    if (my_rounds == 0) asm volatile("s_barrier" ::: "memory");
 #pragma clang loop unroll(disable)
     for (int rnd = 0; rnd < my_rounds; ++rnd) {
         // a lane index the compiler cannot carry across rounds: the per-lane
@@ -1307,14 +1309,29 @@ void launch_kq_chunk(bool q4k, const uint8_t *w, const uint8_t *a, float *c, int
         hipLaunchKernelGGL((gemv_iq2_xxs_mfma_chunk_kernel<C, 0>), grid, block, lds, stream, w, a, c, m, n, nsb);
 }
 
-// k the chunked MFMA tile kernels take: at least one super-block per wave, and
-// every row's blocks at the same offset from a 16-byte boundary with the last
-// block's copy ending at the row's end (q4_K: k % 1024 == 0, the q8_K blocks'
-// offset set by the block index mod 4; iq2_xxs: k % 2048 == 0, its 66-byte
-// weight blocks' offset by the index mod 8)
+// k the chunked MFMA tile kernels take: every row's blocks at the same offset
+// from a 16-byte boundary, with the last block's copy ending at the row's end
+// (q4_K: k % 1024 == 0, the q8_K blocks' offset set by the block index mod 4;
+// iq2_xxs: k % 2048 == 0, its 66-byte weight blocks' offset by the index mod
+// 8). Below k = 4096 the waves past the last super-block idle.
 bool kq_tiles_take_k(int type, int64_t k) {
     const int64_t unit = type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K ? 1024 : 2048;
-    return k % unit == 0 && k >= 256 * kKqMfWaves;
+    return k % unit == 0 && k >= unit;
+}
+
+// Smallest m from which the one-chunk tile runs, measured at n = 4096 against
+// the staged kernels (us, tile / staged): q4_K k = 1024 m = 3 3.17 / 3.51;
+// k = 2048 m = 4 3.63 / 3.93 (m = 3 3.64 / 3.70); k = 3072 m = 4 3.94 / 4.14
+// (m = 3 3.95 / 3.94); k = 4096 m = 5 4.66 / 5.01 (m = 4 4.66 / 4.55); k = 8192
+// m = 5 7.83 / 8.25. iq2_xxs k = 2048 m = 5 4.03 / 4.13 (m = 4 4.05 / 3.70);
+// k = 4096 from m = 9, m = 5..8 taking the two-half-copy kernel (4096 x 4096
+// against the staged kernel, us: m = 4 5.23 / 5.08, m = 5 5.34 / 5.91, m = 8
+// 5.56 / 6.58); above 4096 m = 5 (k = 8192 m = 5 8.29 / 9.46, m = 12 8.87 /
+// 16.72; k = 14336 m = 8 12.54 / 18.98).
+int kq_tiles_min_m(int type, int64_t k) {
+    if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K) return k == 4096 ? 9 : 5;
+    if (k <= 1024) return 3;
+    return k < 4096 ? 4 : 5;
 }
 
 template <int M>
@@ -1323,26 +1340,19 @@ hipError_t launch_kq_gemv(int type, const void *w, const void *a, float *c, int6
     const auto *wp = static_cast<const uint8_t *>(w);
     const auto *ap = static_cast<const uint8_t *>(a);
     const int64_t nsb = k / 256;
-    if constexpr (M >= 5) {
-        // one super-block per wave (and round), from m = 5 (4096 x 4096 against
-        // the staged kernel, us: iq2_xxs m = 4 5.23 / 5.08, m = 5 5.34 / 5.91,
-        // m = 8 5.56 / 6.58): one chunk of the chunked kernel for q4_K and for
-        // iq2_xxs (at k = 4096 from m = 9, m = 5..8 taking the two-half-copy
-        // kernel; n = 4096 against the staged kernel, us: k = 8192 q4_K m = 8
-        // 8.06 / 11.12, m = 12 8.67 / 14.64, iq2_xxs m = 12 8.87 / 16.72;
-        // k = 14336 q4_K m = 5 11.15 / 15.03, iq2_xxs m = 8 12.54 / 18.98)
-        const dim3 tiles((unsigned)((n + 15) / 16)), block(kKqMfWaves * 64);
-        if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && kq_tiles_take_k(type, k) && (M >= 9 || k > 4096)) {
-            launch_kq_chunk<1>(false, wp, ap, c, M, (int)n, (int)nsb, stream);
+    if constexpr (M >= 3) {
+        // one chunk of the chunked kernel from m = kq_tiles_min_m(type, k)
+        if (M >= kq_tiles_min_m(type, k) && kq_tiles_take_k(type, k)) {
+            launch_kq_chunk<1>(type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K, wp, ap, c, M, (int)n, (int)nsb, stream);
             return hipGetLastError();
         }
+    }
+    if constexpr (M >= 5) {
+        // iq2_xxs m = 5..8 at k = 4096: the two-half-copy kernel
         if (type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K && k == 4096) {
+            const dim3 tiles((unsigned)((n + 15) / 16)), block(kKqMfWaves * 64);
             hipLaunchKernelGGL(gemv_iq2_xxs_mfma_sb_kernel<M>, tiles, block, (size_t)iq2_sb_lds_bytes(M), stream, wp,
                                ap, c, (int)n);
-            return hipGetLastError();
-        }
-        if (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K && kq_tiles_take_k(type, k)) {
-            launch_kq_chunk<1>(true, wp, ap, c, M, (int)n, (int)nsb, stream);
             return hipGetLastError();
         }
     }
@@ -1417,7 +1427,7 @@ bool kquant_gemv_staged_fits(int64_t m, int64_t k) {
 }
 
 bool kquant_gemv_chunked_fits(int type, int64_t m, int64_t k) {
-    return m >= 9 && m <= 16 * kMaxGemvChunks && kq_tiles_take_k(type, k);
+    return m >= 9 && m <= gemv_tiles_max_m(k) && kq_tiles_take_k(type, k);
 }
 
 hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,

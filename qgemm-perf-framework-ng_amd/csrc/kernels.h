@@ -19,7 +19,7 @@ hipError_t launch_quantize_q4_K(const float *x, void *y, int64_t rows, int64_t k
 hipError_t launch_naive_mul_mat(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                                 hipStream_t stream);
 
-// gemv.hip (q4_0) and gemv_kquant.hip (q4_K, iq2_xxs) — m <= 16, up to 128 from k = 4096
+// gemv.hip (q4_0) and gemv_kquant.hip (q4_K, iq2_xxs) — m <= 16, up to 64 or 128 for the MFMA tiles
 bool gemv_supported(int type, int64_t m, int64_t k);
 hipError_t launch_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
                        hipStream_t stream);
@@ -33,7 +33,7 @@ hipError_t launch_kquant_fused_gemv(int type, const void *w, const float *x, flo
                                     hipStream_t stream);
 // q4_K / iq2_xxs GEMV rows m = 9..16 run only with the activations staged in LDS
 bool kquant_gemv_staged_fits(int64_t m, int64_t k);
-// m = 9..128 from k = 4096 (q4_K k % 1024 == 0, iq2_xxs k % 2048 == 0): MFMA tiles of 16
+// m = 9..gemv_tiles_max_m(k) at q4_K k % 1024 == 0, iq2_xxs k % 2048 == 0: MFMA tiles of 16
 // weight rows over chunks of 16 activation rows
 bool kquant_gemv_chunked_fits(int type, int64_t m, int64_t k);
 hipError_t launch_kquant_gemv(int type, const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,

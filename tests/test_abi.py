@@ -87,14 +87,16 @@ def test_argument_validation(pkg, call, expect):
     (0, 128, 4096, 4096, 1), (0, 129, 4096, 4096, 2), (0, 480, 1536, 1536, 2),
     (0, 3, 5, 96, -1), (0, 17, 8, 96, -1), (0, 24, 32, 256, 2), (0, 0, 8, 64, 0),
     (1, 8, 64, 512, 1), (1, 480, 1536, 1536, 2), (2, 512, 4096, 4096, 2), (2, 1, 4096, 4096, 1),
-    # from k = 4096 the GEMV path runs up to m = 128 (MFMA tiles over chunks of 16
-    # activation rows, one K group per wave and round) for q4_0 at k % 256 == 0,
-    # q4_K at k % 1024 == 0 and iq2_xxs at k % 2048 == 0; other k take the GEMM
-    # from m = 17
+    # the GEMV path runs MFMA tiles over chunks of 16 activation rows (one K group
+    # per wave and round) up to m = 128 from k = 2048 and up to m = 64 below, for
+    # q4_0 at k % 256 == 0 from 512, q4_K at k % 1024 == 0 and iq2_xxs at
+    # k % 2048 == 0; other k take the GEMM from m = 17
     (1, 32, 4096, 4096, 1), (2, 128, 4096, 4096, 1), (2, 129, 4096, 4096, 2), (1, 17, 4096, 8192, 1),
     (0, 17, 4096, 8192, 1), (0, 64, 4096, 12288, 1), (2, 16, 4096, 8192, 1), (1, 12, 4096, 12288, 1),
     (1, 129, 4096, 8192, 2), (0, 17, 4096, 6144, 1), (2, 17, 4096, 6144, 1), (0, 12, 4096, 14336, 1),
-    (0, 17, 4096, 4352, 1), (0, 128, 4096, 11008, 1), (0, 17, 4096, 3840, 2), (1, 17, 4096, 5120, 1),
+    (0, 17, 4096, 4352, 1), (0, 128, 4096, 11008, 1), (0, 17, 4096, 3840, 1), (1, 17, 4096, 5120, 1),
+    (0, 64, 4096, 1024, 1), (0, 65, 4096, 1024, 2), (0, 128, 4096, 2048, 1), (0, 17, 4096, 256, 2),
+    (1, 64, 4096, 1024, 1), (1, 65, 4096, 1024, 2), (1, 128, 4096, 3072, 1), (2, 128, 4096, 2048, 1),
     (1, 17, 4096, 4352, 2), (2, 17, 4096, 5120, 2), (2, 64, 4096, 14336, 1), (1, 16, 4096, 14336, 1),
     (0, 4, 4, 48, -1), (3, 4, 4, 64, -1),
 ])

@@ -177,12 +177,13 @@ def test_gemv_q4_0(hip, torch_gpu, oracle, m, n, k):
     rounds of 16 KB up to 64 KB, k = 20480 taking two rounds, a dword tail at
     k = 320 and 64), m = 2..16 with the activations staged in LDS
     (m * (k / 64) * 76 + 16 <= 160 KB), m = 2..8 beyond that (groups of 8
-    blocks per lane); from k = 4096 at k % 256 == 0 the one-chunk 16x16 MFMA
-    tile kernel, from m = 6 at k = 4096 and m = 5 above, over one to 16 rounds
-    (k = 6144 and 7680: waves with different numbers of rounds; 100, 33, 37 and
-    129 columns partial tiles), with 8 waves from m = 12 at k = 2048."""
+    blocks per lane); at k % 256 == 0 from k = 512 the one-chunk 16x16 MFMA
+    tile kernel, from m = 3..6 by k (k = 1536 and 2048 from m = 4, k = 4096
+    from 6, above from 5), over up to 16 rounds (k = 1536 and 2048: waves
+    without a K group; 6144 and 7680: waves with different numbers of rounds;
+    100, 33, 37 and 129 columns partial tiles)."""
     torch = torch_gpu
-    tiles = k % 256 == 0 and k >= 4096
+    tiles = k % 256 == 0 and k >= 512
     if m > 8 and not tiles and m * (k // 64) * 76 + 16 > 160 * 1024:
         pytest.skip("m > 8 takes the GEMV below the tiles' k only while the staged activations fit in LDS")
     say(f"gemv q4_0 m={m} n={n} k={k}")
@@ -460,12 +461,12 @@ def test_gemv_kquant(hip, torch_gpu, oracle, qtype, m, n, k):
     (k <= 57344; k = 65536 takes the global-read kernel), iq2_xxs reads it from
     global memory; m = 2..16 stage the rows in LDS while m * (k / 256) * 320 +
     3072 bytes fit 160 KB (at k = 20480 only m <= 6 do, at k = 65536 none; the
-    others up to m = 8 take the global-read kernel). From k = 4096 (q4_K at
-    k % 1024 == 0, iq2_xxs at k % 2048 == 0) the one-chunk MFMA tile kernel
-    takes q4_K from m = 5 and iq2_xxs from m = 9 at k = 4096 (m = 5..8 there:
-    the two-half-copy tile) and from m = 5 above, one super-block per wave and
+    others up to m = 8 take the global-read kernel). At q4_K k % 1024 == 0 and
+    iq2_xxs k % 2048 == 0 the one-chunk MFMA tile kernel takes q4_K from m = 5
+    (k >= 4096) and iq2_xxs from m = 9 at k = 4096 (m = 5..8 there: the
+    two-half-copy tile) and from m = 5 above, one super-block per wave and
     round (16 rounds at k = 65536)."""
-    tiles = k >= 4096 and k % (1024 if qtype == 1 else 2048) == 0
+    tiles = k % (1024 if qtype == 1 else 2048) == 0
     if m > 8 and not tiles and m * (k // 256) * 320 + 3072 > 160 * 1024:
         pytest.skip("m > 8 takes the GEMV below the tiles' k only while the staged activations fit in LDS")
     torch = torch_gpu
@@ -631,6 +632,32 @@ def test_compute_fused_kquant_gemv(hip, torch_gpu, oracle, qtype, m, n, k):
     unfused = hip.mul_mat(qtype, wt, hip.quantize_q8_K(at), m, n, k, path=hip.PATH_GEMV)
     torch.cuda.synchronize()
     assert torch.equal(fused, unfused)
+
+
+@pytest.mark.parametrize("m", [3, 4, 5, 9, 16, 17, 64, 65, 128])
+@pytest.mark.parametrize("qtype,n,k", [(0, 96, 512), (0, 37, 1024), (0, 64, 1536), (0, 50, 2048), (0, 40, 3072),
+                                       (1, 96, 1024), (1, 37, 2048), (1, 50, 3072), (2, 64, 2048), (2, 37, 2048)])
+def test_gemv_tiles_small_k(hip, torch_gpu, oracle, qtype, m, n, k):
+    """Below k = 4096 the one-chunk and chunked MFMA tile GEMVs run with the
+    waves past the last K group idle (q4_0 at k = 512: 14 of 16; iq2_xxs's idle
+    waves still take the table barrier), from the m measured fastest for the
+    format and k, up to m = 64 below k = 2048 and 128 from there; the other m
+    take the staged or pair kernels or the GEMM. The automatic path against the
+    oracle, on the generator's inputs and on random weight bytes against
+    activations at the int8 limits."""
+    torch = torch_gpu
+    say(f"gemv small k type={qtype} m={m} n={n} k={k}")
+    if 9 <= m <= (128 if k >= 2048 else 64):
+        assert hip.auto_path(qtype, m, n, k) == hip.PATH_GEMV
+    quantize = oracle.quantize_q8_0 if qtype == 0 else oracle.quantize_q8_K
+    act, w = oracle.create_input(qtype, m, n, k, seed=m * 5 + n + qtype)
+    aq = quantize(act)
+    got = run_mul_mat(hip, torch, qtype, w, aq, m, n, k, hip.PATH_AUTO)
+    check_close(oracle, qtype, got, w, aq, m, n, k, label=f"gemv small k type={qtype} m={m} n={n} k={k}")
+    wr = random_weight_blocks(oracle, qtype, n, k, seed=97 + m + qtype)
+    ax = quantize(np.where(np.random.default_rng(m + 7).random((m, k)) < 0.5, -1.0, 1.0).astype(np.float32))
+    got = run_mul_mat(hip, torch, qtype, wr, ax, m, n, k, hip.PATH_AUTO)
+    check_close(oracle, qtype, got, wr, ax, m, n, k, label=f"gemv small k random bytes type={qtype} m={m} k={k}")
 
 
 @pytest.mark.parametrize("qtype,m,n,k", [(0, 24, 96, 14336), (0, 7, 64, 11008), (1, 40, 64, 14336), (1, 9, 50, 5120),
