@@ -42,31 +42,30 @@ typedef enum {
 } pfng_status;
 
 /* Matrix-product implementations; PFNG_PATH_AUTO picks per shape (the GEMV
- * where it applies, up to m = 16, and up to m = 128 from k = 4096: q4_0 at
- * k % 256 == 0, q4_K at k % 1024 == 0, iq2_xxs at k % 2048 == 0; then the
- * MFMA tiles) and returns PFNG_ERR_UNSUPPORTED when neither applies (see
- * pfng_hip_auto_path). */
+ * where it applies: up to m = 16, and its MFMA tiles up to m = 64 below
+ * k = 2048 and m = 128 from there, for q4_0 at k % 256 == 0 from 512, q4_K at
+ * k % 1024 == 0, iq2_xxs at k % 2048 == 0; then the MFMA GEMM tiles) and
+ * returns PFNG_ERR_UNSUPPORTED when neither applies (see pfng_hip_auto_path). */
 typedef enum {
     PFNG_PATH_AUTO = 0,
     PFNG_PATH_GEMV = 1,  /* the decode-batch kernels. Shapes taken:
                             q4_0: m == 1 with k % 64 == 0; m = 2..8 with
                             k % 256 == 0, or k % 64 == 0 while
                             m * (k / 64) * 76 + 16 <= 163840; m = 9..16 with
-                            k % 64 == 0 under that same LDS bound;
-                            m = 9..128 with k % 256 == 0 and k >= 4096.
+                            k % 64 == 0 under that same LDS bound; m = 9..64
+                            (k < 2048) or 9..128 with k % 256 == 0, k >= 512.
                             q4_K and iq2_xxs: m <= 8 with k % 256 == 0;
                             m = 9..16 while m * (k / 256) * 320 + 3072 <= 163840;
-                            m = 9..128 with k >= 4096 and k % 1024 == 0 (q4_K)
-                            or k % 2048 == 0 (iq2_xxs).
+                            m = 9..64 (k < 2048) or 9..128 with k % 1024 == 0
+                            (q4_K) or k % 2048 == 0 (iq2_xxs).
                             Kernels: wavefront-per-row GEMVs for short batches;
                             16x16 int8-MFMA tiles with K split over 16 waves
-                            from k = 4096 (wave w takes the 256-element groups
-                            w, w + 16, ..., one per round), the weights decoded
-                            once per wave and round and the activation rows
-                            streamed in chunks of 16: at k == 4096 from m = 6
-                            (q4_0), 5 (q4_K) and 9 (iq2_xxs; m = 5..8 a tile
-                            with two-half copies), at larger k from m = 5;
-                            q4_0 also from m = 12 at k == 2048 (8 waves) */
+                            (wave w takes the 256-element groups w, w + 16, ...,
+                            one per round; below k = 4096 some waves idle), the
+                            weights decoded once per wave and round and the
+                            activation rows streamed in chunks of 16, from
+                            m = 3..6 by format and k (iq2_xxs at k == 4096 from
+                            m = 9, m = 5..8 a tile with two-half copies) */
     PFNG_PATH_MFMA = 2,  /* int8-MFMA GEMM, LDS-staged tiles: q4_0 with k % 128 == 0,
                             q4_K and iq2_xxs for every k % 256 == 0 */
     PFNG_PATH_NAIVE = 3  /* one thread per output, the reference's exact fp32 order */
