@@ -178,7 +178,8 @@ ValidationResult validate(const BenchmarkRequest &r) {
     }
     if constexpr (Path == PFNG_PATH_GEMV) {
         // the automatic path prefers the GEMV wherever one applies
-        if (auto_path != PFNG_PATH_GEMV) return {false, "no GEMV kernel takes this shape (M <= 16 and K limits)"};
+        if (auto_path != PFNG_PATH_GEMV)
+            return {false, "no GEMV kernel takes this shape (the M and K limits of pfng_hip_auto_path)"};
     }
     if constexpr (Path == PFNG_PATH_MFMA && T == QuantizationType::WeightQ4_0ActivationQ8_0) {
         if (r.k % 128) return {false, "the q4_0 MFMA path needs K % 128 == 0"};
@@ -203,22 +204,30 @@ using QT = QuantizationType;
 
 void register_q4_0_hip_mi355x() {
     add<QT::WeightQ4_0ActivationQ8_0, PFNG_PATH_AUTO>("q4_0-q8_0-HIP-mi355x",
-                                                      "Q4_0/Q8_0 HIP gfx950 (GEMV for M<=16, int8 MFMA otherwise)");
-    add<QT::WeightQ4_0ActivationQ8_0, PFNG_PATH_GEMV>("q4_0-q8_0-HIP-gemv", "Q4_0/Q8_0 HIP gfx950 wave-per-row GEMV");
+                                                      "Q4_0/Q8_0 HIP gfx950 "
+                                                      "(decode GEMVs up to M=16, MFMA tile GEMVs up to M=128 "
+                                                      "at their K, int8 MFMA GEMM above)");
+    add<QT::WeightQ4_0ActivationQ8_0, PFNG_PATH_GEMV>("q4_0-q8_0-HIP-gemv",
+                                                      "Q4_0/Q8_0 HIP gfx950 decode GEMVs (wave-per-row and MFMA tiles)");
     add<QT::WeightQ4_0ActivationQ8_0, PFNG_PATH_MFMA>("q4_0-q8_0-HIP-mfma", "Q4_0/Q8_0 HIP gfx950 int8 MFMA GEMM");
     add<QT::WeightQ4_0ActivationQ8_0, PFNG_PATH_NAIVE>("q4_0-q8_0-HIP-naive",
                                                        "Q4_0/Q8_0 HIP thread-per-output, reference fp32 order");
 }
 
 void register_q4_K_hip_mi355x() {
-    add<QT::WeightQ4_KActivationQ8_K, PFNG_PATH_AUTO>("q4_K-q8_K-HIP-mi355x", "Q4_K/Q8_K HIP gfx950 (GEMV for M<=16, int8 MFMA otherwise)");
+    add<QT::WeightQ4_KActivationQ8_K, PFNG_PATH_AUTO>("q4_K-q8_K-HIP-mi355x",
+                                                      "Q4_K/Q8_K HIP gfx950 "
+                                                      "(decode GEMVs up to M=16, MFMA tile GEMVs up to M=128 "
+                                                      "at their K, int8 MFMA GEMM above)");
     add<QT::WeightQ4_KActivationQ8_K, PFNG_PATH_NAIVE>("q4_K-q8_K-HIP-naive",
                                                        "Q4_K/Q8_K HIP thread-per-output, reference fp32 order");
 }
 
 void register_iq2_xxs_hip_mi355x() {
     add<QT::WeightIQ2_XXSActivationQ8_K, PFNG_PATH_AUTO>("iq2_xxs-q8_K-HIP-mi355x",
-                                                         "IQ2_XXS/Q8_K HIP gfx950 (GEMV for M<=16, int8 MFMA otherwise)");
+                                                      "IQ2_XXS/Q8_K HIP gfx950 "
+                                                      "(decode GEMVs up to M=16, MFMA tile GEMVs up to M=128 "
+                                                      "at their K, int8 MFMA GEMM above)");
     add<QT::WeightIQ2_XXSActivationQ8_K, PFNG_PATH_NAIVE>("iq2_xxs-q8_K-HIP-naive",
                                                           "IQ2_XXS/Q8_K HIP thread-per-output, reference fp32 order");
 }

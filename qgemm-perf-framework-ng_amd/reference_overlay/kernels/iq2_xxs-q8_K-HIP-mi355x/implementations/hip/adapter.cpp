@@ -19,7 +19,8 @@ PrepareResult prepare(const BenchmarkRequest &request, const BenchmarkInput &inp
 
 void register_iq2_xxs_hip_mi355x() {
     register_kernel({"iq2_xxs-q8_K-HIP-mi355x",
-                     "IQ2_XXS/Q8_K HIP gfx950 (wave-per-row GEMV for M<=16, int8 MFMA tiles above)",
+                     "IQ2_XXS/Q8_K HIP gfx950 (decode GEMVs up to M=16, MFMA tile GEMVs up to M=128 "
+                     "at their K, int8 MFMA GEMM above)",
                      kPair,
                      {hip_mi355x::peak_i8_mac, validate, prepare, hip_mi355x::reset, hip_mi355x::run,
                       hip_mi355x::export_output, hip_mi355x::checksum, hip_mi355x::destroy}});

@@ -19,7 +19,8 @@ PrepareResult prepare(const BenchmarkRequest &request, const BenchmarkInput &inp
 
 void register_q4_0_hip_mi355x() {
     register_kernel({"q4_0-q8_0-HIP-mi355x",
-                     "Q4_0/Q8_0 HIP gfx950 (wave-per-row GEMV for M<=16, int8 MFMA tiles above)",
+                     "Q4_0/Q8_0 HIP gfx950 (decode GEMVs up to M=16, MFMA tile GEMVs up to M=128 "
+                     "at their K, int8 MFMA GEMM above)",
                      kPair,
                      {hip_mi355x::peak_i8_mac, validate, prepare, hip_mi355x::reset, hip_mi355x::run,
                       hip_mi355x::export_output, hip_mi355x::checksum, hip_mi355x::destroy}});
