@@ -112,3 +112,25 @@ def test_workspace_size(pkg):
     assert L.pfng_hip_compute_workspace_size(0, 3, 64) == 3 * 2 * 34
     assert L.pfng_hip_compute_workspace_size(1, 3, 512) == 3 * 2 * 292
     assert L.pfng_hip_compute_workspace_size(2, 0, 512) == 0
+
+
+def test_auto_path_sweep(pkg):
+    """The automatic path over a grid of shapes follows the documented rules:
+    every shape with m <= 8 and k % 256 == 0 takes the GEMV; the MFMA tile
+    GEMVs take m up to 64 below k = 2048 and 128 from there, at q4_0 k % 256
+    (from 512), q4_K k % 1024 and iq2_xxs k % 2048; past those m the GEMM takes
+    over (q4_0 needs k % 128 there, which k % 256 gives)."""
+    for qtype in (0, 1, 2):
+        unit = {0: 256, 1: 1024, 2: 2048}[qtype]
+        for k in (256, 512, 768, 1024, 1536, 2048, 3072, 4096, 4352, 5120, 6144, 8192, 11008, 14336, 16384):
+            tiles = k % unit == 0 and k >= (512 if qtype == 0 else unit)
+            max_m = 128 if k >= 2048 else 64
+            for m in list(range(1, 18)) + [31, 32, 33, 63, 64, 65, 96, 127, 128, 129, 160]:
+                got = pkg.auto_path(qtype, m, 4096, k)
+                assert got in (1, 2), (qtype, m, k, got)
+                if m <= 8:
+                    assert got == 1, (qtype, m, k)
+                if 9 <= m <= max_m and tiles:
+                    assert got == 1, (qtype, m, k)
+                if m > 16 and not (tiles and m <= max_m):
+                    assert got == 2, (qtype, m, k)
