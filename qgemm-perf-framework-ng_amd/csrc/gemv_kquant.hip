@@ -1322,7 +1322,7 @@ bool kq_tiles_take_k(int type, int64_t k) {
 // Smallest m from which the one-chunk tile runs, measured at n = 4096 against
 // the staged kernels (us, tile / staged): q4_K k = 1024 m = 3 3.17 / 3.51;
 // k = 2048 m = 4 3.63 / 3.93 (m = 3 3.64 / 3.70); k = 3072 m = 4 3.94 / 4.14
-// (m = 3 3.95 / 3.94); k = 4096 m = 5 4.66 / 5.01 (m = 4 4.66 / 4.55); k = 8192
+// (m = 3 3.95 / 3.94); k = 4096 m = 5 4.66 / 5.12 (m = 4 4.66 / 4.55); k = 8192
 // m = 5 7.83 / 8.25. iq2_xxs k = 2048 m = 5 4.03 / 4.13 (m = 4 4.05 / 3.70);
 // k = 4096 from m = 9, m = 5..8 taking the two-half-copy kernel (4096 x 4096
 // against the staged kernel, us: m = 4 5.23 / 5.08, m = 5 5.34 / 5.91, m = 8
