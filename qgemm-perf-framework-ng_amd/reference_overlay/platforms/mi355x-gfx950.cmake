@@ -1,8 +1,12 @@
 # Platform profile of the MI355X HIP backend for the reference's CMake build
 # (variables required by cmake/PlatformConfig.cmake:14-30). The kernels run on
 # one AMD Instinct MI355X (gfx950); this profile builds the host side (harness,
-# adapters) for the x86-64 host with the host C++ compiler, e.g.
-#   cmake -S <reference> -B build -DPFNG_TARGET_PLATFORM=mi355x-gfx950 \
+# adapters) for the x86-64 host with the host C++ compiler (g++ or ROCm's
+# clang++), through the reference's own entry point
+#   PFNG_HIP_ROOT=<this repository> ./compile-and-test.sh build \
+#       --platform mi355x-gfx950 --cxx "$(command -v g++)"
+# or directly
+#   cmake -S <reference> -B build -G Ninja -DPFNG_TARGET_PLATFORM=mi355x-gfx950 \
 #         -DCMAKE_CXX_COMPILER=g++ -DPFNG_HIP_ROOT=<this repository>
 # after `make -C <this repository>/qgemm-perf-framework-ng_amd` has built
 # libpfng_hip.so (device code is compiled by hipcc there, not by this build).

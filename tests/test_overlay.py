@@ -5,13 +5,15 @@ reference tree.
 CPU: the patch applies to the reference; the profile defines every variable the
 reference's cmake/PlatformConfig.cmake requires; the kernel CMakeLists register
 through the reference's own pfng_declare_kernel (cmake/Kernel.cmake); and the
-reference harness (bench/main.cpp, bench/framework, llama_reference,
-kernels/common) compiles and links with the adapters against the reference's
-kernel_registry.h / adapter_common.h. These need the reference tree and skip
-without it.
+reference's own entry point, `compile-and-test.sh build --platform
+mi355x-gfx950` (CMake + Ninja, g++), builds the reference harness
+(bench/main.cpp, bench/framework, llama_reference, kernels/common) with the
+adapters against the reference's kernel_registry.h / adapter_common.h. These
+need the reference tree and skip without it.
 
 GPU: the harness built that way (the reference's own pfng-bench) runs the HIP
-kernel IDs on the device and verifies them against llama_reference::compute.
+kernel IDs on the device and verifies them against llama_reference::compute,
+first with the script's default preflight (--kernel all --m 24 --n 32 --k 256).
 """
 from __future__ import annotations
 
@@ -104,19 +106,49 @@ def test_kernel_ids_register_through_the_reference_kernel_cmake(tmp_path):
 
 @needs_ref
 def test_reference_harness_builds_with_the_overlay(pkg, tmp_path):
-    """The reference's bench/main.cpp, framework, llama_reference and
-    kernels/common compile and link with the three adapters and libpfng_hip
-    (g++, -Wall -Wextra); the binary reports the mi355x-gfx950 build."""
+    """The overlay Makefile builds through the patched reference's own
+    compile-and-test.sh (CMake + Ninja, g++): the reference's bench/main.cpp,
+    framework, llama_reference and kernels/common compile and link with the
+    three adapters and libpfng_hip, without warnings; the generated
+    registration calls the three HIP IDs and the binary reports the
+    mi355x-gfx950 build (listing the IDs needs the GPU: see below)."""
     pkg.lib()  # libpfng_hip.so is built
     out = tmp_path / "out"
     r = subprocess.run(["make", "-s", "-C", OVERLAY, f"REF={REF}", f"WORK={tmp_path / 'work'}", f"OUT={out}"],
                        capture_output=True, text=True, timeout=600)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "warning" not in (r.stdout + r.stderr).lower(), r.stdout + r.stderr
-    env = dict(os.environ, LD_LIBRARY_PATH=os.path.dirname(pkg.LIB_PATH))  # the rpath is relative to _build/
-    info = subprocess.run([str(out / "pfng-bench"), "--build-info"], capture_output=True, text=True, timeout=60,
-                          env=env)
+    assert "Linking CXX executable pfng-bench" in r.stdout, r.stdout
+    manifest = (out / "cmake" / "build-manifest.json").read_text()
+    assert '"platform": "mi355x-gfx950"' in manifest
+    generated = (out / "cmake" / "generated" / "builtin_kernels.cpp").read_text()
+    for fn in ("register_q4_0_hip_mi355x", "register_q4_K_hip_mi355x", "register_iq2_xxs_hip_mi355x"):
+        assert fn + "();" in generated
+    info = subprocess.run([str(out / "pfng-bench"), "--build-info"], capture_output=True, text=True, timeout=60)
     assert info.returncode == 0 and "platform: mi355x-gfx950" in info.stdout, info.stdout + info.stderr
+
+
+@needs_ref
+def test_compile_and_test_script_takes_the_gpu_profile(tmp_path):
+    """The patched compile-and-test.sh lists mi355x-gfx950, requires
+    PFNG_HIP_ROOT for it, and runs `run` on this machine (no --remote): here,
+    without a GPU, the binary's own platform check is what stops it."""
+    work = tmp_path / "ref"
+    shutil.copytree(REF, work, ignore=shutil.ignore_patterns("docs", "machine-benchmarks", "build"))
+    subprocess.run(["patch", "-s", "-p1", "-d", str(work), "-i", os.path.join(OVERLAY, "reference.patch")],
+                   check=True)
+    script = str(work / "compile-and-test.sh")
+    usage = subprocess.run([script], capture_output=True, text=True)
+    assert "mi355x-gfx950" in usage.stderr, usage.stderr
+    env = {k: v for k, v in os.environ.items() if k != "PFNG_HIP_ROOT"}
+    r = subprocess.run([script, "configure", "--platform", "mi355x-gfx950", "--cxx", shutil.which("g++"),
+                        "--build-dir", str(tmp_path / "b")], capture_output=True, text=True, env=env)
+    assert r.returncode == 2 and "set PFNG_HIP_ROOT" in r.stderr, r.stderr
+    r = subprocess.run([script, "run", "--platform", "mi355x-gfx950", "--build-dir", str(tmp_path / "none")],
+                       capture_output=True, text=True)
+    assert r.returncode == 2 and "binary does not exist" in r.stderr and "--remote" not in r.stderr, r.stderr
+    r = subprocess.run([script, "build", "--platform", "riscv-nonexistent"], capture_output=True, text=True)
+    assert "unsupported platform" in r.stderr
 
 
 def run_built(*args, timeout=300):
@@ -138,6 +170,21 @@ def test_reference_harness_lists_and_detects_the_device(hip):
         assert re.search(r"^" + re.escape(kid) + r"\s.*\[platform=mi355x-gfx950\]", r.stdout, re.M), r.stdout
     r = run_built("--platform-info", timeout=120)
     assert r.returncode == 0 and "platform check: PASS" in r.stdout, r.stdout + r.stderr
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not os.path.isfile(BUILT), reason="reference harness with the overlay was not built")
+def test_reference_harness_default_preflight(hip):
+    """compile-and-test.sh's default test arguments (--kernel all --m 24 --n 32
+    --k 256 --samples 3 --iterations 10): every registered kernel ID, the three
+    HIP ones on this profile, verifies against llama_reference::compute."""
+    print("[case] reference pfng-bench --kernel all --m 24 --n 32 --k 256", flush=True)
+    r = run_built("--kernel", "all", "--m", "24", "--n", "32", "--k", "256", "--samples", "3", "--iterations", "10")
+    for kid in IDS:
+        block = kernel_block(r.stdout, kid)
+        assert "error elements: 0/768 " in block, r.stdout + r.stderr
+    if r.returncode != 0:
+        assert "perf_event_open" in r.stdout + r.stderr, r.stdout + r.stderr
 
 
 @pytest.mark.gpu
