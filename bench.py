@@ -5,15 +5,20 @@ Metric: "q4_0×q8_0 GEMM TOPS @480×1536×1536; M=1 GEMV GB/s @4
 One step = one pass of the hot path over one batch of synthetic input:
   * value   : config 1 — q4_0 x q8_0 GEMV, M=1 N=4096 K=4096, GB/s of algorithmic
               bytes (weights + q8_0 activation + fp32 output) per second. The steps
-              rotate over 32 weight copies (302 MB > the 256 MB Infinity Cache), so
-              the weights stream from HBM as in decode.
+              rotate over 48 weight copies (453 MB > the 256 MB Infinity Cache),
+              whatever the step count, so the weights stream from HBM as in decode.
   * gemm    : config 0 — q4_0 x q8_0 GEMM, M=480 N=1536 K=1536, TOPS = 2*M*N*K/s,
-              the other half of the compound metric.
+              the other half of the compound metric (its TOPS and roofline
+              fraction are repeated at the top level as gemm_tops / gemm_frac).
   * q4_K, iq2_xxs, prefill: configs 2, 3 and 4 in the same form.
   * gemv_q4_K, gemv_iq2_xxs: the M=1 GEMV of the super-block formats at
     N=K=4096 (not baseline configs; reported beside the headline).
-  * decode: the M=8 and M=16 GEMVs (decode batches) of all three formats at
-    N=K=4096, 32 rotating weight copies (not baseline configs).
+  * decode: the M=8, 16, 32, 64 and 128 GEMVs (decode batches) of all three
+    formats at N=K=4096, 48 rotating weight copies (not baseline configs).
+    These side items (and the M=1 K-quant GEMVs) time a fixed --decode-steps
+    (default 512) launches per sample, independent of --steps.
+Items the automatic path runs on the GEMV kernels report GB/s against the HBM
+roofline (and TOPS beside it), the others TOPS against the int8 MFMA peak.
 Every item carries two figures: the product alone on activations quantized
 before the timed region (the reference quantizes in prepare(),
 kernels/*/adapter.cpp, and times run() only), and `e2e`, the end-to-end
@@ -59,6 +64,7 @@ METRIC = "q4_0×q8_0 GEMM TOPS @480×1536×1536; M=1 GEMV GB/s @4096×4096"
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA (5.0 POPS)
 PER_REPLAY = 32          # launches per captured graph
+COPIES = 48              # rotating weight copies of the GEMV items (c1: 453 MB)
 
 
 def log(*a):
@@ -100,16 +106,21 @@ def algorithmic_bytes(pkg, qtype, m, n, k):
 
 
 class Timer:
-    """Graphs of exactly `steps` launches of fn(i), i = 0..steps-1 (a graph of
-    PER_REPLAY launches replayed steps // PER_REPLAY times, then one of the
-    rest), timed over `samples` samples."""
+    """Graphs of exactly `steps` launches of fn(i) per sample: graphs of
+    min(PER_REPLAY, steps) launches, replayed steps // PER_REPLAY times, then
+    one graph of the rest. With distinct > 1, fn's index keeps advancing from
+    one replay to the next (ceil(distinct / PER_REPLAY) graphs taken in turn),
+    so rotating operand copies (fn(i) reads copy i % copies) cycle through all
+    `distinct` of them whatever `steps` is."""
 
-    def __init__(self, torch, fn, steps):
+    def __init__(self, torch, fn, steps, distinct=1):
         self.torch, self.steps = torch, steps
         self.full = min(PER_REPLAY, steps)
         self.reps, rest = divmod(steps, self.full)
-        self.main = self._capture(fn, 0, self.full)
-        self.rest = self._capture(fn, self.reps * self.full, rest) if rest else None
+        count = max(1, -(-distinct // self.full))
+        self.graphs = [self._capture(fn, j * self.full, self.full) for j in range(count)]
+        self.rest = self._capture(fn, count * self.full, rest) if rest else None
+        self.turn = 0
 
     def _capture(self, fn, first, count):
         torch = self.torch
@@ -129,14 +140,15 @@ class Timer:
 
     def _once(self):
         for _ in range(self.reps):
-            self.main.replay()
+            self.graphs[self.turn].replay()
+            self.turn = (self.turn + 1) % len(self.graphs)
         if self.rest is not None:
             self.rest.replay()
 
     def run(self, warmup, samples):
         """Returns (median wall s per step, median event us per launch, walls, events)."""
         torch = self.torch
-        for _ in range(max(1, -(-warmup // self.steps))):
+        for _ in range(max(1, -(-warmup // self.steps), len(self.graphs))):
             self._once()
         torch.cuda.synchronize()
         walls, evs = [], []
@@ -187,11 +199,12 @@ def measure(torch, pkg, label, qtype, m, n, k, steps, warmup, samples, variant, 
     ws = torch.empty(max(1, pkg.lib().pfng_hip_compute_workspace_size(qtype, m, k)), dtype=torch.uint8, device="cuda")
     torch.cuda.synchronize()
 
-    product = Timer(torch, lambda i: pkg.mul_mat(qtype, weights[i % copies], aq, m, n, k, out=outs[i % copies]), steps)
+    product = Timer(torch, lambda i: pkg.mul_mat(qtype, weights[i % copies], aq, m, n, k, out=outs[i % copies]), steps,
+                    copies)
     wall, k_us, walls, _ = product.run(warmup, samples)
     del product
     e2e = Timer(torch, lambda i: pkg.compute(qtype, act_t, weights[i % copies], n, out=outs[i % copies], workspace=ws),
-                steps)
+                steps, copies)
     e_wall, e_us, _, _ = e2e.run(warmup, samples)
     del e2e
 
@@ -206,7 +219,7 @@ def measure(torch, pkg, label, qtype, m, n, k, steps, warmup, samples, variant, 
         ver["rows_verified"] = f"{verify_rows} of {m} rows (seeded sample), every column"
         ver_e2e["rows_verified"] = ver["rows_verified"]
 
-    gemv = m <= 16
+    gemv = pkg.auto_path(qtype, m, n, k) == pkg.PATH_GEMV
     bytes_ = algorithmic_bytes(pkg, qtype, m, n, k)
     ops = 2.0 * m * n * k
     if gemv:
@@ -220,6 +233,7 @@ def measure(torch, pkg, label, qtype, m, n, k, steps, warmup, samples, variant, 
         e2e_value = ops / e_wall / 1e12
     item = {
         "workload": label, "value": round(value, 3), "unit": unit, "steps": steps, "samples": samples,
+        "tops": round(ops / wall / 1e12, 3), "weight_copies": copies,
         "ms_per_step": round(wall * 1e3, 6),
         "sample_spread_pct": round(100.0 * (max(walls) - min(walls)) / wall, 2),
         "verify": ver,
@@ -341,8 +355,8 @@ def main():
     ap.add_argument("--iq2-steps", type=int, default=256, help="timed c3 GEMM steps per sample (0 = skip)")
     ap.add_argument("--prefill-steps", type=int, default=32, help="timed c4 GEMM steps per sample (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="bounded CPU-baseline budget (0 = skip)")
-    ap.add_argument("--decode-steps", type=int, default=None,
-                    help="timed steps of each M=1/8/16 side GEMV per sample (default steps/8, 0 = skip)")
+    ap.add_argument("--decode-steps", type=int, default=512,
+                    help="timed steps of each side GEMV (M=1 K-quants, M=8..128 decode) per sample (0 = skip)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -360,8 +374,8 @@ def main():
     log(f"[bench] device {arch}, {cus} CUs; {pkg.version()}")
     ref, base = pkg.INPUT_REFERENCE, pkg.INPUT_BASELINE
 
-    head = measure(torch, pkg, "c1: q4_0 x q8_0 GEMV M=1 N=4096 K=4096, 32 rotating weight copies (302 MB)", 0, 1,
-                   4096, 4096, steps, args.warmup, samples, ref, "gemv_q4_0_m1_kernel", copies=32)
+    head = measure(torch, pkg, f"c1: q4_0 x q8_0 GEMV M=1 N=4096 K=4096, {COPIES} rotating weight copies (453 MB)",
+                   0, 1, 4096, 4096, steps, args.warmup, samples, ref, "gemv_q4_0_m1_kernel", copies=COPIES)
     gemm = measure(torch, pkg, "c0: q4_0 x q8_0 GEMM M=480 N=1536 K=1536", 0, 480, 1536, 1536, args.gemm_steps, 256,
                    samples, ref, "gemm_q4_0_wt_kernel")
     q4k = measure(torch, pkg, "c2: q4_K x q8_K GEMM M=480 N=1536 K=1536", 1, 480, 1536, 1536, args.gemm_steps, 256,
@@ -375,27 +389,27 @@ def main():
         prefill = measure(torch, pkg, "c4: q4_0 x q8_0 GEMM M=2048 N=11008 K=4096", 0, 2048, 11008, 4096,
                           args.prefill_steps, 8, samples, ref, "gemm_q4_0_kernel", verify_rows=256)
 
-    side = steps // 8 if args.decode_steps is None else args.decode_steps
+    side = max(0, args.decode_steps)
+    log(f"[bench] side GEMV items: {side} timed launches per sample")
     gemv_kq, decode = [], []
     if side > 0:
         for qt, name, variant in ((1, "q4_K", ref), (2, "iq2_xxs", base)):
-            gemv_kq.append(measure(torch, pkg, f"m1_{name}: {name} x q8_K GEMV M=1 N=4096 K=4096, 32 rotating "
+            gemv_kq.append(measure(torch, pkg, f"m1_{name}: {name} x q8_K GEMV M=1 N=4096 K=4096, {COPIES} rotating "
                                    "weight copies", qt, 1, 4096, 4096, side, max(side // 10, 32), samples, variant,
-                                   f"gemv_{name}_kernel<1>", copies=32))
-        # at K = 4096 M = 8 and 16 run the 16x16 MFMA tile GEMVs: one chunk of 16
-        # activation rows of the chunked kernels in their one-round form (16
-        # groups; q4_0 from M = 6, q4_K from M = 5, iq2_xxs from M = 9), iq2_xxs
-        # at M = 5..8 the two-half-copy kernel
-        kernels = {0: {8: "gemv_q4_0_mfma_chunk_kernel<1, 16>", 16: "gemv_q4_0_mfma_chunk_kernel<1, 16>"},
-                   1: {8: "gemv_q4_K_mfma_chunk_kernel<1, 16>", 16: "gemv_q4_K_mfma_chunk_kernel<1, 16>"},
-                   2: {8: "gemv_iq2_xxs_mfma_sb_kernel<8>", 16: "gemv_iq2_xxs_mfma_chunk_kernel<1, 16>"}}
+                                   f"gemv_{name}_kernel<1>", copies=COPIES))
+        # at K = 4096 the 16x16 MFMA tile GEMVs run from M = 6 (q4_0), 5 (q4_K)
+        # and 9 (iq2_xxs; M = 5..8 the two-half-copy kernel), over C = M / 16
+        # chunks of 16 activation rows
         for qt, name, variant in ((0, "q4_0", ref), (1, "q4_K", ref), (2, "iq2_xxs", base)):
             act_t = "q8_0" if qt == 0 else "q8_K"
-            for dm in (8, 16):
-                kname = kernels[qt][dm]
+            for dm in (8, 16, 32, 64, 128):
+                if qt == 2 and dm == 8:
+                    kname = "gemv_iq2_xxs_mfma_sb_kernel<8>"
+                else:
+                    kname = f"gemv_{name}_mfma_chunk_kernel<{max(1, dm // 16)}"
                 decode.append(measure(torch, pkg, f"m{dm}_{name}: {name} x {act_t} GEMV M={dm} N=4096 K=4096, "
-                                      "32 rotating weight copies", qt, dm, 4096, 4096, side, max(side // 10, 32),
-                                      samples, variant, kname, copies=32))
+                                      f"{COPIES} rotating weight copies", qt, dm, 4096, 4096, side,
+                                      max(side // 10, 32), samples, variant, kname, copies=COPIES))
 
     cpu = cpu_baseline(args.cpu_seconds, pkg) if args.cpu_seconds > 0 else None
     if cpu:
@@ -420,6 +434,9 @@ def main():
         "roofline": head["roofline"],
         "e2e": head["e2e"],
         "verify": head["verify"],
+        "gemm_tops": gemm["value"],
+        "gemm_frac": gemm["roofline"]["frac"],
+        "gemm_ms_per_step": gemm["ms_per_step"],
         "gemm": gemm,
         "q4_K": q4k,
         "iq2_xxs": iq2,

@@ -58,6 +58,7 @@ typedef enum {
                             m = 9..16 while m * (k / 256) * 320 + 3072 <= 163840;
                             m = 9..64 (k < 2048) or 9..128 with k % 1024 == 0
                             (q4_K) or k % 2048 == 0 (iq2_xxs).
+                            All formats: k <= 2^24 (32-bit load offsets).
                             Kernels: wavefront-per-row GEMVs for short batches;
                             16x16 int8-MFMA tiles with K split over 16 waves
                             (wave w takes the 256-element groups w, w + 16, ...,
@@ -67,7 +68,7 @@ typedef enum {
                             m = 3..6 by format and k (iq2_xxs at k == 4096 from
                             m = 9, m = 5..8 a tile with two-half copies) */
     PFNG_PATH_MFMA = 2,  /* int8-MFMA GEMM, LDS-staged tiles: q4_0 with k % 128 == 0,
-                            q4_K and iq2_xxs for every k % 256 == 0 */
+                            q4_K and iq2_xxs for every k % 256 == 0; k <= 2^24 */
     PFNG_PATH_NAIVE = 3  /* one thread per output, the reference's exact fp32 order */
 } pfng_path;
 
@@ -79,6 +80,9 @@ const char *pfng_hip_version(void);
 
 /* Checks that the current HIP device is a gfx950 (MI355X). Writes the
  * gcnArchName into arch (if non-NULL) and the CU count into cus (if non-NULL).
+ * Also resolves, for this device, what the other entry points look up once per
+ * device (its CU count, the address of pfng_hip_compute_noalloc's scratch), so
+ * that calls made under graph capture afterwards make no such query.
  * Replaces the Device-Tree platform check of bench/framework/platform.cpp:97-133. */
 int pfng_hip_device_check(char *arch, size_t arch_len, int *cus);
 
@@ -155,10 +159,13 @@ int pfng_hip_compute(int type, const float *activation, const void *weight, floa
  * without a workspace. The quantized activations go to a static 16 MiB device
  * array of the library (one per device, held until the process ends), so
  * m * (k/32) * 34 bytes (q4_0) or m * (k/256) * 292 bytes (q4_K, iq2_xxs) must
- * not exceed 16 MiB (e.g. m = 2048 at k = 4096 for q4_0); larger shapes return
+ * not exceed 16 MiB (q4_0 at k = 4096: m <= 3855); larger shapes return
  * PFNG_ERR_INVALID_ARGUMENT. The call itself allocates nothing. Every call on a
  * device shares that device's array: calls that overlap on one device (other
- * streams, other host threads) race and must be serialized by the caller. */
+ * streams, other host threads) race and must be serialized by the caller. The
+ * array's address is looked up on the first call on a device (or by
+ * pfng_hip_device_check): make that call outside graph capture; later calls may
+ * be captured. */
 int pfng_hip_compute_noalloc(int type, const float *activation, const void *weight, float *out, int64_t m, int64_t n,
                              int64_t k, int path, void *stream);
 

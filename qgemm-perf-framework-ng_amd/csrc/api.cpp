@@ -15,7 +15,7 @@
 
 namespace {
 
-thread_local char g_error[512] = "";
+thread_local char g_error[1024] = "";
 
 int fail(int status, const char *fmt, ...) {
     va_list args;
@@ -41,6 +41,27 @@ const char *type_name(int type) {
     case PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K: return "iq2_xxs x q8_K";
     default: return "unknown";
     }
+}
+
+// The shapes each tiled path takes (gemv_supported, mfma_supported; the same
+// rules as include/pfng_hip.h), for the messages of declined calls.
+const char *gemv_rule(int type) {
+    switch (type) {
+    case PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0:
+        return "the q4_0 GEMV takes m == 1 at k%64==0; m = 2..16 at k%64==0 while m*(k/64)*76+16 <= 163840 "
+               "(m <= 8 also at any k%256==0); m = 9..64 (k < 2048) or 9..128 at k%256==0 from k = 512";
+    case PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K:
+        return "the q4_K GEMV takes m <= 8; m = 9..16 while m*(k/256)*320+3072 <= 163840; m = 9..64 at k = 1024 "
+               "and 9..128 at k%1024==0 from k = 2048";
+    default:
+        return "the iq2_xxs GEMV takes m <= 8; m = 9..16 while m*(k/256)*320+3072 <= 163840; m = 9..128 at "
+               "k%2048==0";
+    }
+}
+
+const char *mfma_rule(int type) {
+    return type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0 ? "the q4_0 MFMA GEMM takes k%128==0"
+                                                    : "the MFMA GEMM takes every k%256==0";
 }
 
 // Shape checks shared by every product entry point (validate_shape,
@@ -131,7 +152,12 @@ int pfng_hip_device_check(char *arch, size_t arch_len, int *cus) {
     if (cus) *cus = prop.multiProcessorCount;
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(PFNG_ERR_DEVICE, "device %d is %s, this library is built for gfx950", dev, prop.gcnArchName);
-    return PFNG_OK;
+    // resolve what later calls look up once per device (the CU count of the
+    // tile plans, the no-allocation scratch address) here, outside any graph
+    // capture a caller may start afterwards
+    device_cus(dev);
+    void *scratch_ptr = nullptr;
+    return noalloc_scratch(&scratch_ptr);
 }
 
 int pfng_hip_quantize_q8_0(const float *x, void *y, int64_t rows, int64_t k, void *stream) {
@@ -179,25 +205,37 @@ int pfng_hip_mul_mat(int type, const void *weight, const void *act_q, float *out
     const bool mfma_ok = base_aligned && pfng::mfma_supported(type, m, k);
     switch (path) {
     case PFNG_PATH_AUTO:
-        // measured at 4096x4096: every GEMV that applies (up to m = 16) is
-        // faster than the MFMA tiles. When neither tiled path takes the shape
+        // measured at 4096x4096: every GEMV that applies (up to m = 128 at the
+        // tiles' k) is faster than the MFMA GEMM. When neither tiled path takes the shape
         // the call is declined (as the reference's validate_shape declines,
         // kernels/common/adapter_common.h:28-43) instead of dropping to the
         // one-thread-per-output kernel, which is 10-500x slower; the caller
         // may ask for PFNG_PATH_NAIVE explicitly.
         if (gemv_ok) return hip_status(pfng::launch_gemv(type, weight, act_q, out, m, n, k, s), "gemv launch");
         if (mfma_ok) return launch_mfma(type, weight, act_q, out, m, n, k, s);
+        if (!base_aligned)
+            return fail(PFNG_ERR_UNSUPPORTED,
+                        "%s: the tiled paths need 16-byte aligned weights and activations and a 4-byte aligned C; "
+                        "PFNG_PATH_NAIVE runs every shape in the reference's fp32 order",
+                        type_name(type));
         return fail(PFNG_ERR_UNSUPPORTED,
-                    "%s: no tiled path takes m=%lld k=%lld with these operand alignments (%s); "
-                    "PFNG_PATH_NAIVE runs every shape in the reference's fp32 order",
-                    type_name(type), (long long)m, (long long)k,
-                    base_aligned ? "q4_0 needs k%%64==0 for m<=16 and k%%128==0 above"
-                                 : "weights and activations must be 16-byte and C 4-byte aligned");
+                    "%s: no tiled path takes m=%lld k=%lld (%s; %s; both k <= %lld); PFNG_PATH_NAIVE runs every "
+                    "shape in the reference's fp32 order",
+                    type_name(type), (long long)m, (long long)k, gemv_rule(type), mfma_rule(type),
+                    (long long)pfng::kMaxTiledK);
     case PFNG_PATH_GEMV:
-        if (!gemv_ok) return fail(PFNG_ERR_UNSUPPORTED, "%s GEMV path needs m<=16 (q4_0: k%%64==0 for m==1, else k%%64==0 with m*(k/64)*76+16<=163840, or k%%256==0 for m<=8; q4_K/iq2_xxs: k%%256==0, for m>8 also m*(k/256)*320+3072<=163840) and 16-byte aligned operands (m=%lld k=%lld)", type_name(type), (long long)m, (long long)k);
+        if (!gemv_ok)
+            return fail(PFNG_ERR_UNSUPPORTED,
+                        "%s GEMV path does not take m=%lld k=%lld: %s, k <= %lld, with 16-byte aligned weights and "
+                        "activations and a 4-byte aligned C",
+                        type_name(type), (long long)m, (long long)k, gemv_rule(type), (long long)pfng::kMaxTiledK);
         return hip_status(pfng::launch_gemv(type, weight, act_q, out, m, n, k, s), "gemv launch");
     case PFNG_PATH_MFMA:
-        if (!mfma_ok) return fail(PFNG_ERR_UNSUPPORTED, "%s MFMA path not available for m=%lld k=%lld", type_name(type), (long long)m, (long long)k);
+        if (!mfma_ok)
+            return fail(PFNG_ERR_UNSUPPORTED,
+                        "%s MFMA path does not take m=%lld k=%lld: %s, k <= %lld, with 16-byte aligned weights and "
+                        "activations and a 4-byte aligned C",
+                        type_name(type), (long long)m, (long long)k, mfma_rule(type), (long long)pfng::kMaxTiledK);
         return launch_mfma(type, weight, act_q, out, m, n, k, s);
     case PFNG_PATH_NAIVE:
         return hip_status(pfng::launch_naive_mul_mat(type, weight, act_q, out, m, n, k, s), "naive launch");
@@ -211,9 +249,9 @@ int pfng_hip_auto_path(int type, int64_t m, int64_t n, int64_t k) {
     if (pfng::gemv_supported(type, m, k)) return PFNG_PATH_GEMV;
     if (pfng::mfma_supported(type, m, k)) return PFNG_PATH_MFMA;
     fail(PFNG_ERR_UNSUPPORTED,
-         "%s: no tiled path takes m=%lld k=%lld (q4_0 needs k%%64==0 for m<=16 and k%%128==0 above); "
-         "PFNG_PATH_NAIVE runs every shape in the reference's fp32 order",
-         type_name(type), (long long)m, (long long)k);
+         "%s: no tiled path takes m=%lld k=%lld (%s; %s; both k <= %lld); PFNG_PATH_NAIVE runs every shape in "
+         "the reference's fp32 order",
+         type_name(type), (long long)m, (long long)k, gemv_rule(type), mfma_rule(type), (long long)pfng::kMaxTiledK);
     return -1;
 }
 

@@ -120,7 +120,8 @@ constexpr int kQ8KBytes = 292, kQ4KBytes = 144, kIq2Bytes = 66;
 // Byte offsets of a thread's load tasks from the tile's first row at the
 // stage's super-block: fixed over the K loop (rows past the matrix edge are
 // clamped to its last row), so each stage's loads are a uniform base plus
-// these 32-bit offsets. BM * nb * 292 < 2^32 for any k the library takes.
+// these 32-bit offsets. BM * nb * 292 < 2^32 for every k up to kMaxTiledK
+// (mfma_supported declines longer rows).
 template <class C>
 struct KqOffsets {
     uint32_t a[C::kActPT];  // activation row + part e's qs dwords

@@ -85,8 +85,8 @@ struct StageRegs {
 // row at the current stage's first block. They stay the same over the K loop
 // (rows past the matrix edge are clamped to its last row), so each stage's
 // loads are a uniform stage base plus these 32-bit offsets: no per-stage
-// address arithmetic in the vector ALU. BM * nb * 34 < 2^32 for any k the
-// library takes (nb < 2^20).
+// address arithmetic in the vector ALU. BM * nb * 34 < 2^32 for every k up to
+// kMaxTiledK (mfma_supported declines longer rows).
 template <class C>
 struct LoadOffsets {
     uint32_t a[C::kActPT];
@@ -433,6 +433,7 @@ int64_t tiles_of(int64_t m, int64_t n, int64_t bm, int64_t bn) { return ((m + bm
 
 bool mfma_supported(int type, int64_t m, int64_t k) {
     (void)m;
+    if (k > kMaxTiledK) return false;  // 32-bit load offsets
     if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) return k % (32 * 4) == 0;  // Q40Small4 takes any k % 128 == 0
     // the super-block formats take any k % 256 == 0 (gemm_kquant.hip)
     return (type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K || type == PFNG_WEIGHT_IQ2_XXS_ACTIVATION_Q8_K) && k % 256 == 0;

@@ -829,7 +829,7 @@ hipError_t launch_fused_gemv(int type, const void *w, const float *x, float *c, 
 }
 
 bool gemv_supported(int type, int64_t m, int64_t k) {
-    if (m < 1) return false;
+    if (m < 1 || k > kMaxTiledK) return false;  // 32-bit load offsets
     const bool pairs = k % 64 == 0 && pairs_lds_bytes(m, k / 32) <= kPairsMaxLds;
     if (type == PFNG_WEIGHT_Q4_0_ACTIVATION_Q8_0) {
         if (m == 1) return k % 64 == 0;

@@ -7,6 +7,13 @@
 
 namespace pfng {
 
+// Longest rows the tiled (GEMV and MFMA) kernels take. Their loads address
+// from a tile's first row with 32-bit byte offsets (tile row * row bytes):
+// at k = 2^24 the largest is 127 * 65536 * 292 = 2.43e9 (q8_K, 128-row tiles)
+// and 127 * 524288 * 34 = 2.26e9 (q8_0), below 2^32. Longer rows run only on
+// the naive path.
+constexpr int64_t kMaxTiledK = int64_t(1) << 24;
+
 // quantize.hip
 hipError_t launch_quantize_q8_0(const float *x, void *y, int64_t rows, int64_t k, hipStream_t stream);
 hipError_t launch_quantize_q8_K(const float *x, void *y, int64_t rows, int64_t k, hipStream_t stream);

@@ -107,6 +107,38 @@ def test_auto_path_query(pkg, qtype, m, n, k, expect):
         assert pkg.last_error()
 
 
+@pytest.mark.parametrize("qtype,m", [(0, 1), (0, 16), (0, 100), (0, 480), (1, 1), (1, 40), (1, 480), (2, 8), (2, 512)])
+def test_tiled_paths_stop_at_the_32_bit_offset_limit(pkg, qtype, m):
+    """The tiled kernels address a tile's rows with 32-bit byte offsets, valid
+    up to k = 2^24: the automatic path takes k = 2^24 and declines the next
+    valid k (only the naive path runs it), naming the limit."""
+    limit = 1 << 24
+    assert pkg.auto_path(qtype, m, 64, limit) in (1, 2)
+    assert pkg.auto_path(qtype, m, 64, limit + 256) == -1
+    assert "k <= 16777216" in pkg.last_error()
+    L = pkg.lib()
+    p = ctypes.c_void_p(256)
+    for path in (1, 2):
+        assert L.pfng_hip_mul_mat(qtype, p, p, p, m, 64, limit + 256, path, None) == pkg.ERR_UNSUPPORTED
+        assert "k <= 16777216" in pkg.last_error()
+
+
+@pytest.mark.parametrize("qtype,m,k,path,text", [
+    (0, 17, 96, 0, "m = 9..64 (k < 2048) or 9..128 at k%256==0 from k = 512"),
+    (0, 129, 4096, 1, "the q4_0 GEMV takes m == 1 at k%64==0"),
+    (1, 129, 8192, 1, "m = 9..64 at k = 1024 and 9..128 at k%1024==0"),
+    (2, 17, 5120, 1, "m = 9..128 at k%2048==0"),
+    (0, 17, 96, 2, "the q4_0 MFMA GEMM takes k%128==0"),
+])
+def test_declined_shapes_name_the_rules(pkg, qtype, m, k, path, text):
+    """A declined shape's message states the shapes the paths do take (the GEMV
+    runs up to m = 128 at the tiles' k, not only m <= 16)."""
+    p = ctypes.c_void_p(256)
+    assert pkg.lib().pfng_hip_mul_mat(qtype, p, p, p, m, 64, k, path, None) == pkg.ERR_UNSUPPORTED
+    assert text in pkg.last_error(), pkg.last_error()
+    assert "m<=16" not in pkg.last_error()
+
+
 def test_workspace_size(pkg):
     L = pkg.lib()
     assert L.pfng_hip_compute_workspace_size(0, 3, 64) == 3 * 2 * 34

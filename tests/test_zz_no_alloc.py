@@ -24,7 +24,13 @@ def test_noalloc_rejects_shapes_beyond_the_scratch(pkg):
     assert L.pfng_hip_compute_noalloc(1, fake, fake, fake, 4096, 8, 4096, 0, None) == pkg.ERR_INVALID_ARGUMENT
     assert L.pfng_hip_compute_noalloc(0, fake, fake, fake, 4, 8, 48, 0, None) == pkg.ERR_INVALID_ARGUMENT
     assert L.pfng_hip_compute_noalloc(0, fake, fake, fake, 0, 8, 64, 0, None) == pkg.OK
-    assert L.pfng_hip_compute_workspace_size(0, 2048, 4096) <= SCRATCH_BYTES < L.pfng_hip_compute_workspace_size(0, 4096, 4096)
+    # the boundary at k = 4096: 3855 rows take 16,776,960 bytes, 3856 rows 16,781,312
+    assert L.pfng_hip_compute_workspace_size(0, 3855, 4096) <= SCRATCH_BYTES < L.pfng_hip_compute_workspace_size(0, 3856, 4096)
+    assert L.pfng_hip_compute_noalloc(0, fake, fake, fake, 3856, 8, 4096, 0, None) == pkg.ERR_INVALID_ARGUMENT
+    assert "16781312 bytes" in pkg.last_error()
+    # 3855 rows pass the size check (here, with no device, the next step fails instead)
+    rc = L.pfng_hip_compute_noalloc(0, fake, fake, fake, 3855, 8, 4096, 0, None)
+    assert rc != pkg.ERR_INVALID_ARGUMENT or "static scratch" not in pkg.last_error()
 
 
 # (qtype, m, n, k, variant): each type's first call fills more of the scratch
@@ -55,10 +61,11 @@ def test_noalloc_matches_compute(hip, torch_gpu):
 
 @pytest.mark.gpu
 def test_noalloc_largest_shape_and_naive_path(hip, torch_gpu):
-    """The largest q4_0 shape the scratch takes at k = 4096 (2048 rows, c4's),
-    then a small call on the naive path: both equal pfng_hip_compute."""
+    """The largest q4_0 shape the scratch takes at k = 4096 (3855 rows, all
+    but 256 bytes of it), then a small call on the naive path: both equal
+    pfng_hip_compute."""
     torch = torch_gpu
-    for m, n, k, path in ((2048, 64, 4096, hip.PATH_AUTO), (3, 40, 512, hip.PATH_NAIVE)):
+    for m, n, k, path in ((3855, 64, 4096, hip.PATH_AUTO), (3, 40, 512, hip.PATH_NAIVE)):
         print(f"[case] compute_noalloc q4_0 {m}x{n}x{k} path={path}", flush=True)
         act, w = hip.create_input(0, m, n, k, seed=11, variant=0)
         a_t = torch.from_numpy(act).cuda()
@@ -67,3 +74,32 @@ def test_noalloc_largest_shape_and_naive_path(hip, torch_gpu):
         got = hip.compute_noalloc(0, a_t, w_t, n, path=path)
         torch.cuda.synchronize()
         assert np.array_equal(got.cpu().numpy().view(np.uint32), expect.cpu().numpy().view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_noalloc_under_graph_capture(hip, torch_gpu):
+    """compute_noalloc captured into a graph (the scratch address was resolved
+    by pfng_hip_device_check before): every replay, with other eager work and
+    synchronizations between replays, equals pfng_hip_compute bit for bit. The
+    fused (m = 1) and the separate-quantize (m = 24) forms."""
+    torch = torch_gpu
+    for qtype, m, n, k in ((0, 1, 512, 4096), (0, 24, 256, 2048), (1, 24, 256, 2048)):
+        print(f"[case] compute_noalloc graph type={qtype} {m}x{n}x{k}", flush=True)
+        act, w = hip.create_input(qtype, m, n, k, seed=5, variant=0)
+        a_t = torch.from_numpy(act).cuda()
+        w_t = torch.from_numpy(np.ascontiguousarray(w)).cuda()
+        expect = hip.compute(qtype, a_t, w_t, n)
+        out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            hip.compute_noalloc(qtype, a_t, w_t, n, out=out)
+        for _ in range(3):
+            out.zero_()
+            hip.compute(qtype, a_t[: max(1, m // 2)].contiguous(), w_t, n)  # other work through the same kernels
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(out.cpu().numpy().view(np.uint32), expect.cpu().numpy().view(np.uint32))
