@@ -8,9 +8,16 @@
 // direct-to-LDS buffer loads, 1 KB per instruction and no vector ALU work per
 // copy: L2 -> LDS moves long runs several times faster than row-strided
 // pieces (measured: 68-byte row pieces by 4-byte lanes ~18 B/clk/CU, long
-// 16-byte runs ~73 B/clk/CU). Rows are laid out in LDS as in memory, each
-// padded to an odd number of 16-byte chunks, so the 32 lanes reading one row
-// each meet at most one other lane per bank.
+// 16-byte runs ~73 B/clk/CU; a phase-major layout with 144- and 272-byte row
+// pieces of 16-byte lanes cost 1.1 us more at 480x1536x1536). Rows are laid
+// out in LDS as in memory, each padded to an odd number of 16-byte chunks, and
+// row r's data starts s(r) = (r % 32) / 8 dwords into its first chunk (the
+// copy fetches each chunk 4 s(r) bytes early). The fragment reads are dwords,
+// 32 lanes on 32 rows; the LDS serves them 32 lanes at a time over 32 banks.
+// With the row stride an odd number of chunks (4 mod 8 dwords) rows r = 0..7
+// land on distinct multiples of 4 and the shift fills the banks in between,
+// so every read is conflict-free (without the shift four lanes shared each
+// bank: 8.45 against 7.38 us at 480x1536x1536).
 // Compute: wave w takes column tile w % TN and block pairs
 // [(w / TN)*PPW, (w / TN + 1)*PPW) of its rows (K slice w / TN of WS). Per
 // block: S16 = v_mfma_i32_32x32x32_i8 (exact 16*S_b) on the raw bytes (the
@@ -47,9 +54,10 @@ struct WtConfig {
     static_assert(NB % 8 == 0, "a row is whole 16-byte chunks (8 blocks)");
     static_assert((NB / 2) % WS == 0, "every wave takes whole block pairs");
     static constexpr int kPPW = NB / 2 / WS;  // block pairs per wave
-    // 16-byte chunks of a row: data, and the LDS row made odd
+    // 16-byte chunks of a row: data, and the LDS row: at least one more (the
+    // shifted row's end), an odd number
     static constexpr int kDataA = NB * 34 / 16, kDataW = NB * 18 / 16;
-    static constexpr int kChunksA = kDataA | 1, kChunksW = kDataW | 1;
+    static constexpr int kChunksA = (kDataA + 1) | 1, kChunksW = (kDataW + 1) | 1;
     static constexpr int kRowsW = 32 * TN;
     static constexpr int kCopiesA = (32 * kChunksA + 63) / 64;  // 64 chunks per copy instruction
     static constexpr int kCopiesW = (kRowsW * kChunksW + 63) / 64;
@@ -60,20 +68,27 @@ struct WtConfig {
     static_assert(4 * kGroupBytes <= kBytesW, "partial tiles fit in the weight buffer");
 };
 
+// dword shift of tile row r inside its LDS row
+__device__ __forceinline__ int row_skew(int r) { return (r & 31) >> 3; }
+
 // Byte offset in memory (from the tile's first row) of this lane's chunk in
-// copy instruction j of a region of `rows` LDS rows of C chunks, the first D
-// of them data (the rest padding, a copy of the row's last data chunk);
-// lanes past the region repeat its last chunk, rows past `rows_valid` repeat
-// the last valid row.
+// copy instruction j of a region of `rows` LDS rows of C chunks (D of data,
+// C > D): LDS chunk (r, col) holds the row's bytes [16 col - 4 s(r), +16), so
+// the last chunk carries the end of the shifted row. Lanes past the region
+// repeat its last chunk, rows past `rows_valid` repeat the last valid row
+// (shifted like the row whose place they fill), offsets before the tile are
+// clamped to it, and offsets past the buffer's end read zeros (the buffer
+// resource is bounded).
 template <int C, int D>
 __device__ __forceinline__ uint32_t chunk_source(int j, int lane, int rows, int rows_valid) {
+    static_assert(C > D, "room for the shifted row");
     int i = 64 * j + lane;
     if (i >= rows * C) i = rows * C - 1;
     const int r = i / C;
-    int col = i - r * C;
-    if (col >= D) col = D - 1;
+    const int col = i - r * C;
     const int rr = r < rows_valid ? r : rows_valid - 1;
-    return (uint32_t)rr * (uint32_t)(D * 16) + (uint32_t)col * 16u;
+    const int off = rr * (D * 16) + col * 16 - 4 * row_skew(r);
+    return (uint32_t)(off > 0 ? off : 0);
 }
 
 // This wave's copy instructions (activation rows into bufa, weight rows
@@ -101,8 +116,8 @@ __device__ __forceinline__ void compute_slice(const uint8_t *bufa, const uint8_t
                                               f32x16 &acc, int32_t *isums, int m, int n, int nb, int m0, int n0) {
     const int li = lane & 31, h = lane >> 5;
     const uint32_t keep = h ? 0u : 0xffffffffu;  // K-half 1 lanes feed zeros to the scale products
-    const uint32_t *arow = reinterpret_cast<const uint32_t *>(bufa) + li * Cfg::kChunksA * 4;
-    const uint32_t *wrow = reinterpret_cast<const uint32_t *>(bufw) + (tile * 32 + li) * Cfg::kChunksW * 4;
+    const uint32_t *arow = reinterpret_cast<const uint32_t *>(bufa) + li * Cfg::kChunksA * 4 + row_skew(li);
+    const uint32_t *wrow = reinterpret_cast<const uint32_t *>(bufw) + (tile * 32 + li) * Cfg::kChunksW * 4 + row_skew(li);
 #pragma unroll
     for (int pp = 0; pp < Cfg::kPPW; ++pp) {
         const int lp = slice * Cfg::kPPW + pp;  // pair within the row
