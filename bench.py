@@ -393,10 +393,11 @@ def main():
     log(f"[bench] side GEMV items: {side} timed launches per sample")
     gemv_kq, decode = [], []
     if side > 0:
-        for qt, name, variant in ((1, "q4_K", ref), (2, "iq2_xxs", base)):
+        for qt, name, variant, kname in ((1, "q4_K", ref, "gemv_q4_K_kernel<1, true>"),
+                                         (2, "iq2_xxs", base, "gemv_iq2_xxs_kernel<1>")):
             gemv_kq.append(measure(torch, pkg, f"m1_{name}: {name} x q8_K GEMV M=1 N=4096 K=4096, {COPIES} rotating "
                                    "weight copies", qt, 1, 4096, 4096, side, max(side // 10, 32), samples, variant,
-                                   f"gemv_{name}_kernel<1>", copies=COPIES))
+                                   kname, copies=COPIES))
         # at K = 4096 the 16x16 MFMA tile GEMVs run from M = 6 (q4_0), 5 (q4_K)
         # and 9 (iq2_xxs; M = 5..8 the two-half-copy kernel), over C = M / 16
         # chunks of 16 activation rows

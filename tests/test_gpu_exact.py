@@ -79,6 +79,9 @@ GEMV_CASES = [
     (1, 5, 100, 8192, "gemv_q4_K_mfma_chunk_kernel<1>, 2 rounds"),
     (1, 40, 64, 14336, "gemv_q4_K_mfma_chunk_kernel<3>, 3.5 rounds"),
     (2, 1, 4096, 4096, "gemv_iq2_xxs_kernel<1>"),
+    (2, 1, 300, 2560, "gemv_iq2_xxs_kernel<1>, a partial second step"),
+    (2, 1, 100, 1792, "gemv_iq2_xxs_kernel<1>, one partial step"),
+    (2, 1, 64, 65536, "gemv_iq2_xxs_kernel<1>, 32 steps"),
     (2, 2, 4096, 4096, "gemv_iq2_xxs_staged_kernel<2>"),
     (2, 4, 300, 4096, "gemv_iq2_xxs_staged_kernel<4>"),
     (2, 9, 100, 1536, "gemv_iq2_xxs_staged_kernel<9> (k % 2048 != 0)"),
