@@ -177,6 +177,9 @@ int pfng_hip_compute_noalloc(int type, const float *activation, const void *weig
  *   q4_0   : out[(m*n + n)*(k/32) + b]     = sum (q_w - 8) * q_a over block b
  *   q4_K   : out[((m*n+n)*(k/256) + b)*2]  = sum_j sc_j*S_j, [..+1] = sum_j min_j*(bsum_2j+bsum_2j+1)
  *   iq2_xxs: out[(m*n + n)*(k/256) + b]    = sum_j (2 s_j + 1) * S_j
+ * Where PFNG_PATH_MFMA runs q4_K on whole-K tiles (k = 1024 or 1536), which
+ * split super-blocks between K slices and join the parts only in fp32, the
+ * sums come from the 64 x 64 two-slice tiles that shape would otherwise take.
  * For verification at small sizes; not a performance path. */
 int pfng_hip_block_isums(int type, const void *weight, const void *act_q, int32_t *out, int64_t m, int64_t n,
                          int64_t k, void *stream);

@@ -223,6 +223,35 @@ __device__ __forceinline__ f32x16 mfma_f16_32x32x16(f16x8 a, f16x8 b, f32x16 c) 
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// q4_K scale and min of sub-block j (0..7) from the 12 packed bytes (hd[1..3];
+// hd[0] holds d and dmin), with the reference's decode
+// (llama_reference.cpp:116-121).
+__device__ __forceinline__ void q4_K_scale_min(const uint32_t hd[4], int j, uint32_t &sc, uint32_t &mn) {
+    auto byte = [&](int i) { return (hd[1 + i / 4] >> (8 * (i % 4))) & 0xffu; };
+    if (j < 4) {
+        sc = byte(j) & 63;
+        mn = byte(j + 4) & 63;
+    } else {
+        sc = (byte(j + 4) & 15) | ((byte(j - 4) >> 6) << 4);
+        mn = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+    }
+}
+
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+// Bytes of v (each 0..15) times the digit in both 16-bit halves of digit2
+// (0..7): one packed 16-bit multiply per dword, and no byte product (<= 105)
+// carries into the next byte.
+__device__ __forceinline__ i32x4 mul_planes(i32x4 v, uint32_t digit2) {
+    i32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const u16x2 x = __builtin_bit_cast(u16x2, (uint32_t)v[i]) * __builtin_bit_cast(u16x2, digit2);
+        o[i] = (int32_t)__builtin_bit_cast(uint32_t, x);
+    }
+    return o;
+}
+
 // XCD-aware tile order for a 1-D grid of mt x nt output tiles. Workgroup ids
 // are dealt round-robin to MI355X's 8 XCDs (id % 8), each with its own L2;
 // regroup them so that each XCD owns a contiguous range of tiles, walked

@@ -41,8 +41,6 @@ namespace pfng {
 
 namespace {
 
-typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
-
 __constant__ uint16_t kIq2GridCodes[256] = PFNG_IQ2XXS_GRID_CODES_INIT;
 
 enum class Kq { Q4K, IQ2 };
@@ -201,19 +199,6 @@ __device__ __forceinline__ void kq_load(const uint8_t *__restrict__ a_t, const u
     }
 }
 
-// q4_K scale and min of sub-block j (0..7) from the 12 packed bytes, with the
-// reference's decode (llama_reference.cpp:116-121).
-__device__ __forceinline__ void q4_K_scale_min(const uint32_t hd[4], int j, uint32_t &sc, uint32_t &mn) {
-    auto byte = [&](int i) { return (hd[1 + i / 4] >> (8 * (i % 4))) & 0xffu; };
-    if (j < 4) {
-        sc = byte(j) & 63;
-        mn = byte(j + 4) & 63;
-    } else {
-        sc = (byte(j + 4) & 15) | ((byte(j - 4) >> 6) << 4);
-        mn = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
-    }
-}
-
 template <class C>
 __device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int h, int tid, const KqRegs<C> &r) {
     const uint8_t *signs = grid + (C::kSigns - C::kGrid);
@@ -310,16 +295,6 @@ struct KqAcc {
     i32x16 s1[C::TM][C::TN];   // q4_K: S_H; iq2_xxs: S_HI
     f32x16 im[C::TM][C::TN];   // q4_K: IM (exact integers)
 };
-
-__device__ __forceinline__ i32x4 mul_planes(i32x4 v, uint32_t digit2) {
-    i32x4 o;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const u16x2 x = __builtin_bit_cast(u16x2, (uint32_t)v[i]) * __builtin_bit_cast(u16x2, digit2);
-        o[i] = (int32_t)__builtin_bit_cast(uint32_t, x);
-    }
-    return o;
-}
 
 // Sub-block sums of one stage (half H of the super-block) for one wave: its
 // kWaveSub sub-blocks tb .. tb + kWaveSub - 1 (tb a multiple of kWaveSub).
@@ -656,7 +631,7 @@ using KqBigS2 = KqConfig<T, 128, 64, 2, 2, 1, 2>;
 template <Kq T>
 using KqSmallS2 = KqConfig<T, 64, 64, 2, 2, 1, 2>;
 
-enum { kCfgBig = 0, kCfgTiny = 2, kCfgMid = 3, kCfgMid2 = 4, kCfgBigS2 = 5, kCfgSmallS2 = 6 };
+enum { kCfgBig = 0, kCfgTiny = 2, kCfgMid = 3, kCfgMid2 = 4, kCfgBigS2 = 5, kCfgSmallS2 = 6, kCfgWhole = 7 };
 
 int64_t tiles_of(int64_t m, int64_t n, int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); }
 
@@ -669,6 +644,7 @@ hipError_t dispatch(const void *w, const void *a, float *c, const MfmaPlan &plan
     case kCfgMid2: return launch_kq<KqMid2<T>, false>(w, a, c, nullptr, m, n, k, stream);
     case kCfgBigS2: return launch_kq<KqBigS2<T>, false>(w, a, c, nullptr, m, n, k, stream);
     case kCfgSmallS2: return launch_kq<KqSmallS2<T>, false>(w, a, c, nullptr, m, n, k, stream);
+    case kCfgWhole: return launch_q4_K_small(w, a, c, m, n, k, stream);
     default: return launch_kq<KqTiny<T>, false>(w, a, c, nullptr, m, n, k, stream);
     }
 }
@@ -676,19 +652,26 @@ hipError_t dispatch(const void *w, const void *a, float *c, const MfmaPlan &plan
 }  // namespace
 
 // Tile choice (measured on MI355X, 256 CUs, n = 4096 and the baseline
-// shapes): 128 x 64 tiles at two or more per CU; with 2 super-block slices at
-// one or more per CU (c3); 64 x 64 tiles with 2 slices from half a tile per CU
-// (q4_K) or three quarters (iq2_xxs) (c2: 9.1 instead of 11.3 us); below that
-// the 32 x 32 tile with the most slices (4, 2, 1) that keeps the waves at or
-// under 8 per CU (more slices only added barrier and staging work).
+// shapes): q4_K at k = 1024 or 1536 with half to one 32 x 96 tile per CU: the
+// whole-K tiles of gemm_small.hip (c2: 7.60 against 8.59 us for the 64 x 64
+// tiles with 2 slices); 128 x 64 tiles at two or more per CU; with 2
+// super-block slices at one or more per CU (c3); 64 x 64 tiles with 2 slices
+// from half a tile per CU (q4_K) or three quarters (iq2_xxs) (c2 before the
+// whole-K tiles: 9.1 instead of 11.3 us); below that the 32 x 32 tile with the
+// most slices (4, 2, 1) that keeps the waves at or under 8 per CU (more slices
+// only added barrier and staging work). The block-sum diagnostic of the
+// whole-K plan reports the 64 x 64 two-slice tiles' sums (the whole-K tiles
+// split super-blocks between K slices and add the parts only in fp32).
 MfmaPlan plan_kquant(int type, int64_t m, int64_t n, int64_t k, int cus) {
-    (void)k;
     MfmaPlan p;
     const int64_t c = cus;
     const bool q4k = type == PFNG_WEIGHT_Q4_K_ACTIVATION_Q8_K;
     const int64_t wk = q4k ? 2 : 1;  // KqTiny's K-waves
     const int64_t t32 = tiles_of(m, n, 32, 32), t64 = tiles_of(m, n, 64, 64), t128 = tiles_of(m, n, 128, 64);
-    if (t128 >= 2 * c)
+    const int64_t t96 = tiles_of(m, n, 32, 96);
+    if (q4k && q4_K_small_supported(k) && 2 * t96 >= c && t96 <= c)
+        p.config = kCfgWhole;
+    else if (t128 >= 2 * c)
         p.config = kCfgBig;
     else if (t128 >= c)
         p.config = kCfgBigS2;
@@ -723,7 +706,8 @@ hipError_t dispatch_isums(const void *w, const void *a, int32_t *out, const Mfma
     switch (plan.config) {
     case kCfgBig: return launch_kq<KqIsums<KqBig<T>>, true>(w, a, nullptr, out, m, n, k, stream);
     case kCfgBigS2: return launch_kq<KqIsums<KqBigS2<T>>, true>(w, a, nullptr, out, m, n, k, stream);
-    case kCfgSmallS2: return launch_kq<KqIsums<KqSmallS2<T>>, true>(w, a, nullptr, out, m, n, k, stream);
+    case kCfgSmallS2:
+    case kCfgWhole: return launch_kq<KqIsums<KqSmallS2<T>>, true>(w, a, nullptr, out, m, n, k, stream);
     case kCfgMid: return launch_kq<KqIsums<KqMid<T>>, true>(w, a, nullptr, out, m, n, k, stream);
     case kCfgMid2: return launch_kq<KqIsums<KqMid2<T>>, true>(w, a, nullptr, out, m, n, k, stream);
     default: return launch_kq<KqIsums<KqTiny<T>>, true>(w, a, nullptr, out, m, n, k, stream);

@@ -79,16 +79,23 @@ __device__ __forceinline__ int row_skew(int r) { return (r & 31) >> 3; }
 // (shifted like the row whose place they fill), offsets before the tile are
 // clamped to it, and offsets past the buffer's end read zeros (the buffer
 // resource is bounded).
-template <int C, int D>
-__device__ __forceinline__ uint32_t chunk_source(int j, int lane, int rows, int rows_valid) {
-    static_assert(C > D, "room for the shifted row");
+// Rows RB bytes apart in memory (the q4_0 rows are whole chunks, RB = 16 D);
+// kSkew false: no shift (rows read as 16-byte fragments).
+template <int C, int RB, bool kSkew>
+__device__ __forceinline__ uint32_t chunk_source_rb(int j, int lane, int rows, int rows_valid) {
+    static_assert(16 * C >= RB + (kSkew ? 12 : 0), "room for the (shifted) row");
     int i = 64 * j + lane;
     if (i >= rows * C) i = rows * C - 1;
     const int r = i / C;
     const int col = i - r * C;
     const int rr = r < rows_valid ? r : rows_valid - 1;
-    const int off = rr * (D * 16) + col * 16 - 4 * row_skew(r);
+    const int off = rr * RB + col * 16 - (kSkew ? 4 * row_skew(r) : 0);
     return (uint32_t)(off > 0 ? off : 0);
+}
+template <int C, int D>
+__device__ __forceinline__ uint32_t chunk_source(int j, int lane, int rows, int rows_valid) {
+    static_assert(C > D, "room for the shifted row");
+    return chunk_source_rb<C, D * 16, true>(j, lane, rows, rows_valid);
 }
 
 // This wave's copy instructions (activation rows into bufa, weight rows
@@ -236,9 +243,215 @@ hipError_t launch_wt_any(const void *w, const void *a, float *c, int32_t *isums,
                  : launch_wt<TN, WS, NB, false>(w, a, c, isums, m, n, stream);
 }
 
+// ---------------------------------------------------------------------------
+// q4_K x q8_K with the whole K range in LDS (k = 1024 or 1536, e.g.
+// 480x1536x1536): the q4_0 tile's plan for the super-block format. Per 32 x 96
+// tile the 32 activation rows (q8_K blocks as in memory, each row shifted by
+// s(r) dwords, read as dwords like the q4_0 rows) and the 96 weight rows (q4_K
+// blocks as in memory, unshifted: 16-byte aligned, read as 16-byte fragments;
+// an odd number of chunks per row keeps rows 0..7 of a fragment read on
+// distinct banks) are copied into LDS once; then a table of the activation
+// scales, [block][row].
+// 12 waves = 4 K slices x 3 column tiles; slice S takes sub-blocks
+// [S * 2 NB, (S + 1) * 2 NB) of the row's 8 NB, so a slice ends inside a
+// super-block where NB is odd (the q4_K accuracy bound is per element, so a
+// super-block's partial sums may be scaled separately). Per super-block part,
+// as gemm_kquant.hip's q4_K tiles: sc = 8 h + l, two int8 MFMAs per sub-block on
+// the planes q * l and q * h (IS = 8 S_H + S_L), IM = sum_j m_j (bsum_2j +
+// bsum_2j+1) by one fp16 MFMA (mins of the sub-blocks outside the part are
+// zero), then acc += ad * (d * IS - dmin * IM). The slices' partial tiles are
+// added through LDS in slice order.
+template <int NB>
+struct KtConfig {
+    static constexpr int TN = 3, WS = 4, WK = WS * TN, kThreads = 64 * WK;
+    static constexpr int kRowA = NB * 292, kRowW = NB * 144;
+    static constexpr int kChunksA = ((kRowA + 12 + 15) / 16) | 1;  // shifted by up to 12 bytes
+    static constexpr int kChunksW = ((kRowW + 15) / 16) | 1;
+    static constexpr int kRowsW = 32 * TN;
+    static constexpr int kCopiesA = (32 * kChunksA + 63) / 64;
+    static constexpr int kCopiesW = (kRowsW * kChunksW + 63) / 64;
+    static constexpr int kCopiesPerWave = (kCopiesA + kCopiesW + WK - 1) / WK;
+    static constexpr int kBytesA = kCopiesA * 1024, kBytesW = kCopiesW * 1024;
+    static constexpr int kSubs = NB * 8 / WS;  // sub-blocks of one K slice
+    static constexpr int kGroupBytes = WK * 64 * 16;
+    static_assert(NB * 8 % WS == 0, "K slices of whole sub-blocks");
+    static_assert(4 * kGroupBytes <= kBytesW, "partial tiles fit in the weight buffer");
+    static_assert(kBytesA + kBytesW + NB * 32 * 4 <= 160 * 1024, "tile must fit in LDS");
+};
+
+template <class Cfg>
+__device__ __forceinline__ void kt_copy_tile(uint8_t *bufa, uint8_t *bufw, __amdgpu_buffer_rsrc_t ra,
+                                             __amdgpu_buffer_rsrc_t rw, int wave, int lane, int rows_a, int rows_w) {
+    constexpr int kTotal = Cfg::kCopiesA + Cfg::kCopiesW;
+#pragma unroll
+    for (int i = 0; i < Cfg::kCopiesPerWave; ++i) {
+        int j = wave + i * Cfg::WK;
+        if (j >= kTotal) j = kTotal - 1;
+        if (j < Cfg::kCopiesA)
+            copy16_to_lds(ra, bufa + j * 1024,
+                          chunk_source_rb<Cfg::kChunksA, Cfg::kRowA, true>(j, lane, 32, rows_a));
+        else
+            copy16_to_lds(rw, bufw + (j - Cfg::kCopiesA) * 1024,
+                          chunk_source_rb<Cfg::kChunksW, Cfg::kRowW, false>(j - Cfg::kCopiesA, lane, Cfg::kRowsW,
+                                                                             rows_w));
+    }
+}
+
+// Slice S of the wave's column tile into acc.
+template <class Cfg, int NB, int S>
+__device__ __forceinline__ void kt_compute(const uint8_t *bufa, const uint8_t *bufw, const float *adt, int tile,
+                                           int lane, f32x16 &acc) {
+    constexpr int s0 = S * Cfg::kSubs, s1 = s0 + Cfg::kSubs;
+    const int li = lane & 31, lh = lane >> 5;
+    const uint32_t *arow = reinterpret_cast<const uint32_t *>(bufa) + li * Cfg::kChunksA * 4 + row_skew(li);
+    const uint8_t *wrow = bufw + (tile * 32 + li) * Cfg::kChunksW * 16;
+#pragma unroll
+    for (int sb = s0 / 8; sb <= (s1 - 1) / 8; ++sb) {
+        const int ja = s0 > 8 * sb ? s0 - 8 * sb : 0, jb = s1 < 8 * sb + 8 ? s1 - 8 * sb : 8;
+        const uint4 hdv = *reinterpret_cast<const uint4 *>(wrow + sb * 144);
+        const uint32_t hd[4] = {hdv.x, hdv.y, hdv.z, hdv.w};
+        i32x16 sl = {}, sh = {};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (j < ja || j >= jb) continue;
+            // activation bytes 16 lh .. 16 lh + 15 of sub-block j (dword-aligned)
+            const uint32_t *ap = arow + sb * 73 + 1 + 8 * j + 4 * lh;
+            const i32x4 av = (i32x4){(int)ap[0], (int)ap[1], (int)ap[2], (int)ap[3]};
+            // the nibble bytes of pair j / 2: low nibbles sub-block j even, high odd
+            const uint4 wq = *reinterpret_cast<const uint4 *>(wrow + sb * 144 + 16 + 32 * (j / 2) + 16 * lh);
+            const uint32_t sh4 = (j & 1) ? 4u : 0u;
+            const i32x4 nib = (i32x4){(int)((wq.x >> sh4) & 0x0f0f0f0fu), (int)((wq.y >> sh4) & 0x0f0f0f0fu),
+                                      (int)((wq.z >> sh4) & 0x0f0f0f0fu), (int)((wq.w >> sh4) & 0x0f0f0f0fu)};
+            uint32_t sc, mn;
+            q4_K_scale_min(hd, j, sc, mn);
+            const bool first = j == ja;
+            sl = mfma_i8_32x32x32(av, mul_planes(nib, (sc & 7u) * 0x10001u), first ? (i32x16){} : sl);
+            sh = mfma_i8_32x32x32(av, mul_planes(nib, (sc >> 3) * 0x10001u), first ? (i32x16){} : sh);
+        }
+        // IM: lane supplies the bsums 8 lh .. 8 lh + 7 of row li (sub-blocks
+        // 4 lh .. 4 lh + 3) and the mins of column li for those sub-blocks,
+        // each twice (exact: |bsum| <= 2032 and m <= 63 are fp16 integers)
+        const uint32_t *bp = arow + sb * 73 + 65 + 4 * lh;
+        f16x8 bs, mv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t v = bp[i];
+            bs[2 * i] = (_Float16)(float)(int16_t)(v & 0xffffu);
+            bs[2 * i + 1] = (_Float16)(float)(int16_t)(v >> 16);
+            uint32_t scl, mnl, sch, mnh;
+            q4_K_scale_min(hd, i, scl, mnl);
+            q4_K_scale_min(hd, 4 + i, sch, mnh);
+            const float ml = (i >= ja && i < jb) ? (float)mnl : 0.0f;
+            const float mh = (4 + i >= ja && 4 + i < jb) ? (float)mnh : 0.0f;
+            const _Float16 mm = (_Float16)(lh ? mh : ml);
+            mv[2 * i] = mm;
+            mv[2 * i + 1] = mm;
+        }
+        const f32x16 im = mfma_f16_32x32x16(bs, mv, (f32x16){});
+        const float d = fp16_to_f32(hd[0] & 0xffffu), dmin = fp16_to_f32(hd[0] >> 16);
+        // activation scales of the lane's 16 rows: rows 8 g + 4 lh + 0..3
+        const float *adp = adt + sb * 32 + 4 * lh;
+        f32x4 ad4[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) ad4[g] = *reinterpret_cast<const f32x4 *>(adp + 8 * g);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int is = 8 * sh[q] + sl[q];
+            const float x = fmaf(-dmin, im[q], d * (float)is);
+            acc[q] = fmaf(ad4[q / 4][q % 4], x, acc[q]);
+        }
+    }
+}
+
+template <int NB>
+__global__ __launch_bounds__(KtConfig<NB>::kThreads) void gemm_q4_K_wt_kernel(const uint8_t *__restrict__ w,
+                                                                             const uint8_t *__restrict__ a,
+                                                                             float *__restrict__ c, int m, int n) {
+    using Cfg = KtConfig<NB>;
+    __shared__ __align__(16) uint8_t a0[Cfg::kBytesA], w0[Cfg::kBytesW];
+    __shared__ __align__(16) float adt[NB * 32];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const TileOrigin to = xcd_tile(blockIdx.x, (m + 31) / 32, (n + Cfg::kRowsW - 1) / Cfg::kRowsW);
+    const int m0 = to.mi * 32, n0 = to.ni * Cfg::kRowsW;
+    const int tile = wave % Cfg::TN, slice = wave / Cfg::TN;
+
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a + (size_t)m0 * Cfg::kRowA), 0, (int)((uint32_t)(m - m0) * (uint32_t)Cfg::kRowA), kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(w + (size_t)n0 * Cfg::kRowW), 0, (int)((uint32_t)(n - n0) * (uint32_t)Cfg::kRowW), kBufferWord3);
+    const int rows_a = m - m0 < 32 ? m - m0 : 32;
+    const int rows_w = n - n0 < Cfg::kRowsW ? n - n0 : Cfg::kRowsW;
+    kt_copy_tile<Cfg>(a0, w0, ra, rw, wave, lane, rows_a, rows_w);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int t = threadIdx.x; t < NB * 32; t += Cfg::kThreads) {
+        const int b = t >> 5, r = t & 31;
+        adt[t] = *reinterpret_cast<const float *>(a0 + r * Cfg::kChunksA * 16 + 4 * row_skew(r) + b * 292);
+    }
+    __syncthreads();
+    f32x16 acc = (f32x16){};
+    switch (slice) {
+    case 0: kt_compute<Cfg, NB, 0>(a0, w0, adt, tile, lane, acc); break;
+    case 1: kt_compute<Cfg, NB, 1>(a0, w0, adt, tile, lane, acc); break;
+    case 2: kt_compute<Cfg, NB, 2>(a0, w0, adt, tile, lane, acc); break;
+    default: kt_compute<Cfg, NB, 3>(a0, w0, adt, tile, lane, acc); break;
+    }
+
+    // partial tiles to LDS as float4 register groups [group][wave][lane] (in
+    // the weight array, dead after the barrier), then each wave adds one group
+    // of one column tile over the K slices in order and stores it
+    __syncthreads();
+    auto group_base = [&](int g) -> float4 * { return reinterpret_cast<float4 *>(w0) + g * Cfg::WK * 64; };
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+        group_base(g)[wave * 64 + lane] = make_float4(acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]);
+    __syncthreads();
+    const int li = lane & 31;
+    for (int tg = wave; tg < Cfg::TN * 4; tg += Cfg::WK) {
+        const int t = tg % Cfg::TN, g = tg / Cfg::TN;
+        const float4 *pg = group_base(g);
+        float4 s = pg[t * 64 + lane];
+#pragma unroll
+        for (int sl = 1; sl < Cfg::WS; ++sl) {
+            const float4 v = pg[(sl * Cfg::TN + t) * 64 + lane];
+            s.x += v.x;
+            s.y += v.y;
+            s.z += v.z;
+            s.w += v.w;
+        }
+        const int col = n0 + t * 32 + li;
+        const float r[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = m0 + mfma_row(lane, 4 * g + i);
+            if (row < m && col < n) c[(size_t)row * n + col] = r[i];
+        }
+    }
+}
+
+template <int NB>
+hipError_t launch_kt(const void *w, const void *a, float *c, int64_t m, int64_t n, hipStream_t stream) {
+    using Cfg = KtConfig<NB>;
+    const dim3 grid((unsigned)(((m + 31) / 32) * ((n + Cfg::kRowsW - 1) / Cfg::kRowsW)));
+    hipLaunchKernelGGL((gemm_q4_K_wt_kernel<NB>), grid, dim3(Cfg::kThreads), 0, stream,
+                       static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(a), c, (int)m, (int)n);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 bool q4_0_small_supported(int64_t k) { return k == 1024 || k == 1536; }
+
+bool q4_K_small_supported(int64_t k) { return k == 1024 || k == 1536; }
+
+hipError_t launch_q4_K_small(const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
+                             hipStream_t stream) {
+    // 32 x 96 tiles, 12 waves: 4 K slices x 3 column tiles
+    if (k == 1536) return launch_kt<6>(w, a, c, m, n, stream);
+    if (k == 1024) return launch_kt<4>(w, a, c, m, n, stream);
+    return hipErrorInvalidValue;
+}
 
 hipError_t launch_q4_0_small(const void *w, const void *a, float *c, int32_t *isums, int64_t m, int64_t n,
                              int64_t k, hipStream_t stream) {

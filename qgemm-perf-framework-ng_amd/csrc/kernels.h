@@ -66,6 +66,10 @@ hipError_t launch_mfma_block_isums(int type, const void *w, const void *a, int32
 bool q4_0_small_supported(int64_t k);
 hipError_t launch_q4_0_small(const void *w, const void *a, float *c, int32_t *isums, int64_t m, int64_t n,
                              int64_t k, hipStream_t stream);
+// q4_K against q8_K with the same 32 x 96 whole-K tiles (k = 1024 or 1536)
+bool q4_K_small_supported(int64_t k);
+hipError_t launch_q4_K_small(const void *w, const void *a, float *c, int64_t m, int64_t n, int64_t k,
+                             hipStream_t stream);
 
 // gemm_kquant.hip — q4_K and iq2_xxs against q8_K
 MfmaPlan plan_kquant(int type, int64_t m, int64_t n, int64_t k, int cus);

@@ -146,6 +146,8 @@ GEMM_CASES = [
     (0, 100, 77, 256, None),
     (0, 200, 3072, 2048, 32),
     (1, 480, 1536, 1536, None),
+    (1, 470, 1500, 1536, None),
+    (1, 300, 2000, 1024, None),
     (1, 130, 65, 768, None),
     (1, 2048, 1024, 256, None),
     (2, 512, 4096, 4096, 32),

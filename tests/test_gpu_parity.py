@@ -351,6 +351,18 @@ def test_mfma_kquant(hip, torch_gpu, oracle, qtype, m, n, k):
     check_close(oracle, qtype, got, w, aq, m, n, k, label=f"mfma type={qtype} {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("m,n,k", [(470, 1500, 1536), (300, 2000, 1024), (480, 1536, 1536)])
+def test_mfma_q4_K_whole_k_tiles(hip, torch_gpu, oracle, m, n, k):
+    """Shapes the whole-K q4_K tiles take (k = 1024 or 1536, half to one 32 x 96
+    tile per CU), ragged edges included, against the oracle's bound."""
+    torch = torch_gpu
+    say(f"q4_K whole-K tiles {m}x{n}x{k}")
+    act, w = oracle.create_input(1, m, n, k, seed=m + n)
+    aq = oracle.quantize_q8_K(act)
+    got = run_mul_mat(hip, torch, 1, w, aq, m, n, k, hip.PATH_MFMA)
+    check_close(oracle, 1, got, w, aq, m, n, k, label=f"q4_K whole-K {m}x{n}x{k}")
+
+
 def test_config2_q4_K_full_size(hip, torch_gpu, oracle):
     """c2: q4_K x q8_K M=480 N=1536 K=1536 through pfng_hip_compute, whole output
     checked; then weight-row permutation equivariance and exact doubling with
