@@ -379,7 +379,7 @@ def main():
     gemm = measure(torch, pkg, "c0: q4_0 x q8_0 GEMM M=480 N=1536 K=1536", 0, 480, 1536, 1536, args.gemm_steps, 256,
                    samples, ref, "gemm_q4_0_wt_kernel")
     q4k = measure(torch, pkg, "c2: q4_K x q8_K GEMM M=480 N=1536 K=1536", 1, 480, 1536, 1536, args.gemm_steps, 256,
-                  samples, ref, "gemm_kq_kernel<q4_K>")
+                  samples, ref, "gemm_q4_K_wt_kernel<6>")
     iq2 = None
     if args.iq2_steps > 0:
         iq2 = measure(torch, pkg, "c3: iq2_xxs x q8_K GEMM M=512 N=4096 K=4096 (baseline weight generator)", 2, 512,

@@ -308,8 +308,17 @@ __device__ __forceinline__ void kt_compute(const uint8_t *bufa, const uint8_t *b
 #pragma unroll
     for (int sb = s0 / 8; sb <= (s1 - 1) / 8; ++sb) {
         const int ja = s0 > 8 * sb ? s0 - 8 * sb : 0, jb = s1 < 8 * sb + 8 ? s1 - 8 * sb : 8;
-        const uint4 hdv = *reinterpret_cast<const uint4 *>(wrow + sb * 144);
-        const uint32_t hd[4] = {hdv.x, hdv.y, hdv.z, hdv.w};
+        const uint4 hd = *reinterpret_cast<const uint4 *>(wrow + sb * 144);
+        // the reference's scale and min decode (llama_reference.cpp:116-121)
+        // four sub-blocks per word: byte i of sc_lo / mn_lo is sub-block i's,
+        // of sc_hi / mn_hi sub-block 4 + i's
+        const uint32_t sc_lo = hd.y & 0x3f3f3f3fu, mn_lo = hd.z & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u);
+        const uint32_t mn_hi = ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u);
+        // octal digits l, h of the scales, then one sub-block's digit in both
+        // 16-bit halves by a byte permute
+        const uint32_t dl_lo = sc_lo & 0x07070707u, dh_lo = (sc_lo >> 3) & 0x07070707u;
+        const uint32_t dl_hi = sc_hi & 0x07070707u, dh_hi = (sc_hi >> 3) & 0x07070707u;
         i32x16 sl = {}, sh = {};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -322,28 +331,32 @@ __device__ __forceinline__ void kt_compute(const uint8_t *bufa, const uint8_t *b
             const uint32_t sh4 = (j & 1) ? 4u : 0u;
             const i32x4 nib = (i32x4){(int)((wq.x >> sh4) & 0x0f0f0f0fu), (int)((wq.y >> sh4) & 0x0f0f0f0fu),
                                       (int)((wq.z >> sh4) & 0x0f0f0f0fu), (int)((wq.w >> sh4) & 0x0f0f0f0fu)};
-            uint32_t sc, mn;
-            q4_K_scale_min(hd, j, sc, mn);
+            const uint32_t sel = 0x0c000c00u | (uint32_t)(j & 3) * 0x00010001u;
+            const uint32_t d2l = __builtin_amdgcn_perm(0u, j < 4 ? dl_lo : dl_hi, sel);
+            const uint32_t d2h = __builtin_amdgcn_perm(0u, j < 4 ? dh_lo : dh_hi, sel);
             const bool first = j == ja;
-            sl = mfma_i8_32x32x32(av, mul_planes(nib, (sc & 7u) * 0x10001u), first ? (i32x16){} : sl);
-            sh = mfma_i8_32x32x32(av, mul_planes(nib, (sc >> 3) * 0x10001u), first ? (i32x16){} : sh);
+            sl = mfma_i8_32x32x32(av, mul_planes(nib, d2l), first ? (i32x16){} : sl);
+            sh = mfma_i8_32x32x32(av, mul_planes(nib, d2h), first ? (i32x16){} : sh);
         }
         // IM: lane supplies the bsums 8 lh .. 8 lh + 7 of row li (sub-blocks
         // 4 lh .. 4 lh + 3) and the mins of column li for those sub-blocks,
-        // each twice (exact: |bsum| <= 2032 and m <= 63 are fp16 integers)
+        // each twice (exact: |bsum| <= 2032 and m <= 63 are fp16 integers);
+        // the mins of sub-blocks outside [ja, jb) are zeroed
         const uint32_t *bp = arow + sb * 73 + 65 + 4 * lh;
+        uint32_t keep_lo = 0, keep_hi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (i >= ja && i < jb) keep_lo |= 0xffu << (8 * i);
+            if (4 + i >= ja && 4 + i < jb) keep_hi |= 0xffu << (8 * i);
+        }
+        const uint32_t mins = lh ? (mn_hi & keep_hi) : (mn_lo & keep_lo);
         f16x8 bs, mv;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t v = bp[i];
-            bs[2 * i] = (_Float16)(float)(int16_t)(v & 0xffffu);
-            bs[2 * i + 1] = (_Float16)(float)(int16_t)(v >> 16);
-            uint32_t scl, mnl, sch, mnh;
-            q4_K_scale_min(hd, i, scl, mnl);
-            q4_K_scale_min(hd, 4 + i, sch, mnh);
-            const float ml = (i >= ja && i < jb) ? (float)mnl : 0.0f;
-            const float mh = (4 + i >= ja && 4 + i < jb) ? (float)mnh : 0.0f;
-            const _Float16 mm = (_Float16)(lh ? mh : ml);
+            bs[2 * i] = (_Float16)(int16_t)(v & 0xffffu);
+            bs[2 * i + 1] = (_Float16)(int16_t)(v >> 16);
+            const _Float16 mm = (_Float16)((mins >> (8 * i)) & 0xffu);
             mv[2 * i] = mm;
             mv[2 * i + 1] = mm;
         }

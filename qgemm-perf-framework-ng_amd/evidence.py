@@ -48,7 +48,7 @@ CONFIGS = {
     "c0": ("q4_0 x q8_0 GEMM M=480 N=1536 K=1536", 0, 480, 1536, 1536, 0, "gemm_q4_0_wt_kernel", "mfma"),
     "c1": ("q4_0 x q8_0 GEMV M=1 N=4096 K=4096, 48 rotating weight copies", 0, 1, 4096, 4096, 0,
            "gemv_q4_0_m1_kernel", "hbm"),
-    "c2": ("q4_K x q8_K GEMM M=480 N=1536 K=1536", 1, 480, 1536, 1536, 0, "gemm_kq_kernel", "mfma"),
+    "c2": ("q4_K x q8_K GEMM M=480 N=1536 K=1536", 1, 480, 1536, 1536, 0, "gemm_q4_K_wt_kernel", "mfma"),
     "c3": ("iq2_xxs x q8_K GEMM M=512 N=4096 K=4096 (baseline weight generator)", 2, 512, 4096, 4096, 1,
            "gemm_kq_kernel", "mfma"),
     "c4": ("q4_0 x q8_0 GEMM M=2048 N=11008 K=4096", 0, 2048, 11008, 4096, 0, "gemm_q4_0_kernel", "mfma"),
