@@ -258,12 +258,14 @@ __device__ __forceinline__ i32x4 mul_planes(i32x4 v, uint32_t digit2) {
 // m-fastest in groups of kGroupM m-tiles, so the workgroups resident on one XCD
 // at a time share weight and activation tiles in its L2. The map is a bijection
 // on [0, mt*nt): the first 8*q ids are regrouped (q tiles per XCD), the last
-// (mt*nt) % 8 ids keep their own index.
+// (mt*nt) % 8 ids keep their own index. kGroupM = 1 walks n fastest, so an
+// XCD's range covers as few m-tiles (activation rows) as possible.
 struct TileOrigin {
     int mi, ni;  // tile coordinates
 };
+template <int kGroupM = 8>
 __device__ __forceinline__ TileOrigin xcd_tile(int id, int mt, int nt) {
-    constexpr int kXcds = 8, kGroupM = 8;
+    constexpr int kXcds = 8;
     const int tiles = mt * nt;
     const int q = tiles / kXcds;
     const int t = id < q * kXcds ? (id % kXcds) * q + id / kXcds : id;
