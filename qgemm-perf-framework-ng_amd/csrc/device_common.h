@@ -63,13 +63,22 @@ __device__ __forceinline__ uint32_t f32_to_fp16_bits(float value) {
     return (sign >> 16) | (shl1_w > 0xFF000000u ? 0x7E00u : nonsign);
 }
 
+// (int)roundf(t), half away from zero, for the |t| <= 130 the q8 quantizers
+// produce (|x * id| <= 127 up to rounding; an infinite id gives +-inf or NaN,
+// which take the same conversion either way): trunc(t + copysign(0.5 - 2^-25,
+// t)) in three operations instead of roundf's six. Equal to roundf for every
+// float in [0, 130] (checked exhaustively), and both sides are odd functions.
+__device__ __forceinline__ int round_half_away_q8(float t) {
+    return (int)add_rn(t, __builtin_copysignf(0x1.fffffep-2f, t));
+}
+
 // Four values of a q8_0 / q8_K block: (int8)round(x * id) packed little-endian
 // (llama_reference.cpp:49, :63; x * id separately rounded, roundf = std::round).
 __device__ __forceinline__ uint32_t q8_quantize4(float4 v, float id) {
-    const int q0 = (int)roundf(mul_rn(v.x, id));
-    const int q1 = (int)roundf(mul_rn(v.y, id));
-    const int q2 = (int)roundf(mul_rn(v.z, id));
-    const int q3 = (int)roundf(mul_rn(v.w, id));
+    const int q0 = round_half_away_q8(mul_rn(v.x, id));
+    const int q1 = round_half_away_q8(mul_rn(v.y, id));
+    const int q2 = round_half_away_q8(mul_rn(v.z, id));
+    const int q3 = round_half_away_q8(mul_rn(v.w, id));
     return (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
            ((uint32_t)(q3 & 0xff) << 24);
 }
