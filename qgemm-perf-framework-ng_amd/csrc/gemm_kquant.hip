@@ -13,8 +13,10 @@
 //
 // A K stage is half a super-block (4 sub-blocks, 128 elements). Per stage the
 // workgroup stages into LDS:
-//   * activation int8 rows as they are, the q8_K scale and (q4_K) the eight
-//     16-element bsums of the half as fp16 (|bsum| <= 2032 is exact in fp16);
+//   * activation int8 rows as they are, copied by direct-to-LDS buffer loads
+//     (no registers), and through registers the q8_K scale and (q4_K) the
+//     eight 16-element bsums of the half as fp16 (|bsum| <= 2032 is exact in
+//     fp16);
 //   * weight values expanded to int8 (q4_K nibble 0..15 and the sub-block
 //     scale digits; iq2_xxs two planes of the scaled value), and the fp16
 //     scales.
@@ -61,9 +63,16 @@ struct KqConfig {
     static constexpr int kSub = 4;                    // sub-blocks per stage
     static constexpr int kWaveSub = kSub / WK;        // sub-blocks per stage of one wave
     static constexpr int kRowStride = kSub * 32 + 16;  // LDS bytes per int8 row (+ pad against bank conflicts)
-    // LDS layout of one stage buffer
-    static constexpr int kAq = 0;                                   // int8 [BM][kRowStride]
-    static constexpr int kAd = kAq + BM * kRowStride;               // fp32 [BM] activation scale
+    // A stage's activation rows of one slice, [BM][kRowStride] int8: nine
+    // 16-byte chunks per row (eight of data, the pad), 64 chunks per copy
+    // instruction, the region padded to whole instructions
+    static constexpr int kRowChunks = kRowStride / 16;
+    static constexpr int kActCopies = (BM * kRowChunks + 63) / 64;
+    static constexpr int kAqBytes = kActCopies * 1024;
+    static constexpr int kWaves = kThreads / 64;  // waves of one slice
+    static constexpr int kActCopiesPerWave = (kActCopies + kWaves - 1) / kWaves;
+    // LDS layout of the rest of one stage buffer
+    static constexpr int kAd = 0;                                   // fp32 [BM] activation scale
     static constexpr int kAb = kAd + BM * 4;                        // q4_K: fp16 [BM][8] bsums of the half
     static constexpr int kWq = kAb + (kQ4K ? BM * 16 : 0);          // int8 [BN][kRowStride] (iq2: the lo plane)
     static constexpr int kWq2 = kWq + BN * kRowStride;              // iq2: int8 [BN][kRowStride] hi plane
@@ -72,14 +81,16 @@ struct KqConfig {
     static constexpr int kWdm = kWd + BN * 4;                       // q4_K: fp32 [BN] dmin
     static constexpr int kWmin = kWdm + (kQ4K ? BN * 4 : 0);        // q4_K: fp16 [BN][8] mins, each twice
     static constexpr int kBufBytes = kWmin + (kQ4K ? BN * 16 : 0);
-    static constexpr int kSliceBytes = 2 * kBufBytes;                // a slice's two stage buffers
-    // iq2 tables after the slices: 256 x 8 grid code bytes (0, 1, 2 for 8, 25,
-    // 43), 128 x 8 sign selector bytes (4 where the value is negative), and
-    // per scale s the (lo, hi) byte pairs of the six signed products
-    static constexpr int kGrid = WS * kSliceBytes;
-    static constexpr int kSigns = kGrid + 256 * 8;
+    // iq2 tables: 256 x 8 grid code bytes (0, 1, 2 for 8, 25, 43), 128 x 8
+    // sign selector bytes (4 where the value is negative), and per scale s the
+    // (lo, hi) byte pairs of the six signed products
+    static constexpr int kSigns = 256 * 8;
     static constexpr int kScaleTab = kSigns + 128 * 8;
-    static constexpr int kLdsBytes = kGrid + (kQ4K ? 0 : 256 * 8 + 128 * 8 + 16 * 16);
+    static constexpr int kTabBytes = kQ4K ? 16 : kScaleTab + 16 * 16;
+    // the partial accumulators' reduction reuses the even stages' activation array
+    static constexpr int kRedBytes = (WK * WS - 1) * WM * WN * TM * TN * 16 * 64 * 4;
+    static constexpr int kAct0Bytes = WS * kAqBytes > kRedBytes ? WS * kAqBytes : kRedBytes;
+    static constexpr int kLdsBytes = kAct0Bytes + WS * kAqBytes + 2 * WS * kBufBytes + kTabBytes;
     static constexpr int kAllThreads = kThreads * WS;
     // global -> register tasks per stage: each activation row in kActE parts
     // (2 or 4) of its 128 int8 and 8 bsums, each weight row per sub-block
@@ -95,14 +106,13 @@ struct KqConfig {
     static_assert(kAd % 16 == 0 && kAb % 16 == 0 && kWq % 16 == 0 && kWq2 % 16 == 0 && kWs % 16 == 0 && kWd % 16 == 0 &&
                       kWdm % 16 == 0 && kWmin % 16 == 0 && kBufBytes % 16 == 0,
                   "LDS regions 16-byte aligned");
+    static_assert(kRowStride % 16 == 0 && kRowChunks % 2 == 1, "rows of an odd number of whole chunks");
     static_assert(kWaveSub * WK == kSub, "the stage's sub-blocks split evenly over the K-waves");
-    static_assert((WK * WS - 1) * WM * WN * TM * TN * 16 * 64 * 4 <= WS * kSliceBytes, "K-wave reduction fits in LDS");
     static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
 };
 
 template <class C>
 struct KqRegs {
-    uint32_t aq[C::kActPT][C::kQsDw];  // 128 / kActE activation bytes
     uint32_t ab[C::kActPT][C::kBsDw];  // 8 / kActE bsums (q4_K)
     float ad[C::kActPT];
     // q4_K: 16 nibble bytes + the 16-byte header (d, dmin, scales)
@@ -122,7 +132,7 @@ constexpr int kQ8KBytes = 292, kQ4KBytes = 144, kIq2Bytes = 66;
 // (mfma_supported declines longer rows).
 template <class C>
 struct KqOffsets {
-    uint32_t a[C::kActPT];  // activation row + part e's qs dwords
+    uint32_t a[C::kActPT];  // activation row + part e's qs dwords (its scale and bsums are read)
     uint32_t w[C::kWPT];    // weight row + sub-block e (iq2_xxs: its first byte past d)
 };
 
@@ -159,11 +169,7 @@ __device__ __forceinline__ void kq_load(const uint8_t *__restrict__ a_t, const u
     for (int it = 0; it < C::kActPT; ++it) {
         const int task = tid + it * C::kThreads;
         const int e = task % C::kActE;
-        const uint8_t *part = a_st + o.a[it];  // qs dwords of part e at part + 4 + 128 H
-        const uint8_t *blk = part - 4 * C::kQsDw * e;
-        const uint32_t *qs = reinterpret_cast<const uint32_t *>(part + 4 + 128 * H);
-#pragma unroll
-        for (int i = 0; i < C::kQsDw; ++i) r.aq[it][i] = qs[i];
+        const uint8_t *blk = a_st + o.a[it] - 4 * C::kQsDw * e;
         const uint32_t *bs = reinterpret_cast<const uint32_t *>(blk + 260 + 16 * H + 4 * C::kBsDw * e);
         if constexpr (C::kQ4K) {
 #pragma unroll
@@ -199,19 +205,64 @@ __device__ __forceinline__ void kq_load(const uint8_t *__restrict__ a_t, const u
     }
 }
 
+// One 16-byte direct-to-LDS buffer load per lane (64 lanes: 1 KB at dst). A
+// plain function: inside a kernel template the 16-byte form of the builtin
+// makes the host pass drop the kernel's launch stub.
+__device__ __forceinline__ void kq_copy16(__amdgpu_buffer_rsrc_t r, uint8_t *dst, uint32_t voffset, uint32_t soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)dst, 16, voffset, soffset, 0,
+                                             0);
+}
+
+// One slice's direct-to-LDS copies of a stage's activation rows (half H of
+// super-block b) into act + aoff: copy j's lane l moves chunk c = 64 j + l, row
+// c / 9, column c % 9 (the pad column repeats column 7; lanes past the rows
+// repeat the last chunk into the region's padding; rows past rows_valid
+// repeat the last valid row). The copies are dealt round-robin over the
+// slice's waves, every wave issuing the same number (a wave past the last
+// copy repeats it: c3 28.9 against 29.3 us when such waves skip it).
+template <class C, int H>
+__device__ __forceinline__ void kq_act_copy(uint8_t *act, int aoff, __amdgpu_buffer_rsrc_t ra, int b, int wave, int lane,
+                                            int rows_valid, int nb) {
+#pragma unroll
+    for (int i = 0; i < C::kActCopiesPerWave; ++i) {
+        int j = wave + i * C::kWaves;
+        if (j > C::kActCopies - 1) j = C::kActCopies - 1;  // repeats the last copy
+        int ch = 64 * j + lane;
+        if (ch > C::kBM * C::kRowChunks - 1) ch = C::kBM * C::kRowChunks - 1;
+        const int row = ch / C::kRowChunks;
+        int col = ch - row * C::kRowChunks;
+        if (col > C::kRowChunks - 2) col = C::kRowChunks - 2;
+        const int rr = row < rows_valid ? row : rows_valid - 1;
+        const uint32_t off = (uint32_t)rr * (uint32_t)nb * (uint32_t)kQ8KBytes + 4u + 16u * (uint32_t)col;
+        kq_copy16(ra, act + (aoff + j * 1024), off, (uint32_t)b * kQ8KBytes + 128u * H);
+    }
+}
+
+// An LDS address as the array plus one opaque offset (plus constants). The
+// compiler attaches an array's alias scope only to accesses a few address
+// steps from the array, and makes an LDS access without it wait for every
+// direct-to-LDS copy in flight; left alone, it splits offsets into chains of
+// address steps.
+template <class T, class B>
+__device__ __forceinline__ T *lds_at(B *arr, int off) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm("" : "+v"(off));
+#endif
+    return reinterpret_cast<T *>(arr + off);
+}
+
+// Registers of a stage into the stage buffer at rest + roff.
 template <class C>
-__device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int h, int tid, const KqRegs<C> &r) {
-    const uint8_t *signs = grid + (C::kSigns - C::kGrid);
-    const uint8_t *scale_tab = grid + (C::kScaleTab - C::kGrid);
+__device__ __forceinline__ void kq_store(uint8_t *rest, int roff, const uint8_t *tab, int h, int tid,
+                                         const KqRegs<C> &r) {
+    const uint8_t *grid = tab;
+    const uint8_t *signs = tab + C::kSigns;
+    const uint8_t *scale_tab = tab + C::kScaleTab;
 #pragma unroll
     for (int it = 0; it < C::kActPT; ++it) {
         const int task = tid + it * C::kThreads;
         const int row = task / C::kActE, e = task % C::kActE;
-        const uint32_t *v = r.aq[it];
-        uint4 *dst = reinterpret_cast<uint4 *>(lds + C::kAq + row * C::kRowStride + 4 * C::kQsDw * e);
-#pragma unroll
-        for (int i = 0; i < C::kQsDw / 4; ++i) dst[i] = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-        *reinterpret_cast<float *>(lds + C::kAd + row * 4) = r.ad[it];  // every part writes the same value
+        *lds_at<float>(rest, roff + C::kAd + row * 4) = r.ad[it];  // every part writes the same value
         if constexpr (C::kQ4K) {
             uint32_t hb[C::kBsDw];
 #pragma unroll
@@ -220,7 +271,7 @@ __device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int 
                 const _Float16 hi = (_Float16)(float)(int16_t)(r.ab[it][i] >> 16);
                 hb[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
             }
-            uint32_t *bdst = reinterpret_cast<uint32_t *>(lds + C::kAb + row * 16 + 4 * C::kBsDw * e);
+            uint32_t *bdst = lds_at<uint32_t>(rest, roff + C::kAb + row * 16 + 4 * C::kBsDw * e);
 #pragma unroll
             for (int i = 0; i < C::kBsDw; ++i) bdst[i] = hb[i];
         }
@@ -229,7 +280,7 @@ __device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int 
     for (int it = 0; it < C::kWPT; ++it) {
         const int task = tid + it * C::kThreads;
         const int row = task / C::kSub, e = task % C::kSub;
-        uint8_t *wrow = lds + C::kWq + row * C::kRowStride;
+        const int wrow = roff + C::kWq + row * C::kRowStride;  // the row's lo (iq2) or value plane
         if constexpr (C::kQ4K) {
             // bytes 16e..16e+15 of the half's 64 nibble bytes: pair p = e/2
             // holds local sub-block 2p (low nibbles) and 2p+1 (high nibbles),
@@ -241,17 +292,19 @@ __device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int 
                 lo[i] = r.wq[it][i] & 0x0f0f0f0fu;
                 hi[i] = (r.wq[it][i] >> 4) & 0x0f0f0f0fu;
             }
-            *reinterpret_cast<uint4 *>(wrow + (2 * p) * 32 + i0) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            *reinterpret_cast<uint4 *>(wrow + (2 * p + 1) * 32 + i0) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            uint4 *dst = lds_at<uint4>(rest, wrow + (2 * p) * 32 + i0);
+            dst[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            dst[2] = make_uint4(hi[0], hi[1], hi[2], hi[3]);  // 32 bytes on: sub-block 2p + 1
             // scale digits and min of local sub-block e
             uint32_t sc, mn;
             q4_K_scale_min(r.wh[it], 4 * h + e, sc, mn);
             const uint32_t l = sc & 7u, hh = sc >> 3;
-            *reinterpret_cast<uint2 *>(lds + C::kWs + row * 32 + 8 * e) = make_uint2(l * 0x10001u, hh * 0x10001u);
+            *lds_at<uint2>(rest, roff + C::kWs + row * 32 + 8 * e) = make_uint2(l * 0x10001u, hh * 0x10001u);
             const uint32_t mh = __builtin_bit_cast(uint16_t, (_Float16)(float)mn);
-            *reinterpret_cast<uint32_t *>(lds + C::kWmin + row * 16 + 4 * e) = mh | (mh << 16);
-            *reinterpret_cast<float *>(lds + C::kWd + row * 4) = fp16_to_f32(r.wh[it][0] & 0xffffu);
-            *reinterpret_cast<float *>(lds + C::kWdm + row * 4) = fp16_to_f32(r.wh[it][0] >> 16);
+            *lds_at<uint32_t>(rest, roff + C::kWmin + row * 16 + 4 * e) = mh | (mh << 16);
+            float *dd = lds_at<float>(rest, roff + C::kWd + row * 4);
+            dd[0] = fp16_to_f32(r.wh[it][0] & 0xffffu);
+            dd[(C::kWdm - C::kWd) / 4] = fp16_to_f32(r.wh[it][0] >> 16);
         } else {
             // iq2_xxs sub-block (kernels/common/iq2_xxs.h:29-41): four groups of
             // 8 values. A value's selector byte is its grid code (0, 1, 2 for
@@ -276,13 +329,12 @@ __device__ __forceinline__ void kq_store(uint8_t *lds, const uint8_t *grid, int 
                 hi[2 * g] = __builtin_amdgcn_perm(tab.w, tab.z, s0);
                 hi[2 * g + 1] = __builtin_amdgcn_perm(tab.w, tab.z, s1);
             }
-            uint4 *dlo = reinterpret_cast<uint4 *>(wrow + 32 * e);
-            uint4 *dhi = reinterpret_cast<uint4 *>(lds + C::kWq2 + row * C::kRowStride + 32 * e);
+            uint4 *dlo = lds_at<uint4>(rest, wrow + 32 * e), *dhi = dlo + (C::kWq2 - C::kWq) / 16;
             dlo[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
             dlo[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
             dhi[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
             dhi[1] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
-            *reinterpret_cast<float *>(lds + C::kWd + row * 4) = 0.125f * fp16_to_f32(r.wh[it][0]);
+            *lds_at<float>(rest, roff + C::kWd + row * 4) = 0.125f * fp16_to_f32(r.wh[it][0]);
         }
     }
 }
@@ -298,12 +350,14 @@ struct KqAcc {
 
 // Sub-block sums of one stage (half H of the super-block) for one wave: its
 // kWaveSub sub-blocks tb .. tb + kWaveSub - 1 (tb a multiple of kWaveSub).
+// The stage's activation rows at act + aoff, the rest of its buffer at
+// rest + roff (every LDS address the array plus one offset, as in kq_store).
 template <class C, int H>
-__device__ __forceinline__ void kq_compute(const uint8_t *buf, KqAcc<C> &A, int tb, int lane, int wave_m,
-                                           int wave_n) {
+__device__ __forceinline__ void kq_compute(const uint8_t *act, int aoff, const uint8_t *rest, int roff, KqAcc<C> &A,
+                                           int tb, int lane, int wave_m, int wave_n) {
     const int li = lane & 31, lh = lane >> 5;
-    const uint8_t *aq = buf + C::kAq + (wave_m * C::TM * 32 + li) * C::kRowStride + lh * 16;
-    const uint8_t *wq = buf + C::kWq + (wave_n * C::TN * 32 + li) * C::kRowStride + lh * 16;
+    const uint8_t *aq = lds_at<const uint8_t>(act, aoff + (wave_m * C::TM * 32 + li) * C::kRowStride + lh * 16);
+    const uint8_t *wq = lds_at<const uint8_t>(rest, roff + C::kWq + (wave_n * C::TN * 32 + li) * C::kRowStride + lh * 16);
     const int wrow = wave_n * C::TN * 32 + li;
     if constexpr (C::kQ4K) {
 #pragma unroll
@@ -317,7 +371,7 @@ __device__ __forceinline__ void kq_compute(const uint8_t *buf, KqAcc<C> &A, int 
             for (int tn = 0; tn < C::TN; ++tn) {
                 const i32x4 v = *reinterpret_cast<const i32x4 *>(wq + tn * 32 * C::kRowStride + t * 32);
                 // digit pair (l, h) of sub-block t, each replicated in both 16-bit halves
-                const uint2 d = *reinterpret_cast<const uint2 *>(buf + C::kWs + (wrow + tn * 32) * 32 + 8 * t);
+                const uint2 d = lds_at<const uint2>(rest, roff + C::kWs + wrow * 32)[(tn * 32 * 32 + 8 * t) / 8];
                 vl[tn] = mul_planes(v, d.x);
                 vh[tn] = mul_planes(v, d.y);
             }
@@ -337,10 +391,10 @@ __device__ __forceinline__ void kq_compute(const uint8_t *buf, KqAcc<C> &A, int 
         f16x4 ab[C::TM], wm[C::TN];
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm)
-            ab[tm] = *reinterpret_cast<const f16x4 *>(buf + C::kAb + (wave_m * C::TM * 32 + tm * 32 + li) * 16 + lh * 8);
+            ab[tm] = lds_at<const f16x4>(rest, roff + C::kAb + (wave_m * C::TM * 32 + li) * 16 + lh * 8)[tm * 32 * 2];
 #pragma unroll
         for (int tn = 0; tn < C::TN; ++tn) {
-            wm[tn] = *reinterpret_cast<const f16x4 *>(buf + C::kWmin + (wrow + tn * 32) * 16 + lh * 8);
+            wm[tn] = lds_at<const f16x4>(rest, roff + C::kWmin + wrow * 16 + lh * 8)[tn * 32 * 2];
             if (!mine) wm[tn] = (f16x4){};
         }
 #pragma unroll
@@ -377,7 +431,7 @@ __device__ __forceinline__ void kq_compute(const uint8_t *buf, KqAcc<C> &A, int 
 
 // End of super-block b: fold the exact sums into C (or write them out).
 template <class C, bool kIsums>
-__device__ __forceinline__ void kq_epilogue(const uint8_t *buf, KqAcc<C> &A, int32_t *isums, int m, int n, int nb,
+__device__ __forceinline__ void kq_epilogue(const uint8_t *rest, int roff, KqAcc<C> &A, int32_t *isums, int m, int n, int nb,
                                             int m0, int n0, int b, int lane, int wave_m, int wave_n) {
     const int li = lane & 31, lh = lane >> 5;
     if constexpr (kIsums) {
@@ -404,18 +458,19 @@ __device__ __forceinline__ void kq_epilogue(const uint8_t *buf, KqAcc<C> &A, int
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm) {
             // activation scales of the lane's 16 rows: rows 8g + 4lh + 0..3
-            const float *adp = reinterpret_cast<const float *>(buf + C::kAd) + wave_m * C::TM * 32 + tm * 32 + 4 * lh;
             f32x4 ad4[4];
             if constexpr (C::kQ4K) {
+                const f32x4 *adp = lds_at<const f32x4>(rest, roff + C::kAd + 4 * (wave_m * C::TM * 32 + tm * 32 + 4 * lh));
 #pragma unroll
-                for (int g = 0; g < 4; ++g) ad4[g] = *reinterpret_cast<const f32x4 *>(adp + 8 * g);
+                for (int g = 0; g < 4; ++g) ad4[g] = adp[2 * g];
             }
 #pragma unroll
             for (int tn = 0; tn < C::TN; ++tn) {
                 const int wr = wave_n * C::TN * 32 + tn * 32 + li;
-                const float d = reinterpret_cast<const float *>(buf + C::kWd)[wr];
+                const float *dp = lds_at<const float>(rest, roff + C::kWd + 4 * wr);
+                const float d = dp[0];
                 if constexpr (C::kQ4K) {
-                    const float dmin = reinterpret_cast<const float *>(buf + C::kWdm)[wr];
+                    const float dmin = dp[(C::kWdm - C::kWd) / 4];
 #pragma unroll
                     for (int q = 0; q < 16; ++q) {
                         const int is = 8 * A.s1[tm][tn][q] + A.s0[tm][tn][q];
@@ -427,7 +482,7 @@ __device__ __forceinline__ void kq_epilogue(const uint8_t *buf, KqAcc<C> &A, int
                     // l % 32 and d of column l % 32 at K index l / 32, and the
                     // upper lanes' d is zero, so P[r][c] = ad_r * d_c, the
                     // correctly rounded product
-                    const float adl = reinterpret_cast<const float *>(buf + C::kAd)[wave_m * C::TM * 32 + tm * 32 + li];
+                    const float adl = *lds_at<const float>(rest, roff + C::kAd + 4 * (wave_m * C::TM * 32 + tm * 32 + li));
                     const f32x16 pr = __builtin_amdgcn_mfma_f32_32x32x2f32(adl, lh ? 0.0f : d, (f32x16){}, 0, 0, 0);
 #pragma unroll
                     for (int q = 0; q < 16; ++q)
@@ -443,11 +498,20 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
                                                                     const uint8_t *__restrict__ a,
                                                                     float *__restrict__ c, int32_t *__restrict__ isums,
                                                                     int m, int n, int nb) {
-    extern __shared__ __align__(16) uint8_t lds[];
+    // The activation rows of the even and the odd stages are separate arrays,
+    // as is the rest of the stage buffers: the compiler then waits, before
+    // a stage's LDS reads, only for the copies into that stage's array, not
+    // for those of the next stage, which are in flight meanwhile.
+    __shared__ __align__(16) uint8_t act0[C::kAct0Bytes];
+    __shared__ __align__(16) uint8_t act1[C::kWS * C::kAqBytes];
+    __shared__ __align__(16) uint8_t rest0[C::kWS * C::kBufBytes];
+    __shared__ __align__(16) uint8_t rest1[C::kWS * C::kBufBytes];
+    __shared__ __align__(16) uint8_t tab[C::kTabBytes];
     const int lane = threadIdx.x & 63;
-    const int slice = threadIdx.x / C::kThreads;  // takes super-blocks slice, slice + WS, ...
-    const int tid = threadIdx.x % C::kThreads;    // thread index within the slice
-    const int wave = tid >> 6;
+    // wave-uniform: the copies' LDS addresses go to a scalar register
+    const int slice = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / C::kThreads));  // takes super-blocks slice, slice + WS, ...
+    const int tid = threadIdx.x % C::kThreads;  // thread index within the slice
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wk = wave / (C::kWM * C::kWN);   // which share of each stage's sub-blocks
     const int wmn = wave % (C::kWM * C::kWN);  // which TM x TN sub-tile
     const int wave_m = wmn / C::kWN;
@@ -458,9 +522,7 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
     // end to end 37.3 -> 35.8 us; the product alone within 1 %)
     const TileOrigin to = xcd_tile<1>(blockIdx.x, (m + C::kBM - 1) / C::kBM, (n + C::kBN - 1) / C::kBN);
     const int m0 = to.mi * C::kBM, n0 = to.ni * C::kBN;
-    uint8_t *grid = lds + C::kGrid;
-    uint8_t *buf0 = lds + slice * C::kSliceBytes;
-    uint8_t *buf1 = buf0 + C::kBufBytes;
+    const int aoff = slice * C::kAqBytes, roff = slice * C::kBufBytes;  // the slice's part of each array
     if constexpr (!C::kQ4K) {
         // grid codes (kernels/iq2_xxs-q8_K-RVV-common/ggml_min.h:69-134): per
         // value one byte 0, 1 or 2 for the magnitude 8, 25 or 43
@@ -469,7 +531,7 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
             uint32_t v[2] = {0, 0};
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[j / 4] |= ((code >> (2 * j)) & 3u) << (8 * (j % 4));
-            *reinterpret_cast<uint2 *>(lds + C::kGrid + 8 * e) = make_uint2(v[0], v[1]);
+            *reinterpret_cast<uint2 *>(tab + 8 * e) = make_uint2(v[0], v[1]);
         }
         // signs (the reference's ksigns_iq2xs, ggml_min.h:58-67: byte
         // idx | parity(idx) << 7): 4 in the byte of each negative value
@@ -478,7 +540,7 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
             uint32_t v[2] = {0, 0};
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[j / 4] |= ((sgn >> j) & 1u) << (8 * (j % 4) + 2);
-            *reinterpret_cast<uint2 *>(lds + C::kSigns + 8 * e) = make_uint2(v[0], v[1]);
+            *reinterpret_cast<uint2 *>(tab + C::kSigns + 8 * e) = make_uint2(v[0], v[1]);
         }
         // per 4-bit scale s: w' = +-mag * (2 s + 1) = 128 hi + lo, byte c of
         // the positive and byte c of the negative words for code c
@@ -493,7 +555,7 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
                 ln |= (uint32_t)(q & 127) << (8 * c);
                 hn |= (uint32_t)((q >> 7) & 0xff) << (8 * c);
             }
-            *reinterpret_cast<uint4 *>(lds + C::kScaleTab + 16 * e) = make_uint4(lp, ln, hp, hn);
+            *reinterpret_cast<uint4 *>(tab + C::kScaleTab + 16 * e) = make_uint4(lp, ln, hp, hn);
         }
         __syncthreads();
     }
@@ -505,8 +567,9 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
         for (int j = 0; j < C::TN; ++j) A.acc[i][j] = (f32x16){};
 
     // Double-buffered LDS with one barrier per stage. Stage 2b+h is computed
-    // from buffer h while the registers of the next stage are stored into the
-    // other buffer and the loads of the stage after it are issued. Stores and
+    // from buffer h while the next stage's activation rows are copied into
+    // the other buffer, its registers are stored there and the loads of the
+    // stage after it are issued. Stores and
     // loads are unconditional (the super-block index is clamped at the end);
     // every slice runs the same number of iterations, and one whose
     // super-block is past the end skips only the arithmetic. That check is
@@ -520,28 +583,37 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
     const uint8_t *a_t = a + (size_t)m0 * nb * kQ8KBytes;
     const uint8_t *w_t = w + (size_t)n0 * nb * (C::kQ4K ? kQ4KBytes : kIq2Bytes);
     const KqOffsets<C> offs = kq_offsets<C>(m, n, nb, m0, n0, tid);
-    kq_load<C, 0>(a_t, w_t, slice < nb ? slice : last, offs, tid, regs);
-    kq_store<C>(buf0, grid, 0, tid, regs);
-    kq_load<C, 1>(a_t, w_t, slice < nb ? slice : last, offs, tid, regs);
+    const int rows_a = m - m0 < C::kBM ? m - m0 : C::kBM;
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a_t, 0, (int)((uint32_t)rows_a * (uint32_t)nb * kQ8KBytes), 0x00020000);
+    const int b0 = slice < nb ? slice : last;
+    kq_act_copy<C, 0>(act0, aoff, ra, b0, wave, lane, rows_a, nb);
+    kq_load<C, 0>(a_t, w_t, b0, offs, tid, regs);
+    kq_store<C>(rest0, roff, tab, 0, tid, regs);
+    kq_load<C, 1>(a_t, w_t, b0, offs, tid, regs);
     __syncthreads();
     auto step = [&](int it, bool guard) __attribute__((always_inline)) {
         const int b = it * C::kWS + slice;
         const bool mine = !guard || b < nb;  // uniform across the slice's waves
         const int bn = b + C::kWS < nb ? b + C::kWS : last;
         __builtin_amdgcn_sched_barrier(0);
-        if (mine) kq_compute<C, 0>(buf0, A, tb, lane, wave_m, wave_n);
+        kq_act_copy<C, 1>(act1, aoff, ra, b < nb ? b : last, wave, lane, rows_a, nb);
         __builtin_amdgcn_sched_barrier(0);
-        kq_store<C>(buf1, grid, 1, tid, regs);
+        if (mine) kq_compute<C, 0>(act0, aoff, rest0, roff, A, tb, lane, wave_m, wave_n);
+        __builtin_amdgcn_sched_barrier(0);
+        kq_store<C>(rest1, roff, tab, 1, tid, regs);
         __builtin_amdgcn_sched_barrier(0);
         kq_load<C, 0>(a_t, w_t, bn, offs, tid, regs);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
+        kq_act_copy<C, 0>(act0, aoff, ra, bn, wave, lane, rows_a, nb);
+        __builtin_amdgcn_sched_barrier(0);
         if (mine) {
-            kq_compute<C, 1>(buf1, A, tb, lane, wave_m, wave_n);
-            kq_epilogue<C, kIsums>(buf1, A, isums, m, n, nb, m0, n0, b, lane, wave_m, wave_n);
+            kq_compute<C, 1>(act1, aoff, rest1, roff, A, tb, lane, wave_m, wave_n);
+            kq_epilogue<C, kIsums>(rest1, roff, A, isums, m, n, nb, m0, n0, b, lane, wave_m, wave_n);
         }
         __builtin_amdgcn_sched_barrier(0);
-        kq_store<C>(buf0, grid, 0, tid, regs);
+        kq_store<C>(rest0, roff, tab, 0, tid, regs);
         __builtin_amdgcn_sched_barrier(0);
         kq_load<C, 1>(a_t, w_t, bn, offs, tid, regs);
         __builtin_amdgcn_sched_barrier(0);
@@ -558,7 +630,7 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
             // group order; the stage buffers are free after the last barrier
             constexpr int kRegs = C::TM * C::TN * 16;
             const int grp = slice * C::kWK + wk;
-            float *red = reinterpret_cast<float *>(lds);
+            float *red = reinterpret_cast<float *>(act0);
             if (grp > 0) {
                 float *dst = red + ((grp - 1) * C::kWM * C::kWN + wmn) * kRegs * 64 + lane;
 #pragma unroll
@@ -604,7 +676,7 @@ template <class C, bool kIsums>
 hipError_t launch_kq(const void *w, const void *a, float *c, int32_t *isums, int64_t m, int64_t n, int64_t k,
                      hipStream_t stream) {
     const dim3 grid((unsigned)(((n + C::kBN - 1) / C::kBN) * ((m + C::kBM - 1) / C::kBM)));
-    hipLaunchKernelGGL((gemm_kq_kernel<C, kIsums>), grid, dim3(C::kAllThreads), C::kLdsBytes, stream,
+    hipLaunchKernelGGL((gemm_kq_kernel<C, kIsums>), grid, dim3(C::kAllThreads), 0, stream,
                        static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(a), c, isums, (int)m, (int)n,
                        (int)(k / 256));
     return hipGetLastError();
