@@ -311,10 +311,14 @@ def extreme_activation(oracle, m, k, seed):
 
 # the configuration follows the plan: 32x32 tiles with 4/2/1 super-block
 # slices (small shapes), 64x64 with 2 slices (480x1536), 128x64 with 2 slices
-# (2048x1024) and 128x64 (2048x2048)
+# (2048x1024; 1000x2048x768: ragged row tile, three super-blocks over two
+# slices) and 128x64 (2048x2048; 1000x4096x512: ragged row tile, two
+# super-blocks), so the activation rows' direct-to-LDS copies run with rows
+# past m and with a slice that has no super-block in its last step
 @pytest.mark.parametrize("qtype", [1, 2])
 @pytest.mark.parametrize("m,n,k", [(32, 64, 256), (100, 77, 512), (1, 1, 256), (130, 65, 768), (480, 64, 1536),
-                                   (480, 1536, 256), (2048, 1024, 256), (2048, 2048, 256)])
+                                   (480, 1536, 256), (2048, 1024, 256), (2048, 2048, 256), (1000, 2048, 768),
+                                   (1000, 4096, 512)])
 def test_block_isums_kquant_bit_exact(hip, torch_gpu, oracle, qtype, m, n, k):
     torch = torch_gpu
     say(f"block isums type={qtype} {m}x{n}x{k}")
