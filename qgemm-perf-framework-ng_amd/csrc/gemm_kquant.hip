@@ -221,8 +221,8 @@ __device__ __forceinline__ void kq_copy16(__amdgpu_buffer_rsrc_t r, uint8_t *dst
 // slice's waves, every wave issuing the same number (a wave past the last
 // copy repeats it: c3 28.9 against 29.3 us when such waves skip it).
 template <class C, int H>
-__device__ __forceinline__ void kq_act_copy(uint8_t *act, int aoff, __amdgpu_buffer_rsrc_t ra, int b, int wave, int lane,
-                                            int rows_valid, int nb) {
+__device__ __forceinline__ void kq_act_copy(uint8_t *act, int aoff, __amdgpu_buffer_rsrc_t ra, int b, int wave,
+                                            int lane, int rows_valid, int nb) {
 #pragma unroll
     for (int i = 0; i < C::kActCopiesPerWave; ++i) {
         int j = wave + i * C::kWaves;
@@ -357,7 +357,8 @@ __device__ __forceinline__ void kq_compute(const uint8_t *act, int aoff, const u
                                            int tb, int lane, int wave_m, int wave_n) {
     const int li = lane & 31, lh = lane >> 5;
     const uint8_t *aq = lds_at<const uint8_t>(act, aoff + (wave_m * C::TM * 32 + li) * C::kRowStride + lh * 16);
-    const uint8_t *wq = lds_at<const uint8_t>(rest, roff + C::kWq + (wave_n * C::TN * 32 + li) * C::kRowStride + lh * 16);
+    const uint8_t *wq =
+        lds_at<const uint8_t>(rest, roff + C::kWq + (wave_n * C::TN * 32 + li) * C::kRowStride + lh * 16);
     const int wrow = wave_n * C::TN * 32 + li;
     if constexpr (C::kQ4K) {
 #pragma unroll
@@ -391,7 +392,8 @@ __device__ __forceinline__ void kq_compute(const uint8_t *act, int aoff, const u
         f16x4 ab[C::TM], wm[C::TN];
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm)
-            ab[tm] = lds_at<const f16x4>(rest, roff + C::kAb + (wave_m * C::TM * 32 + li) * 16 + lh * 8)[tm * 32 * 2];
+            ab[tm] =
+                lds_at<const f16x4>(rest, roff + C::kAb + (wave_m * C::TM * 32 + li) * 16 + lh * 8)[tm * 32 * 2];
 #pragma unroll
         for (int tn = 0; tn < C::TN; ++tn) {
             wm[tn] = lds_at<const f16x4>(rest, roff + C::kWmin + wrow * 16 + lh * 8)[tn * 32 * 2];
@@ -431,8 +433,8 @@ __device__ __forceinline__ void kq_compute(const uint8_t *act, int aoff, const u
 
 // End of super-block b: fold the exact sums into C (or write them out).
 template <class C, bool kIsums>
-__device__ __forceinline__ void kq_epilogue(const uint8_t *rest, int roff, KqAcc<C> &A, int32_t *isums, int m, int n, int nb,
-                                            int m0, int n0, int b, int lane, int wave_m, int wave_n) {
+__device__ __forceinline__ void kq_epilogue(const uint8_t *rest, int roff, KqAcc<C> &A, int32_t *isums, int m, int n,
+                                            int nb, int m0, int n0, int b, int lane, int wave_m, int wave_n) {
     const int li = lane & 31, lh = lane >> 5;
     if constexpr (kIsums) {
 #pragma unroll
@@ -460,7 +462,8 @@ __device__ __forceinline__ void kq_epilogue(const uint8_t *rest, int roff, KqAcc
             // activation scales of the lane's 16 rows: rows 8g + 4lh + 0..3
             f32x4 ad4[4];
             if constexpr (C::kQ4K) {
-                const f32x4 *adp = lds_at<const f32x4>(rest, roff + C::kAd + 4 * (wave_m * C::TM * 32 + tm * 32 + 4 * lh));
+                const f32x4 *adp =
+                    lds_at<const f32x4>(rest, roff + C::kAd + 4 * (wave_m * C::TM * 32 + tm * 32 + 4 * lh));
 #pragma unroll
                 for (int g = 0; g < 4; ++g) ad4[g] = adp[2 * g];
             }
@@ -482,7 +485,8 @@ __device__ __forceinline__ void kq_epilogue(const uint8_t *rest, int roff, KqAcc
                     // l % 32 and d of column l % 32 at K index l / 32, and the
                     // upper lanes' d is zero, so P[r][c] = ad_r * d_c, the
                     // correctly rounded product
-                    const float adl = *lds_at<const float>(rest, roff + C::kAd + 4 * (wave_m * C::TM * 32 + tm * 32 + li));
+                    const float adl =
+                        *lds_at<const float>(rest, roff + C::kAd + 4 * (wave_m * C::TM * 32 + tm * 32 + li));
                     const f32x16 pr = __builtin_amdgcn_mfma_f32_32x32x2f32(adl, lh ? 0.0f : d, (f32x16){}, 0, 0, 0);
 #pragma unroll
                     for (int q = 0; q < 16; ++q)
@@ -508,8 +512,9 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
     __shared__ __align__(16) uint8_t rest1[C::kWS * C::kBufBytes];
     __shared__ __align__(16) uint8_t tab[C::kTabBytes];
     const int lane = threadIdx.x & 63;
-    // wave-uniform: the copies' LDS addresses go to a scalar register
-    const int slice = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / C::kThreads));  // takes super-blocks slice, slice + WS, ...
+    // slice takes super-blocks slice, slice + WS, ...; slice and wave are
+    // wave-uniform (the copies' LDS addresses go to a scalar register)
+    const int slice = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / C::kThreads));
     const int tid = threadIdx.x % C::kThreads;  // thread index within the slice
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wk = wave / (C::kWM * C::kWN);   // which share of each stage's sub-blocks
@@ -569,23 +574,22 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
     // Double-buffered LDS with one barrier per stage. Stage 2b+h is computed
     // from buffer h while the next stage's activation rows are copied into
     // the other buffer, its registers are stored there and the loads of the
-    // stage after it are issued. Stores and
-    // loads are unconditional (the super-block index is clamped at the end);
-    // every slice runs the same number of iterations, and one whose
-    // super-block is past the end skips only the arithmetic. That check is
-    // only compiled into the one iteration that can need it: a branch around
-    // the arithmetic in every iteration made the compiler copy the just-loaded
-    // registers before the barrier and so wait for the loads there. (Loads
-    // issued two stages ahead, from a register set per half, measured no
-    // faster on c2/c3.)
+    // stage after it are issued. Copies, stores and loads are unconditional
+    // (the super-block index is clamped at the end); every slice runs the
+    // same number of iterations, and one whose super-block is past the end
+    // skips only the arithmetic. That check is only compiled into the one
+    // iteration that can need it: a branch around the arithmetic in every
+    // iteration made the compiler copy the just-loaded registers before the
+    // barrier and so wait for the loads there. (Loads issued two stages
+    // ahead, from a register set per half, measured no faster on c2/c3.)
     KqRegs<C> regs;
     const int last = nb - 1;
     const uint8_t *a_t = a + (size_t)m0 * nb * kQ8KBytes;
     const uint8_t *w_t = w + (size_t)n0 * nb * (C::kQ4K ? kQ4KBytes : kIq2Bytes);
     const KqOffsets<C> offs = kq_offsets<C>(m, n, nb, m0, n0, tid);
     const int rows_a = m - m0 < C::kBM ? m - m0 : C::kBM;
-    const __amdgpu_buffer_rsrc_t ra =
-        __builtin_amdgcn_make_buffer_rsrc((void *)a_t, 0, (int)((uint32_t)rows_a * (uint32_t)nb * kQ8KBytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)a_t, 0, (int)((uint32_t)rows_a * (uint32_t)nb * kQ8KBytes), 0x00020000);
     const int b0 = slice < nb ? slice : last;
     kq_act_copy<C, 0>(act0, aoff, ra, b0, wave, lane, rows_a, nb);
     kq_load<C, 0>(a_t, w_t, b0, offs, tid, regs);
