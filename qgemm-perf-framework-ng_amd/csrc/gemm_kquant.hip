@@ -667,9 +667,7 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
 #pragma unroll
                     for (int q = 0; q < 16; ++q) {
                         const int row = m0 + wave_m * C::TM * 32 + tm * 32 + mfma_row(lane, q);
-                        // non-temporal: C is not read again here, so it is kept
-                        // from displacing operand tiles in L2
-                        if (row < m) __builtin_nontemporal_store(A.acc[tm][tn][q], &c[(size_t)row * n + col]);
+                        if (row < m) store_through(&c[(size_t)row * n + col], A.acc[tm][tn][q]);
                     }
                 }
             }

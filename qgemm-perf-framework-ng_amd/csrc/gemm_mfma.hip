@@ -390,9 +390,7 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWavesPerEU) void gemm_q4_0_kern
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int row = m0 + wave_m * C::TM * 32 + tm * 32 + mfma_row(lane, r);
-                        // non-temporal: C is not read again here, so it is kept
-                        // from displacing operand tiles in L2
-                        if (row < m) __builtin_nontemporal_store(acc[tm][tn][r] * 0.0625f, &c[(size_t)row * n + col]);
+                        if (row < m) store_through(&c[(size_t)row * n + col], acc[tm][tn][r] * 0.0625f);
                     }
                 }
             }

@@ -633,7 +633,7 @@ __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(co
         float s = red[g * 64 + lane];
         for (int v = 1; v < kMf8Waves; ++v) s += red[(v * 4 * C + g) * 64 + lane];
         const int row = 16 * (g / 4) + 4 * q + g % 4;
-        if (col < n && row < m) c[(size_t)row * n + col] = s * 0.0625f;
+        if (col < n && row < m) store_through(&c[(size_t)row * n + col], s * 0.0625f);
     }
 }
 

@@ -1144,7 +1144,7 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
         float s = red[g * 64 + lane];
         for (int v = 1; v < kKqMfWaves; ++v) s += red[(v * 4 * C + g) * 64 + lane];
         const int row = 16 * (g / 4) + 4 * q + g % 4;
-        if (col < n && row < m) c[(size_t)row * n + col] = s;
+        if (col < n && row < m) store_through(&c[(size_t)row * n + col], s);
     }
 }
 
@@ -1287,7 +1287,7 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
         float s = red[g * 64 + lane];
         for (int v = 1; v < kKqMfWaves; ++v) s += red[(v * 4 * C + g) * 64 + lane];
         const int row = 16 * (g / 4) + 4 * q + g % 4;
-        if (col < n && row < m) c[(size_t)row * n + col] = s;
+        if (col < n && row < m) store_through(&c[(size_t)row * n + col], s);
     }
 }
 
