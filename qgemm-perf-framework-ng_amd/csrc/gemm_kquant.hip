@@ -512,6 +512,22 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
     __shared__ __align__(16) uint8_t rest1[C::kWS * C::kBufBytes];
     __shared__ __align__(16) uint8_t tab[C::kTabBytes];
     const int lane = threadIdx.x & 63;
+    // iq2_xxs grid codes (kernels/iq2_xxs-q8_K-RVV-common/ggml_min.h:69-134):
+    // their address is fixed at load time, so their loads go out before the
+    // wave waits for its kernel arguments, and the tables are built only
+    // after the first stage's copies and loads have been issued: the codes'
+    // trip from L2 overlaps the first stage's from HBM (iq2_xxs
+    // 256x4096x4096 19.6 -> 19.4 us, c3 within noise)
+    constexpr int kCodeIters = C::kQ4K ? 1 : (256 + C::kAllThreads - 1) / C::kAllThreads;
+    uint32_t codes[kCodeIters];
+    if constexpr (!C::kQ4K) {
+#pragma unroll
+        for (int i = 0; i < kCodeIters; ++i) {
+            const int e = (int)threadIdx.x + i * C::kAllThreads;
+            codes[i] = kIq2GridCodes[e < 256 ? e : 255];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
     // slice takes super-blocks slice, slice + WS, ...; slice and wave are
     // wave-uniform (the copies' LDS addresses go to a scalar register)
     const int slice = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / C::kThreads));
@@ -528,11 +544,14 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
     const TileOrigin to = xcd_tile<1>(blockIdx.x, (m + C::kBM - 1) / C::kBM, (n + C::kBN - 1) / C::kBN);
     const int m0 = to.mi * C::kBM, n0 = to.ni * C::kBN;
     const int aoff = slice * C::kAqBytes, roff = slice * C::kBufBytes;  // the slice's part of each array
-    if constexpr (!C::kQ4K) {
-        // grid codes (kernels/iq2_xxs-q8_K-RVV-common/ggml_min.h:69-134): per
-        // value one byte 0, 1 or 2 for the magnitude 8, 25 or 43
-        for (int e = threadIdx.x; e < 256; e += C::kAllThreads) {
-            const uint32_t code = kIq2GridCodes[e];
+    // the iq2_xxs tables in LDS, from the codes loaded above
+    auto build_tables = [&]() __attribute__((always_inline)) {
+        // grid: per value one byte 0, 1 or 2 for the magnitude 8, 25 or 43
+#pragma unroll
+        for (int i = 0; i < kCodeIters; ++i) {
+            const int e = (int)threadIdx.x + i * C::kAllThreads;
+            if (e >= 256) break;
+            const uint32_t code = codes[i];
             uint32_t v[2] = {0, 0};
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[j / 4] |= ((code >> (2 * j)) & 3u) << (8 * (j % 4));
@@ -562,8 +581,7 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
             }
             *reinterpret_cast<uint4 *>(tab + C::kScaleTab + 16 * e) = make_uint4(lp, ln, hp, hn);
         }
-        __syncthreads();
-    }
+    };
 
     KqAcc<C> A;
 #pragma unroll
@@ -593,6 +611,11 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
     const int b0 = slice < nb ? slice : last;
     kq_act_copy<C, 0>(act0, aoff, ra, b0, wave, lane, rows_a, nb);
     kq_load<C, 0>(a_t, w_t, b0, offs, tid, regs);
+    if constexpr (!C::kQ4K) {
+        __builtin_amdgcn_sched_barrier(0);
+        build_tables();
+        __syncthreads();
+    }
     kq_store<C>(rest0, roff, tab, 0, tid, regs);
     kq_load<C, 1>(a_t, w_t, b0, offs, tid, regs);
     __syncthreads();
