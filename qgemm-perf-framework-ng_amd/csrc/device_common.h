@@ -256,6 +256,9 @@ __device__ __forceinline__ void q4_K_scale_min(const uint32_t hd[4], int j, uint
 __device__ __forceinline__ void store_through(float *p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
+__device__ __forceinline__ void store_through(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
