@@ -376,6 +376,33 @@ __device__ __forceinline__ void run_copy(const uint8_t *src, uint32_t rstride, i
                                          0, 0);
     }
 }
+// run_copy without the pad: the run's first kN / 64 * 64 chunks as above,
+// the kN % 64 == 16 chunks left by one 4-byte copy (lane l: dword l % 4 of
+// chunk kN / 64 * 64 + l / 4), so exactly kN * 16 bytes are written, every
+// lane active, and in as many instructions as run_copy issues.
+template <int kRows, int kCols>
+__device__ __forceinline__ void run_copy_exact(const uint8_t *src, uint32_t rstride, int col0, int rvalid,
+                                               uint8_t *dst, int lane) {
+    constexpr int kN = kRows * kCols, kFull = kN / 64;
+    static_assert(kN % 64 == 16, "a 16-chunk tail: one 4-byte copy of 64 lanes");
+#pragma unroll
+    for (int i = 0; i < kFull; ++i) {
+        const int p = 64 * i + lane;
+        int r = p / kCols;
+        const int col = col0 + p - r * kCols;
+        if (r > rvalid - 1) r = rvalid - 1;
+        const uint32_t off = (uint32_t)r * rstride + 16u * (uint32_t)col;
+        __builtin_amdgcn_global_load_lds(src + off, (__attribute__((address_space(3))) void *)(dst + i * 1024), 16,
+                                         0, 0);
+    }
+    const int p = 64 * kFull + (lane >> 2);
+    int r = p / kCols;
+    const int col = col0 + p - r * kCols;
+    if (r > rvalid - 1) r = rvalid - 1;
+    const uint32_t off = (uint32_t)r * rstride + 16u * (uint32_t)col + 4u * (uint32_t)(lane & 3);
+    __builtin_amdgcn_global_load_lds(src + off, (__attribute__((address_space(3))) void *)(dst + kFull * 1024), 4, 0,
+                                     0);
+}
 // chunks of 16 activation rows the chunked MFMA tile GEMVs take (m <= 128)
 constexpr int kMaxGemvChunks = 8;
 

@@ -1186,11 +1186,17 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
 
 // iq2_xxs, from k = 4096 at k % 2048 == 0: as gemv_q4_K_mfma_chunk_kernel, with the
 // weight decode of gemv_iq2_xxs_mfma_sb_kernel done once per wave (5 weight
-// columns per row, H1 = activation chunks 8..16) and the grid and sign tables
-// copied by waves 0..2 before everything else.
-constexpr int kIq2ChunkWaveBytes = 8 * 1024;  // weight run 2 KB, H0 and H1 3 KB each
+// columns per row, H1 = activation chunks 8..16). Every wave copies the grid
+// and sign tables into its own LDS region before everything else and reads
+// only that copy, so no wave waits at a workgroup barrier for another's
+// table (against one shared copy behind a barrier, 4096 x 4096: M = 16
+// 5.20 -> 4.70 us, M = 32 6.04 -> 5.54, M = 128 13.95 -> 13.11).
+// To fit 16 such regions the runs are copied without pad (run_copy_exact):
+// per wave the tables (3 KB), the weight run (1280 B) and H0, H1 (2304 B each).
+constexpr int kIq2ChunkRunW = 16 * 5 * 16, kIq2ChunkRunH = 16 * 9 * 16;
+constexpr int kIq2ChunkWaveBytes = kIq2TableBytes + kIq2ChunkRunW + 2 * kIq2ChunkRunH;  // 8960
 
-__host__ __device__ constexpr int iq2_chunk_lds_bytes() { return kIq2TableBytes + kKqMfWaves * kIq2ChunkWaveBytes; }
+__host__ __device__ constexpr int iq2_chunk_lds_bytes() { return kKqMfWaves * kIq2ChunkWaveBytes; }
 
 template <int C, int kG>
 __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kernel(const uint8_t *__restrict__ w,
@@ -1202,24 +1208,23 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
     // is fixed at compile time (k = 4096: one round, constant strides), else groups
     const int nsb = kG > 0 ? kG : groups;
     const uint32_t kARow = (uint32_t)nsb * kQ8KBytes;
-    constexpr int kH = run_copies<16, 9>();
+    constexpr int kH = run_copies<16, 9>();  // instructions per copy (run_copy_exact issues as many)
     constexpr int kW = run_copies<16, 5>();
-    static_assert(kH * 1024 <= 3072 && kW * 1024 <= 2048, "run sizes");
+    static_assert(kIq2ChunkRunH == 16 * 9 * 16 && kIq2ChunkRunW == 16 * 5 * 16, "run sizes");
     static_assert(kKqMfWaves * 4 * C * 64 * 4 <= iq2_chunk_lds_bytes(), "wave partials fit the LDS");
     extern __shared__ __align__(16) uint8_t lds[];
-    uint8_t *grid = lds;  // grid magnitudes, then sign masks
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int n0 = blockIdx.x * 16;
     const int o2 = 2 * (wave & 7), o = 4 * (wave & 3);
-    uint8_t *wl = lds + kIq2TableBytes + wave * kIq2ChunkWaveBytes, *h0 = wl + 2048, *h1 = wl + 5120;
+    uint8_t *grid = lds + wave * kIq2ChunkWaveBytes;  // grid magnitudes, then sign masks
+    uint8_t *wl = grid + kIq2TableBytes, *h0 = wl + kIq2ChunkRunW, *h1 = h0 + kIq2ChunkRunH;
     static_assert(kIq2TableBytes == 3 * 1024, "three 1-KB table pieces");
-    if (wave < 3) {
-        const uint8_t *tsrc = wave < 2 ? reinterpret_cast<const uint8_t *>(&kIq2Grid) + wave * 1024
-                                       : reinterpret_cast<const uint8_t *>(&kIq2Signs);
-        __builtin_amdgcn_global_load_lds(tsrc + 16 * lane, (__attribute__((address_space(3))) void *)(grid + wave * 1024),
-                                         16, 0, 0);
-    }
+    // the table's address is fixed at load time: its copies go out first
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(&kIq2Tables) + 1024 * i + 16 * lane,
+                                         (__attribute__((address_space(3))) void *)(grid + 1024 * i), 16, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     float acc[C][4];
 #pragma unroll
@@ -1228,11 +1233,8 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
         for (int r = 0; r < 4; ++r) acc[ch][r] = 0.0f;
     // round rnd takes the wave's K slice 16 rnd + wave of every row; the next
     // round's copies start once the last round's buffers have been read
-    // this wave's rounds: its super-blocks wave, wave + 16, ... below nsb; a wave
-    // without any (nsb < 16) still takes round 0's table barrier, so that every
-    // wave reaches the same barriers (waves 0..2, which copy the tables, have one)
+    // this wave's rounds: its super-blocks wave, wave + 16, ... below nsb
     const int my_rounds = (nsb - wave + kKqMfWaves - 1) / kKqMfWaves;
-    if (my_rounds == 0) asm volatile("s_barrier" ::: "memory");
 #pragma clang loop unroll(disable)
     for (int rnd = 0; rnd < my_rounds; ++rnd) {
         // a lane index the compiler cannot carry across rounds: the per-lane
@@ -1247,16 +1249,17 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int sb = kKqMfWaves * rnd + wave;
         const uint8_t *asrc = a + sb * kQ8KBytes - o;
-        auto copy_h0 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, cl); };
-        auto copy_h1 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 8, m - 16 * ch, h1, cl); };
-        run_copy<16, 5>(w + ((size_t)n0 * nsb + sb) * kIq2Bytes - o2, nsb * kIq2Bytes, 0, n - n0, wl, cl);
+        auto copy_h0 = [&](int ch) {
+            run_copy_exact<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, cl);
+        };
+        auto copy_h1 = [&](int ch) {
+            run_copy_exact<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 8, m - 16 * ch, h1, cl);
+        };
+        run_copy_exact<16, 5>(w + ((size_t)n0 * nsb + sb) * kIq2Bytes - o2, nsb * kIq2Bytes, 0, n - n0, wl, cl);
         copy_h0(0);
         copy_h1(0);
-        // the table piece has landed once at most (weights + H0 + H1) loads are
-        // outstanding; round 0 only, which every wave runs (waves can differ in
-        // their number of rounds, and the reduction's barrier follows the loop)
-        if (rnd == 0) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kW + 2 * kH) : "memory");
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // weights and H0(0)
+        // weights and H0(0) (and, issued before them, the table copies)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");
         // the weight row's decode, once: group q of every sub-block, its scale, d
         const uint8_t *wr = wl + li * 80;  // weight block byte b at copy byte o2 + b
         const uint32_t sh = (uint32_t)(o2 + 2) & 3u;
