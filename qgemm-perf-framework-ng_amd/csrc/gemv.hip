@@ -510,6 +510,14 @@ constexpr int kMf8Waves = 16;
 // 5.15, m = 8 5.42 / 5.16, m = 16 5.83 / 5.28; below m = 6 the pairs kernel
 // is faster (m = 5 4.93 / 5.15).
 constexpr int kQ40ChunkWaveBytes = 9 * 1024;  // weight run, H0, H1: 3 KB each
+// One chunk (m <= 16): the 16 waves' partials (16 KB) get a region of their
+// own past the wave buffers (160 KB in all), so a wave stores them as soon as
+// it is done and one barrier suffices; with more chunks they reuse the
+// buffers after a first barrier (4096 x 4096: m = 16 5.06 -> 5.01 us, m = 8
+// 4.75 -> 4.72).
+template <int C> constexpr int q4_0_chunk_lds_bytes() {
+    return kMf8Waves * kQ40ChunkWaveBytes + (C == 1 ? kMf8Waves * 4 * 64 * 4 : 0);
+}
 
 template <int C, int kG>
 __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(const uint8_t *__restrict__ w,
@@ -525,6 +533,7 @@ __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(co
     constexpr int kH = run_copies<16, 9>();
     static_assert(kH * 1024 <= 3072, "3 KB per run");
     static_assert(kMf8Waves * 4 * C * 64 * 4 <= kMf8Waves * kQ40ChunkWaveBytes, "wave partials fit the LDS");
+    static_assert(q4_0_chunk_lds_bytes<C>() <= 160 * 1024, "the LDS of one CU");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -620,9 +629,9 @@ __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(co
     }
     // wave partials through LDS ([wave][group g = 4 chunk + r][lane]); wave w
     // adds groups w, w + 16, ... over the waves in wave order and stores them
-    __syncthreads();
+    if constexpr (C > 1) __syncthreads();  // the partials reuse the wave buffers
     const int li = lane & 15, q = lane >> 4;
-    float *red = reinterpret_cast<float *>(lds);
+    float *red = reinterpret_cast<float *>(lds + (C == 1 ? kMf8Waves * kQ40ChunkWaveBytes : 0));
 #pragma unroll
     for (int ch = 0; ch < C; ++ch)
 #pragma unroll
@@ -642,7 +651,7 @@ __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(co
 template <int C>
 void launch_q4_0_chunk(const uint8_t *w, const uint8_t *a, float *c, int m, int n, int ng, hipStream_t stream) {
     const dim3 grid((unsigned)((n + 15) / 16)), block(kMf8Waves * 64);
-    const size_t lds = (size_t)kMf8Waves * kQ40ChunkWaveBytes;
+    const size_t lds = (size_t)q4_0_chunk_lds_bytes<C>();
     if (ng == kMf8Waves)
         hipLaunchKernelGGL((gemv_q4_0_mfma_chunk_kernel<C, kMf8Waves>), grid, block, lds, stream, w, a, c, m, n, ng);
     else

@@ -1055,7 +1055,15 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_sb_kernel(c
 // kernel); iq2_xxs m = 8 5.53 / 5.61, m = 9 5.85 / 5.78, m = 16 6.27 / 5.98.
 constexpr int kChunkWaveBytes = 9 * 1024;  // per wave: weight run, H0, H1 (3 KB each)
 
-__host__ __device__ constexpr int q4k_chunk_lds_bytes() { return kKqMfWaves * kChunkWaveBytes; }
+// One chunk (m <= 16): the waves' partials (16 KB) get a region of their own
+// past the wave buffers, so a wave stores them as soon as it is done and one
+// barrier suffices (as gemv_q4_0_mfma_chunk_kernel; with more chunks they
+// reuse the buffers after a first barrier). q4_K 4096 x 4096, m = 8: 4.46 ->
+// 4.43 us; m = 16 and iq2_xxs within noise.
+constexpr int kChunkPartialBytes = kKqMfWaves * 4 * 64 * 4;
+__host__ __device__ constexpr int q4k_chunk_lds_bytes(int c) {
+    return kKqMfWaves * kChunkWaveBytes + (c == 1 ? kChunkPartialBytes : 0);
+}
 
 template <int C, int kG>
 __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(const uint8_t *__restrict__ w,
@@ -1069,7 +1077,8 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
     const uint32_t kARow = (uint32_t)nsb * kQ8KBytes;
     constexpr int kH = run_copies<16, 11>();  // instructions per half (H1: 11 columns, H0: 9)
     static_assert(run_copies<16, 9>() == kH && run_copies<16, 9>() * 1024 <= 3072, "3 KB per run");
-    static_assert(kKqMfWaves * 4 * C * 64 * 4 <= q4k_chunk_lds_bytes(), "wave partials fit the LDS");
+    static_assert(kKqMfWaves * 4 * C * 64 * 4 <= q4k_chunk_lds_bytes(2), "wave partials fit the buffers");
+    static_assert(q4k_chunk_lds_bytes(C) <= 160 * 1024, "the LDS of one CU");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -1167,9 +1176,9 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
     }
     // wave partials through LDS ([wave][group g = 4 chunk + r][lane]); wave w
     // adds groups w, w + 16, ... over the waves in wave order and stores them
-    __syncthreads();
+    if constexpr (C > 1) __syncthreads();  // the partials reuse the wave buffers
     const int li = lane & 15, q = lane >> 4;
-    float *red = reinterpret_cast<float *>(lds);
+    float *red = reinterpret_cast<float *>(lds + (C == 1 ? kKqMfWaves * kChunkWaveBytes : 0));
 #pragma unroll
     for (int ch = 0; ch < C; ++ch)
 #pragma unroll
@@ -1196,7 +1205,9 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
 constexpr int kIq2ChunkRunW = 16 * 5 * 16, kIq2ChunkRunH = 16 * 9 * 16;
 constexpr int kIq2ChunkWaveBytes = kIq2TableBytes + kIq2ChunkRunW + 2 * kIq2ChunkRunH;  // 8960
 
-__host__ __device__ constexpr int iq2_chunk_lds_bytes() { return kKqMfWaves * kIq2ChunkWaveBytes; }
+__host__ __device__ constexpr int iq2_chunk_lds_bytes(int c) {
+    return kKqMfWaves * kIq2ChunkWaveBytes + (c == 1 ? kChunkPartialBytes : 0);
+}
 
 template <int C, int kG>
 __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kernel(const uint8_t *__restrict__ w,
@@ -1211,7 +1222,8 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
     constexpr int kH = run_copies<16, 9>();  // instructions per copy (run_copy_exact issues as many)
     constexpr int kW = run_copies<16, 5>();
     static_assert(kIq2ChunkRunH == 16 * 9 * 16 && kIq2ChunkRunW == 16 * 5 * 16, "run sizes");
-    static_assert(kKqMfWaves * 4 * C * 64 * 4 <= iq2_chunk_lds_bytes(), "wave partials fit the LDS");
+    static_assert(kKqMfWaves * 4 * C * 64 * 4 <= iq2_chunk_lds_bytes(2), "wave partials fit the buffers");
+    static_assert(iq2_chunk_lds_bytes(C) <= 160 * 1024, "the LDS of one CU");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -1313,9 +1325,9 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
     }
     // wave partials through LDS ([wave][group g = 4 chunk + r][lane]); wave w
     // adds groups w, w + 16, ... over the waves in wave order and stores them
-    __syncthreads();
+    if constexpr (C > 1) __syncthreads();  // the partials reuse the wave buffers
     const int li = lane & 15, q = lane >> 4;
-    float *red = reinterpret_cast<float *>(lds);
+    float *red = reinterpret_cast<float *>(lds + (C == 1 ? kKqMfWaves * kIq2ChunkWaveBytes : 0));
 #pragma unroll
     for (int ch = 0; ch < C; ++ch)
 #pragma unroll
@@ -1336,7 +1348,7 @@ template <int C>
 void launch_kq_chunk(bool q4k, const uint8_t *w, const uint8_t *a, float *c, int m, int n, int nsb,
                      hipStream_t stream) {
     const dim3 grid((unsigned)((n + 15) / 16)), block(kKqMfWaves * 64);
-    const size_t lds = q4k ? (size_t)q4k_chunk_lds_bytes() : (size_t)iq2_chunk_lds_bytes();
+    const size_t lds = q4k ? (size_t)q4k_chunk_lds_bytes(C) : (size_t)iq2_chunk_lds_bytes(C);
     if (q4k && nsb == kKqMfWaves)
         hipLaunchKernelGGL((gemv_q4_K_mfma_chunk_kernel<C, kKqMfWaves>), grid, block, lds, stream, w, a, c, m, n, nsb);
     else if (q4k)
