@@ -562,9 +562,9 @@ __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(co
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int kb0 = (kMf8Waves * rnd + wave) * kMf8Blocks;  // the wave's first block
         const uint8_t *asrc = a + kb0 * 34;  // the wave's slice of activation row 0
-        auto copy_h0 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, cl); };
-        auto copy_h1 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 8, m - 16 * ch, h1, cl); };
-        run_copy<16, 9>(w + ((size_t)n0 * nb + kb0) * 18, nb * 18, 0, n - n0, wl, cl);
+        auto copy_h0 = [&](int ch) { copy_run<C, 16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, cl); };
+        auto copy_h1 = [&](int ch) { copy_run<C, 16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 8, m - 16 * ch, h1, cl); };
+        copy_run<C, 16, 9>(w + ((size_t)n0 * nb + kb0) * 18, nb * 18, 0, n - n0, wl, cl);
         copy_h0(0);
         copy_h1(0);
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // weights and H0(0)

@@ -1108,9 +1108,9 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int sb = kKqMfWaves * rnd + wave;
         const uint8_t *asrc = a + sb * kQ8KBytes - o;  // copy start of the wave's block in activation row 0
-        auto copy_h0 = [&](int ch) { run_copy<16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, cl); };
+        auto copy_h0 = [&](int ch) { copy_run<C, 16, 9>(asrc + (size_t)ch * 16 * kARow, kARow, 0, m - 16 * ch, h0, cl); };
         auto copy_h1 = [&](int ch) { run_copy<16, 11>(asrc + (size_t)ch * 16 * kARow, kARow, 8, m - 16 * ch, h1, cl); };
-        run_copy<16, 9>(w + ((size_t)n0 * nsb + sb) * 144, nsb * 144, 0, n - n0, wl, cl);
+        copy_run<C, 16, 9>(w + ((size_t)n0 * nsb + sb) * 144, nsb * 144, 0, n - n0, wl, cl);
         copy_h0(0);
         copy_h1(0);
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kH) : "memory");  // weights and H0(0)
