@@ -929,13 +929,18 @@ __device__ __forceinline__ void sb_copy(const uint8_t *wsrc, const uint8_t *asrc
 // byte 48) and activation chunks 0..8; half 1: weight chunks 2..4 (chunk 2
 // twice, so that sub-blocks 4..7, bytes 34..65, lie in one region) and
 // activation chunks 8..16 (bytes 132..259 lie at or past copy byte 128). The
-// grid and sign tables are copied into LDS by
-// direct loads issued before the run, and published by a barrier that waits
-// for them only, not for the run, which each wave waits for itself.
+// grid and sign tables are copied into LDS by direct loads issued before the
+// run. Where a wave's run is 4 KB or more (m >= 6) each wave copies them into
+// the front of its own region and reads only that copy, with no barrier (m = 8:
+// 5.05 -> 4.91 us); at m = 5 (3 KB runs, 4.78 against 4.89 us that way) waves
+// 0..2 copy one shared set, published by a barrier that waits for it only,
+// not for the run, which each wave waits for itself.
 typedef uint64_t u64_a4 __attribute__((aligned(4)));  // 8-byte value at a dword-aligned address
 
+__host__ __device__ constexpr bool iq2_sb_private_tables(int m) { return sb_copies<Iq2Run>(m) >= 4; }
 __host__ __device__ constexpr int iq2_sb_lds_bytes(int m) {
-    return kIq2TableBytes + kKqMfWaves * sb_copies<Iq2Run>(m) * 1024;
+    return iq2_sb_private_tables(m) ? kKqMfWaves * (kIq2TableBytes + sb_copies<Iq2Run>(m) * 1024)
+                                    : kIq2TableBytes + kKqMfWaves * sb_copies<Iq2Run>(m) * 1024;
 }
 
 template <int M>
@@ -949,16 +954,25 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_sb_kernel(c
     constexpr int kCopies = sb_copies<R>(M);
     constexpr int kAfterHalf0 = kCopies - (kH0 + 63) / 64;  // instructions issued after those writing half 0
     extern __shared__ __align__(16) uint8_t lds[];
-    uint8_t *grid = lds;  // grid magnitudes, then sign masks
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int n0 = blockIdx.x * 16;
     const int o2 = 2 * (wave & 7), o = 4 * (wave & 3);
-    uint8_t *base = lds + kIq2TableBytes + wave * kCopies * 1024;
-    // the tables by direct loads as well, issued first: waves 0 and 1 copy the
-    // two halves of the grid, wave 2 the sign masks (1 KB each)
+    constexpr bool kPrivate = iq2_sb_private_tables(M);
     static_assert(kIq2TableBytes == 3 * 1024, "three 1-KB table pieces");
-    if (wave < 3) {
+    // grid magnitudes, then sign masks: the wave's own copy at the front of
+    // its region, or one shared copy before all regions
+    uint8_t *grid = kPrivate ? lds + wave * (kIq2TableBytes + kCopies * 1024) : lds;
+    uint8_t *base = kPrivate ? grid + kIq2TableBytes : lds + kIq2TableBytes + wave * kCopies * 1024;
+    // the tables by direct loads as well, issued first (their address is fixed
+    // at load time), 1 KB each: every wave its three, or waves 0 and 1 the two
+    // halves of the grid and wave 2 the sign masks
+    if constexpr (kPrivate) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(&kIq2Tables) + 1024 * i + 16 * lane,
+                                             (__attribute__((address_space(3))) void *)(grid + 1024 * i), 16, 0, 0);
+    } else if (wave < 3) {
         const uint8_t *tsrc = wave < 2 ? reinterpret_cast<const uint8_t *>(&kIq2Grid) + wave * 1024
                                        : reinterpret_cast<const uint8_t *>(&kIq2Signs);
         __builtin_amdgcn_global_load_lds(tsrc + 16 * lane, (__attribute__((address_space(3))) void *)(grid + wave * 1024),
@@ -966,8 +980,10 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_sb_kernel(c
     }
     __builtin_amdgcn_sched_barrier(0);
     sb_copy<R, M>(w + ((size_t)n0 * nsb + wave) * kIq2Bytes - o2, a + wave * kQ8KBytes - o, base, lane, n - n0);
-    // the table piece has landed once at most kCopies loads are outstanding
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kCopies) : "memory");
+    // a shared table piece has landed once at most kCopies loads are
+    // outstanding; a private copy, issued before the run, is covered by the
+    // run's own first wait
+    if constexpr (!kPrivate) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kCopies) : "memory");
     const int li = lane & 15, q = lane >> 4;  // q: the sub-block's group of 8 K positions this lane holds
     const int arow = li < M ? li : M - 1;
     int orow[4];

@@ -144,13 +144,15 @@ def test_dma_lds_address_is_scalar(source):
     assert dma_m0_from_vector(lines) == []
 
 
-def check_half_split(lines: list[str], copies: int, after_half0: int) -> None:
+def check_half_split(lines: list[str], copies: int, after_half0: int, lead: int = 0) -> None:
     """Two-half copies (the iq2_xxs M = 5..8 MFMA tile GEMV): the wave's run of
     `copies` direct-to-LDS instructions writes consecutive 1-KB pieces of its
     LDS region in issue order (M0 = base + 0x400 i), and the first wait after
     the run is vmcnt(after_half0): loads complete in issue order, so it holds
     the wave until the instructions that wrote half 0 have landed. A run
-    reordered by the compiler would make that wait cover the wrong pieces."""
+    reordered by the compiler would make that wait cover the wrong pieces.
+    `lead` copies into the same region (the wave's own table pieces, issued
+    before the run) are dropped first; they must precede the run."""
     run, m0 = [], None
     for i, t in enumerate(lines):
         m = re.match(r"s_mov_b32 m0, (s\d+)$", t)
@@ -163,7 +165,8 @@ def check_half_split(lines: list[str], copies: int, after_half0: int) -> None:
             m0 = None  # a base plus a register: not part of the run (a table piece)
         if t.startswith("global_load_lds") and m0 is not None:
             run.append((i, m0))
-    assert len(run) == copies, f"{len(run)} run copies, expected {copies}"
+    assert len(run) == copies + lead, f"{len(run)} copies, expected {lead} + {copies}"
+    run = run[lead:]
     assert len({b for _, (b, _) in run}) == 1, "the run's copies use different LDS bases"
     offsets = [o for _, (_, o) in run]
     assert offsets == [0x400 * (offsets[0] // 0x400 + k) for k in range(copies)], f"run out of order: {offsets}"
@@ -185,19 +188,27 @@ def test_half_split_checker():
         check_half_split(good, 3, 2)
     table = ["s_add_i32 m0, s14, s8", "global_load_lds_dwordx4 v1, s[8:9]"] + good[:6] + ["s_waitcnt vmcnt(3)"] + good[6:]
     check_half_split(table, 3, 1)
+    # two leading pieces into the same region, then the run at 0x800..
+    lead = ["s_mov_b32 m0, s14", "global_load_lds_dwordx4 v1, s[8:9]", "s_add_i32 m0, s14, 0x400",
+            "global_load_lds_dwordx4 v1, s[8:9]"]
+    run3 = lead + ["s_add_i32 m0, s14, 0x800", good[1], "s_add_i32 m0, s14, 0xc00", good[3],
+                   "s_add_i32 m0, s14, 0x1000", good[5]] + good[6:]
+    check_half_split(run3, 3, 1, lead=2)
+    with pytest.raises(AssertionError):  # the leading pieces not declared
+        check_half_split(run3, 3, 1)
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC) or shutil.which("make") is None, reason="needs hipcc and make")
-@pytest.mark.parametrize("source,kernel,copies,after_half0", [
-    ("gemv_kquant.hip", "gemv_iq2_xxs_mfma_sb_kernelILi5E", 3, 1),
-    ("gemv_kquant.hip", "gemv_iq2_xxs_mfma_sb_kernelILi8E", 4, 2),
+@pytest.mark.parametrize("source,kernel,copies,after_half0,lead", [
+    ("gemv_kquant.hip", "gemv_iq2_xxs_mfma_sb_kernelILi5E", 3, 1, 0),
+    ("gemv_kquant.hip", "gemv_iq2_xxs_mfma_sb_kernelILi8E", 4, 2, 3),  # its own three table pieces first
 ])
-def test_half_split_copy_order(source, kernel, copies, after_half0):
+def test_half_split_copy_order(source, kernel, copies, after_half0, lead):
     out = os.path.join(PKG_DIR, "_build", source + ".s")
     subprocess.run(["make", "-s", "-C", PKG_DIR, out], check=True, capture_output=True, timeout=600)
     with open(out) as f:
         asm = f.read()
-    check_half_split(_kernel_lines(asm, kernel), copies, after_half0)
+    check_half_split(_kernel_lines(asm, kernel), copies, after_half0, lead)
 
 
 def check_chunk_waits(lines: list[str], chunks: int, table_wait: int | None = None) -> None:
