@@ -513,8 +513,8 @@ __global__ __launch_bounds__(C::kAllThreads, 2) void gemm_kq_kernel(const uint8_
     __shared__ __align__(16) uint8_t tab[C::kTabBytes];
     const int lane = threadIdx.x & 63;
     // iq2_xxs grid codes (kernels/iq2_xxs-q8_K-RVV-common/ggml_min.h:69-134):
-    // their address is fixed at load time, so their loads go out before the
-    // wave waits for its kernel arguments, and the tables are built only
+    // their address is fixed at load time, so their loads go out before
+    // anything that needs a kernel argument, and the tables are built only
     // after the first stage's copies and loads have been issued: the codes'
     // trip from L2 overlaps the first stage's from HBM (iq2_xxs
     // 256x4096x4096 19.6 -> 19.4 us, c3 within noise)

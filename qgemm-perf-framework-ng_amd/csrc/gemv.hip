@@ -557,8 +557,8 @@ __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(co
         if constexpr (kG == 0) asm volatile("" : "+v"(cl));
         const int li = cl & 15, q = cl >> 4;
         // the last round's LDS reads are done before its buffers are refilled (in
-        // round 0 this covers the kernel arguments' scalar loads, needed anyway;
-        // a wait in round 0 only would make the compiler peel that round)
+        // round 0 there is nothing to wait for; a wait in the later rounds only
+        // would make the compiler peel round 0)
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int kb0 = (kMf8Waves * rnd + wave) * kMf8Blocks;  // the wave's first block
         const uint8_t *asrc = a + kb0 * 34;  // the wave's slice of activation row 0

@@ -322,9 +322,10 @@ __global__ __launch_bounds__(kThreads) void gemv_iq2_xxs_kernel(const uint8_t *_
                                                                int n, int nb) {
     __shared__ __align__(16) uint8_t tables[(kThreads / 64) * kIq2TableBytes];
     const int lane = threadIdx.x & 63;
-    // the table's address is fixed at load time: its loads go out before the
-    // wave waits for its kernel arguments (3.55 against 3.85 us when they
-    // are issued after that wait)
+    // the table's address is fixed at load time: its loads go out first,
+    // before anything that needs a kernel argument (where the arguments are
+    // loaded rather than preloaded, before the wave waits for them: 3.55
+    // against 3.85 us when issued after that wait)
     uint32_t tab[12];
     load_iq2_tables_wave(tab, lane);
     __builtin_amdgcn_sched_barrier(0);
@@ -1119,8 +1120,8 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
         if constexpr (kG == 0) asm volatile("" : "+v"(cl));
         const int li = cl & 15, q = cl >> 4;
         // the last round's LDS reads are done before its buffers are refilled (in
-        // round 0 this covers the kernel arguments' scalar loads, needed anyway;
-        // a wait in round 0 only would make the compiler peel that round)
+        // round 0 there is nothing to wait for; a wait in the later rounds only
+        // would make the compiler peel round 0)
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int sb = kKqMfWaves * rnd + wave;
         const uint8_t *asrc = a + sb * kQ8KBytes - o;  // copy start of the wave's block in activation row 0
@@ -1272,8 +1273,8 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
         if constexpr (kG == 0) asm volatile("" : "+v"(cl));
         const int li = cl & 15, q = cl >> 4;
         // the last round's LDS reads are done before its buffers are refilled (in
-        // round 0 this covers the kernel arguments' scalar loads, needed anyway;
-        // a wait in round 0 only would make the compiler peel that round)
+        // round 0 there is nothing to wait for; a wait in the later rounds only
+        // would make the compiler peel round 0)
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int sb = kKqMfWaves * rnd + wave;
         const uint8_t *asrc = a + sb * kQ8KBytes - o;
