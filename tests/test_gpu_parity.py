@@ -112,6 +112,33 @@ def test_quantize_q8_K_bit_exact(hip, torch_gpu, oracle, rows, k):
     assert np.array_equal(got.cpu().numpy().reshape(-1), expect.view(np.uint8).reshape(-1))
 
 
+@pytest.mark.parametrize("name,rows,k", [("q8_0", 3, 1280), ("q8_0", 1, 64), ("q8_K", 3, 1280), ("q8_K", 5, 4096)])
+@pytest.mark.parametrize("offset", [2, 4, 16])
+def test_quantize_output_alignment(hip, torch_gpu, oracle, name, rows, k, offset):
+    """Both store paths: a dword-aligned output is assembled in LDS and written
+    through as dwords (offsets 4 and 16), a q8_0 output at an odd half-word is
+    stored in 16-bit pieces (offset 2; q8_K outputs must be 4-byte aligned, and
+    the library rejects one at offset 2 before launching anything). Ragged
+    shapes leave the last workgroup partly empty; the bytes around the output
+    must stay untouched."""
+    torch = torch_gpu
+    say(f"quantize {name} rows={rows} k={k} output offset {offset}")
+    rng = np.random.default_rng(rows * 11 + k + offset)
+    x = (rng.standard_normal((rows, k)) * rng.uniform(1e-3, 50, (rows, 1))).astype(np.float32)
+    fn, ref = (hip.quantize_q8_0, oracle.quantize_q8_0) if name == "q8_0" else (hip.quantize_q8_K, oracle.quantize_q8_K)
+    nbytes = rows * (k // 32) * 34 if name == "q8_0" else rows * (k // 256) * 292
+    buf = torch.full((nbytes + 64,), 0xA5, dtype=torch.uint8, device="cuda")
+    if name == "q8_K" and offset % 4:
+        with pytest.raises(RuntimeError, match="4-byte aligned"):
+            fn(dev(torch, x), out=buf[offset:offset + nbytes])
+        return
+    fn(dev(torch, x), out=buf[offset:offset + nbytes])
+    torch.cuda.synchronize()
+    got = buf.cpu().numpy()
+    assert np.array_equal(got[offset:offset + nbytes], ref(x).view(np.uint8).reshape(-1))
+    assert (got[:offset] == 0xA5).all() and (got[offset + nbytes:] == 0xA5).all(), "bytes outside the output written"
+
+
 @pytest.mark.parametrize("name", ["q8_0", "q8_K"])
 def test_quantizer_edges_match_reference_fixture(hip, torch_gpu, name):
     torch = torch_gpu
