@@ -510,13 +510,14 @@ constexpr int kMf8Waves = 16;
 // 5.15, m = 8 5.42 / 5.16, m = 16 5.83 / 5.28; below m = 6 the pairs kernel
 // is faster (m = 5 4.93 / 5.15).
 constexpr int kQ40ChunkWaveBytes = 9 * 1024;  // weight run, H0, H1: 3 KB each
-// One chunk (m <= 16): the 16 waves' partials (16 KB) get a region of their
-// own past the wave buffers (160 KB in all), so a wave stores them as soon as
-// it is done and one barrier suffices; with more chunks they reuse the
-// buffers after a first barrier (4096 x 4096: m = 16 5.06 -> 5.01 us, m = 8
-// 4.75 -> 4.72).
+// A wave stores its partials as soon as it is done and one barrier suffices
+// (against a first barrier and shared buffers, 4096 x 4096): with one chunk
+// (m <= 16) into a 16 KB region of their own past the wave buffers (m = 16
+// 5.06 -> 5.01 us, m = 8 4.75 -> 4.72), with more chunks into the wave's own
+// buffers (C KB of its 9), which no other wave reads and whose last copy has
+// landed once it is done (m = 32 6.88 -> 6.77 us, m = 128 15.32 -> 15.20).
 template <int C> constexpr int q4_0_chunk_lds_bytes() {
-    return kMf8Waves * kQ40ChunkWaveBytes + (C == 1 ? kMf8Waves * 4 * 64 * 4 : 0);
+    return kMf8Waves * kQ40ChunkWaveBytes + (C == 1 ? kMf8Waves * 1024 : 0);
 }
 
 template <int C, int kG>
@@ -532,7 +533,7 @@ __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(co
     const uint32_t kARow = (uint32_t)nb * 34;
     constexpr int kH = run_copies<16, 9>();
     static_assert(kH * 1024 <= 3072, "3 KB per run");
-    static_assert(kMf8Waves * 4 * C * 64 * 4 <= kMf8Waves * kQ40ChunkWaveBytes, "wave partials fit the LDS");
+    static_assert(4 * C * 64 * 4 <= kQ40ChunkWaveBytes, "a wave's partials fit its buffers");
     static_assert(q4_0_chunk_lds_bytes<C>() <= 160 * 1024, "the LDS of one CU");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
@@ -627,20 +628,23 @@ __global__ __launch_bounds__(kMf8Waves * 64) void gemv_q4_0_mfma_chunk_kernel(co
             }
         }
     }
-    // wave partials through LDS ([wave][group g = 4 chunk + r][lane]); wave w
-    // adds groups w, w + 16, ... over the waves in wave order and stores them
-    if constexpr (C > 1) __syncthreads();  // the partials reuse the wave buffers
+    // wave partials through LDS, each wave's in a region only it writes
+    // ([group g = 4 chunk + r][lane]); wave w adds groups w, w + 16, ... over
+    // the waves in wave order and stores them
     const int li = lane & 15, q = lane >> 4;
+    // wave v's partials at red + v * kStride: a compile-time stride, so the
+    // reads below take immediate offsets from one address
     float *red = reinterpret_cast<float *>(lds + (C == 1 ? kMf8Waves * kQ40ChunkWaveBytes : 0));
+    constexpr int kStride = (C == 1 ? 1024 : kQ40ChunkWaveBytes) / 4;
 #pragma unroll
     for (int ch = 0; ch < C; ++ch)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[((wave * C + ch) * 4 + r) * 64 + lane] = acc[ch][r];
+        for (int r = 0; r < 4; ++r) red[wave * kStride + (ch * 4 + r) * 64 + lane] = acc[ch][r];
     __syncthreads();
     const int col = n0 + li;
     for (int g = wave; g < 4 * C; g += kMf8Waves) {
         float s = red[g * 64 + lane];
-        for (int v = 1; v < kMf8Waves; ++v) s += red[(v * 4 * C + g) * 64 + lane];
+        for (int v = 1; v < kMf8Waves; ++v) s += red[v * kStride + g * 64 + lane];
         const int row = 16 * (g / 4) + 4 * q + g % 4;
         if (col < n && row < m) store_through(&c[(size_t)row * n + col], s * 0.0625f);
     }

@@ -1072,12 +1072,12 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_sb_kernel(c
 // kernel); iq2_xxs m = 8 5.53 / 5.61, m = 9 5.85 / 5.78, m = 16 6.27 / 5.98.
 constexpr int kChunkWaveBytes = 9 * 1024;  // per wave: weight run, H0, H1 (3 KB each)
 
-// One chunk (m <= 16): the waves' partials (16 KB) get a region of their own
-// past the wave buffers, so a wave stores them as soon as it is done and one
-// barrier suffices (as gemv_q4_0_mfma_chunk_kernel; with more chunks they
-// reuse the buffers after a first barrier). q4_K 4096 x 4096, m = 8: 4.46 ->
-// 4.43 us; m = 16 and iq2_xxs within noise.
-constexpr int kChunkPartialBytes = kKqMfWaves * 4 * 64 * 4;
+// A wave stores its partials as soon as it is done and one barrier suffices
+// (as gemv_q4_0_mfma_chunk_kernel): with one chunk into a 16 KB region of
+// their own past the wave buffers (against a first barrier and shared
+// buffers, q4_K 4096 x 4096, m = 8: 4.46 -> 4.43 us), with more chunks into
+// the wave's own buffers (iq2_xxs m = 128: 13.00 -> 12.68 us).
+constexpr int kChunkPartialBytes = kKqMfWaves * 1024;
 __host__ __device__ constexpr int q4k_chunk_lds_bytes(int c) {
     return kKqMfWaves * kChunkWaveBytes + (c == 1 ? kChunkPartialBytes : 0);
 }
@@ -1094,7 +1094,7 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
     const uint32_t kARow = (uint32_t)nsb * kQ8KBytes;
     constexpr int kH = run_copies<16, 11>();  // instructions per half (H1: 11 columns, H0: 9)
     static_assert(run_copies<16, 9>() == kH && run_copies<16, 9>() * 1024 <= 3072, "3 KB per run");
-    static_assert(kKqMfWaves * 4 * C * 64 * 4 <= q4k_chunk_lds_bytes(2), "wave partials fit the buffers");
+    static_assert(4 * C * 64 * 4 <= kChunkWaveBytes, "a wave's partials fit its buffers");
     static_assert(q4k_chunk_lds_bytes(C) <= 160 * 1024, "the LDS of one CU");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
@@ -1191,20 +1191,23 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_q4_K_mfma_chunk_kernel(c
             }
         }
     }
-    // wave partials through LDS ([wave][group g = 4 chunk + r][lane]); wave w
-    // adds groups w, w + 16, ... over the waves in wave order and stores them
-    if constexpr (C > 1) __syncthreads();  // the partials reuse the wave buffers
+    // wave partials through LDS, each wave's in a region only it writes
+    // ([group g = 4 chunk + r][lane]); wave w adds groups w, w + 16, ... over
+    // the waves in wave order and stores them
     const int li = lane & 15, q = lane >> 4;
+    // wave v's partials at red + v * kStride: a compile-time stride, so the
+    // reads below take immediate offsets from one address
     float *red = reinterpret_cast<float *>(lds + (C == 1 ? kKqMfWaves * kChunkWaveBytes : 0));
+    constexpr int kStride = (C == 1 ? 1024 : kChunkWaveBytes) / 4;
 #pragma unroll
     for (int ch = 0; ch < C; ++ch)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[((wave * C + ch) * 4 + r) * 64 + lane] = acc[ch][r];
+        for (int r = 0; r < 4; ++r) red[wave * kStride + (ch * 4 + r) * 64 + lane] = acc[ch][r];
     __syncthreads();
     const int col = n0 + li;
     for (int g = wave; g < 4 * C; g += kKqMfWaves) {
         float s = red[g * 64 + lane];
-        for (int v = 1; v < kKqMfWaves; ++v) s += red[(v * 4 * C + g) * 64 + lane];
+        for (int v = 1; v < kKqMfWaves; ++v) s += red[v * kStride + g * 64 + lane];
         const int row = 16 * (g / 4) + 4 * q + g % 4;
         if (col < n && row < m) store_through(&c[(size_t)row * n + col], s);
     }
@@ -1237,9 +1240,8 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
     const int nsb = kG > 0 ? kG : groups;
     const uint32_t kARow = (uint32_t)nsb * kQ8KBytes;
     constexpr int kH = run_copies<16, 9>();  // instructions per copy (run_copy_exact issues as many)
-    constexpr int kW = run_copies<16, 5>();
     static_assert(kIq2ChunkRunH == 16 * 9 * 16 && kIq2ChunkRunW == 16 * 5 * 16, "run sizes");
-    static_assert(kKqMfWaves * 4 * C * 64 * 4 <= iq2_chunk_lds_bytes(2), "wave partials fit the buffers");
+    static_assert(4 * C * 64 * 4 <= kIq2ChunkWaveBytes, "a wave's partials fit its buffers");
     static_assert(iq2_chunk_lds_bytes(C) <= 160 * 1024, "the LDS of one CU");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
@@ -1340,20 +1342,27 @@ __global__ __launch_bounds__(kKqMfWaves * 64) void gemv_iq2_xxs_mfma_chunk_kerne
             }
         }
     }
-    // wave partials through LDS ([wave][group g = 4 chunk + r][lane]); wave w
-    // adds groups w, w + 16, ... over the waves in wave order and stores them
-    if constexpr (C > 1) __syncthreads();  // the partials reuse the wave buffers
+    // wave partials through LDS, each wave's in a region only it writes
+    // ([group g = 4 chunk + r][lane]); wave w adds groups w, w + 16, ... over
+    // the waves in wave order and stores them
     const int li = lane & 15, q = lane >> 4;
+    // wave v's partials at red + v * kStride: a compile-time stride, so the
+    // reads below take immediate offsets from one address
     float *red = reinterpret_cast<float *>(lds + (C == 1 ? kKqMfWaves * kIq2ChunkWaveBytes : 0));
+    constexpr int kStride = (C == 1 ? 1024 : kIq2ChunkWaveBytes) / 4;
+    // from two chunks the partials go where the table copy lands, for which a
+    // wave with no super-block (nsb < 16) has not waited; the others have
+    // waited for everything
+    if constexpr (C > 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
     for (int ch = 0; ch < C; ++ch)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[((wave * C + ch) * 4 + r) * 64 + lane] = acc[ch][r];
+        for (int r = 0; r < 4; ++r) red[wave * kStride + (ch * 4 + r) * 64 + lane] = acc[ch][r];
     __syncthreads();
     const int col = n0 + li;
     for (int g = wave; g < 4 * C; g += kKqMfWaves) {
         float s = red[g * 64 + lane];
-        for (int v = 1; v < kKqMfWaves; ++v) s += red[(v * 4 * C + g) * 64 + lane];
+        for (int v = 1; v < kKqMfWaves; ++v) s += red[v * kStride + g * 64 + lane];
         const int row = 16 * (g / 4) + 4 * q + g % 4;
         if (col < n && row < m) store_through(&c[(size_t)row * n + col], s);
     }

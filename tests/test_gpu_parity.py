@@ -682,10 +682,12 @@ def test_compute_fused_kquant_gemv(hip, torch_gpu, oracle, qtype, m, n, k):
                                        (1, 96, 1024), (1, 37, 2048), (1, 50, 3072), (2, 64, 2048), (2, 37, 2048)])
 def test_gemv_tiles_small_k(hip, torch_gpu, oracle, qtype, m, n, k):
     """Below k = 4096 the one-chunk and chunked MFMA tile GEMVs run with the
-    waves past the last K group idle (q4_0 at k = 512: 14 of 16; iq2_xxs's idle
-    waves still take the table barrier), from the m measured fastest for the
-    format and k, up to m = 64 below k = 2048 and 128 from there; the other m
-    take the staged or pair kernels or the GEMM. The automatic path against the
+    waves past the last K group idle (q4_0 at k = 512: 14 of 16), from the m
+    measured fastest for the format and k, up to m = 64 below k = 2048 and 128
+    from there; the other m take the staged or pair kernels or the GEMM. An idle
+    wave stores its zero partials in its own LDS region, where the iq2_xxs
+    kernel's table copy also lands, so it waits for that copy first (without the
+    wait iq2_xxs at k = 2048, m = 64 read table bytes as partials). The automatic path against the
     oracle, on the generator's inputs and on random weight bytes against
     activations at the int8 limits."""
     torch = torch_gpu
